@@ -1,0 +1,218 @@
+"""Benchmark of the Qwen3.5-9B-shape Gated DeltaNet layer on one MI355X.
+
+    python bench.py [--steps K] [--warmup W]
+
+Headline (the `value` of the JSON line): decode throughput at batch 64 -- tokens per second through one
+9B-shape GDN layer, one step = one token for each of the 64 sequences (in_proj -> fused mixer ->
+out_proj), inputs and states resident in HBM.  To keep the 256 MB Infinity Cache from serving the
+weights, the timed steps rotate over `--copies` independent layers (own weights, own 64 state slots;
+> 1 GB working set), as consecutive layers of a model would.
+
+Also reported: prefill of one 16384-token sequence (tokens/s and bf16-MFMA roofline fraction), the
+roofline of the dominant decode kernel (the fused mixer, timed with HIP events on its stream), and the
+CPU oracle timed on a bounded sample of the same decode workload on the host cores.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "GDN-layer decode tok/s + prefill tok/s at 9B shape; % HBM / MFMA roofline"
+HBM_PEAK = 8.0e12        # B/s, MI355X HBM3E
+BF16_PEAK = 2.5e15       # FLOP/s, MI355X dense bf16 MFMA
+
+
+def decode_bytes(d, B):
+    """Algorithmic HBM bytes of one decode layer step: weights once plus per-sequence state and I/O.
+    W = bf16 projections (qkv, z, a, b, out) + bf16 conv taps; s = fp32 state read + write, fp32 conv
+    history (3 reads + 1 write per channel), bf16 x in and out."""
+    H, nk, nv, dk, dv = d["hidden"], d["num_k_heads"], d["num_v_heads"], d["head_k_dim"], d["head_v_dim"]
+    C, Vd = 2 * nk * dk + nv * dv, nv * dv
+    W = 2 * (C * H + Vd * H + 2 * nv * H + H * Vd) + 2 * C * 4
+    s = nv * dk * dv * 4 * 2 + C * 4 * 4 + 2 * H * 2
+    return W, s
+
+
+def mixer_bytes_per_seq(d):
+    """Algorithmic bytes of the fused mixer kernel per sequence and token: fp32 state read + write,
+    conv history (3 reads + 1 write, fp32), the fp32 projection row it consumes (q|k|v|z|a|b) and the
+    bf16 normalised output row it writes."""
+    nk, nv, dk, dv = d["num_k_heads"], d["num_v_heads"], d["head_k_dim"], d["head_v_dim"]
+    C, Vd = 2 * nk * dk + nv * dv, nv * dv
+    return nv * dk * dv * 4 * 2 + C * 4 * 4 + (C + Vd + 2 * nv) * 4 + Vd * 2
+
+
+def prefill_flops_per_token(d, chunk=64):
+    """Projections (in: q|k|v|z|a|b, out) plus the chunk-64 WY/UT form of the recurrence."""
+    H, nk, nv, dk, dv = d["hidden"], d["num_k_heads"], d["num_v_heads"], d["head_k_dim"], d["head_v_dim"]
+    Kd, Vd = nk * dk, nv * dv
+    C = chunk
+    proj = 2 * H * (2 * Kd + 2 * Vd + 2 * nv) + 2 * Vd * H
+    rec = nv * (2 * C * (3 * dk + 2 * dv) + 6 * dk * dv + 2 * C * C / 3)
+    return proj + rec
+
+
+def cpu_baseline(d, w_np, B, seconds, gen_seed=2):
+    """Time the CPU oracle (fp64 C restatement, OpenMP over the host cores) on decode steps of the same
+    workload until about `seconds` have passed (at least one step)."""
+    import numpy as np
+
+    import oracle
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    oracle.set_threads(threads)
+    rng = np.random.default_rng(gen_seed)
+    dm = oracle.dims(d["hidden"], d["num_k_heads"], d["num_v_heads"], d["head_k_dim"], d["head_v_dim"])
+    rec = (rng.standard_normal((B, d["num_v_heads"], d["head_k_dim"], d["head_v_dim"])) * 0.01).astype(np.float32)
+    conv = np.zeros((B, 2 * d["num_k_heads"] * d["head_k_dim"] + d["num_v_heads"] * d["head_v_dim"], 3), np.float32)
+    x = rng.standard_normal((B, 1, d["hidden"])).astype(np.float32)
+    oracle.layer_forward(dm, w_np, x, rec, conv)  # warm-up (page-in, thread pool)
+    steps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.layer_forward(dm, w_np, x, rec, conv)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or steps >= 50:
+            break
+    return {"value": B * steps / el, "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} decode steps of the 9B layer at batch {B} (fp64 oracle, {el:.1f} s)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--batch", type=int, default=64)
+    ap.add_argument("--copies", type=int, default=4, help="independent layers rotated through (defeats MALL)")
+    ap.add_argument("--prefill-len", type=int, default=16384)
+    ap.add_argument("--prefill-steps", type=int, default=3)
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the layer shards by v-head "
+              "or by sequence across GPUs only in design); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from linear_attention_op_amd import Qwen35GatedDeltaNetHIP
+    from linear_attention_op_amd import synthetic as syn
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    d = syn.SHAPES["9b"]
+    B, L = args.batch, args.copies
+    print(f"[bench] building {L} 9B-shape layers, batch {B}", file=sys.stderr, flush=True)
+
+    w0, gen = syn.make_weights(d, seed=2)
+    layers = []
+    for i in range(L):
+        if i == 0:
+            w = w0
+        else:  # further copies: same distribution, drawn on the GPU (values do not affect timing)
+            gg = torch.Generator(device=dev).manual_seed(100 + i)
+            w = {k: (torch.randn(v.shape, generator=gg, device=dev) * v.float().std()).to(v.dtype)
+                 if k.startswith("w_") or k == "conv_w" else v for k, v in w0.items()}
+        lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B, max_tokens=max(B, 64))
+        s0 = torch.randn(B, d["num_v_heads"], 128, 128, device=dev) * 0.01
+        lay.set_state(rec=s0)
+        layers.append(lay)
+    xs = [(torch.randn(B, 1, d["hidden"], device=dev)).to(torch.bfloat16) for _ in range(4)]
+    torch.cuda.synchronize()
+
+    for i in range(args.warmup):
+        layers[i % L](xs[i % 4])
+    torch.cuda.synchronize()
+    for lay in layers:
+        lay.profile(args.steps)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        layers[i % L](xs[i % 4])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    stage = {"in_proj": 0.0, "mixer": 0.0, "out_proj": 0.0, "total": 0.0}
+    calls = 0
+    for lay in layers:
+        ms, n = lay.profile_read()
+        calls += n
+        for k in stage:
+            stage[k] += ms[k]
+        lay.profile(0)
+    stage_avg_ms = {k: v / max(calls, 1) for k, v in stage.items()}
+
+    ms_per_step = elapsed * 1e3 / args.steps
+    value = B / (ms_per_step / 1e3)
+    W, s = decode_bytes(d, B)
+    step_bytes = W + B * s
+    mix_bytes = B * mixer_bytes_per_seq(d)
+    mix_s = stage_avg_ms["mixer"] / 1e3
+    roofline = {"bound": "hbm", "achieved": mix_bytes / mix_s / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                "frac": mix_bytes / mix_s / HBM_PEAK, "traffic": None, "kernel": "mixer_kernel<128,128>",
+                "bytes_per_launch": mix_bytes, "avg_launch_us": stage_avg_ms["mixer"] * 1e3}
+    layer_roof = {"bytes_per_step": step_bytes, "achieved_GBps": step_bytes / (ms_per_step / 1e3) / 1e9,
+                  "frac": step_bytes / (ms_per_step / 1e3) / HBM_PEAK,
+                  "event_step_us": stage_avg_ms["total"] * 1e3,
+                  "event_frac": step_bytes / (stage_avg_ms["total"] / 1e3) / HBM_PEAK,
+                  "stage_us": {k: v * 1e3 for k, v in stage_avg_ms.items()}}
+    print(f"[bench] decode B={B}: {ms_per_step * 1e3:.1f} us/step wall, stages (us) "
+          f"{ {k: round(v * 1e3, 1) for k, v in stage_avg_ms.items()} }", file=sys.stderr, flush=True)
+    for lay in layers[1:]:
+        lay.close()
+    del layers[1:]
+
+    prefill = None
+    if not args.no_prefill:
+        T = args.prefill_len
+        lay = Qwen35GatedDeltaNetHIP(w0, dims=d, batch=1, max_tokens=T)
+        x = torch.randn(1, T, d["hidden"], device=dev).to(torch.bfloat16)
+        lay.reset_state()
+        lay(x)
+        torch.cuda.synchronize()
+        lay.profile(args.prefill_steps)
+        t0 = time.perf_counter()
+        for _ in range(args.prefill_steps):
+            lay.reset_state()
+            lay(x)
+        torch.cuda.synchronize()
+        pe = (time.perf_counter() - t0) / args.prefill_steps
+        ms, n = lay.profile_read()
+        ev = ms["total"] / max(n, 1) / 1e3
+        flops = prefill_flops_per_token(d) * T
+        prefill = {"tokens": T, "tok_per_s": T / ev, "ms": ev * 1e3, "wall_ms": pe * 1e3,
+                   "stage_ms": {k: v / max(n, 1) for k, v in ms.items()},
+                   "roofline": {"bound": "mfma", "achieved": flops / ev / 1e12, "peak": BF16_PEAK / 1e12,
+                                "unit": "TFLOP/s", "frac": flops / ev / BF16_PEAK, "flops": flops}}
+        print(f"[bench] prefill T={T}: {ev * 1e3:.2f} ms, {T / ev:.0f} tok/s", file=sys.stderr, flush=True)
+        lay.close()
+
+    cpu = None
+    if not args.no_cpu:
+        print("[bench] timing the CPU oracle", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(d, syn.to_numpy(w0), B, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC, "value": value, "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": f"9B-shape GDN layer decode, batch {B}, one token per sequence per step, "
+                               f"rotating over {L} layer copies",
+                   "hidden": d["hidden"], "num_k_heads": d["num_k_heads"], "num_v_heads": d["num_v_heads"],
+                   "head_dim": 128, "batch": B, "state_dtype": "fp32", "weights": "bf16 N(0,0.02) seed 2"},
+        "roofline": roofline, "layer_roofline": layer_roof, "prefill": prefill, "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,161 @@
+/*
+ * gdn.h -- C ABI of the MI355X (gfx950) Gated DeltaNet layer library, libgdn_hip.so.
+ *
+ * One Qwen3.5 Gated DeltaNet (GDN) linear-attention layer:
+ *   x -> in_proj (q|k|v|z|a|b) -> causal conv1d (4 taps) + SiLU -> l2norm(q, k), g, beta
+ *     -> gated delta rule (fp32 state per sequence and v-head) -> gated RMSNorm(o) * silu(z) -> out_proj
+ *
+ * Each entry point replaces one interface of the reference (paths relative to the reference root;
+ * "9B/" = wormhole_n150/qwen3.5_9B/).  Conventions:
+ *   - Every call returns GDN_OK (0) or a negative gdn_status; gdn_last_error() gives a message
+ *     (thread-local).  Nothing aborts.
+ *   - Tensors are device pointers, row-major, rows sequence-major (row m = b * T + t, 9B/gdn_layer.py:291).
+ *     bf16 tensors are raw 16-bit words.  Weights use the HF [out_features, in_features] layout.
+ *   - `stream` is a hipStream_t (NULL = the default stream).  Calls are asynchronous on that stream
+ *     except gdn_layer_create/destroy, which synchronise the device.
+ *   - A gdn_layer handle is not thread-safe.  Two sequences of one launch must not share a state slot.
+ */
+#ifndef GDN_H
+#define GDN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct gdn_layer gdn_layer;
+
+typedef enum gdn_status {
+    GDN_OK = 0,
+    GDN_ERR_INVALID_ARG = -1,     /* null pointer, non-positive size */
+    GDN_ERR_UNSUPPORTED = -2,     /* geometry the kernels do not implement */
+    GDN_ERR_SHAPE = -3,           /* B, T, M or slot count outside the handle's limits */
+    GDN_ERR_SLOT = -4,            /* slot id out of range */
+    GDN_ERR_HIP = -5,             /* a HIP runtime call failed */
+    GDN_ERR_OUT_OF_MEMORY = -6,   /* allocation at create time failed */
+} gdn_status;
+
+/* Layer geometry (HF Qwen3_5TextConfig fields; 9B/gdn_layer.py:58-64).  Supported: head_k_dim ==
+ * head_v_dim in {32, 64, 128}, num_v_heads % num_k_heads == 0, conv_kernel == 4, hidden % 128 == 0. */
+typedef struct gdn_dims {
+    int hidden;        /* H: 4096 (9B), 1024 (0.8B) */
+    int num_k_heads;   /* nk: 16 */
+    int num_v_heads;   /* nv: 32 (9B), 16 (0.8B) */
+    int head_k_dim;    /* dk: 128 */
+    int head_v_dim;    /* dv: 128 */
+    int conv_kernel;   /* 4 */
+    float rms_norm_eps;/* 1e-6 */
+} gdn_dims;
+
+/* Weights of one layer in HF layouts (9B/README.md:44-52).  Pointers may be device or host memory;
+ * gdn_layer_create copies them into the handle's own device layout. */
+typedef struct gdn_weights {
+    const void* in_proj_qkv;   /* bf16 [2*nk*dk + nv*dv, H] */
+    const void* in_proj_z;     /* bf16 [nv*dv, H] */
+    const void* in_proj_a;     /* bf16 [nv, H] */
+    const void* in_proj_b;     /* bf16 [nv, H] */
+    const float* conv1d;       /* fp32 [2*nk*dk + nv*dv, 4]  (conv1d.weight[:, 0, :]) */
+    const float* A_log;        /* fp32 [nv] */
+    const float* dt_bias;      /* fp32 [nv] */
+    const float* norm_weight;  /* fp32 [dv] */
+    const void* out_proj;      /* bf16 [H, nv*dv] */
+} gdn_weights;
+
+/* ---- layer handle: mirrors Qwen35GatedDeltaNetTT (9B/gdn_layer.py:54-292) ------------------------ */
+
+/* 9B/gdn_layer.py:55-78 (__init__), 90-127 (_prepare_weights), 137-151 (reset_state).
+ * Copies the weights into the fused in_proj layout [q|k|v|z|a|b, H], allocates `max_slots` zeroed
+ * state slots (recurrent [nv, dk, dv] fp32 + conv ring) and a workspace for launches of up to
+ * `max_tokens` rows (longer launches are split, 9B/gdn_layer.py:282-292). */
+int gdn_layer_create(const gdn_dims* dims, const gdn_weights* weights, int max_slots, int max_tokens,
+                     gdn_layer** out);
+
+int gdn_layer_destroy(gdn_layer* layer);
+
+/* 9B/gdn_layer.py:282-292 (__call__) and 244-280 (_forward_rows).
+ * x: bf16 [B*T, H]; out: bf16 [B*T, H].  slot_ids: device int32 [B] (state slot of sequence b), or NULL
+ * for slots 0..B-1.  Continues every sequence from its slot's conv and recurrent state. */
+int gdn_layer_forward(gdn_layer* layer, const void* x, int B, int T, const int* slot_ids, void* out,
+                      void* stream);
+
+/* 9B/gdn_layer.py:137-151 (reset_state): zero the states of `n` slots (device ids, NULL = the first n). */
+int gdn_state_reset(gdn_layer* layer, const int* slot_ids, int n, void* stream);
+
+/* 9B/gdn_layer.py:153-157 (get_recurrent_state): copy the states of n slots out.
+ * rec: fp32 [n, nv, dk, dv]; conv: fp32 [n, conv_dim, 3], time order (entry 2 = newest); either may be NULL. */
+int gdn_state_get(gdn_layer* layer, const int* slot_ids, int n, float* rec, float* conv, void* stream);
+
+/* 9B/gated_delta_l1.py:156-173 (reset_state(initial_state)): seed the states of n slots.  rec and conv as
+ * in gdn_state_get; a NULL rec leaves the recurrent state, a NULL conv zeroes the conv history. */
+int gdn_state_set(gdn_layer* layer, const int* slot_ids, int n, const float* rec, const float* conv, void* stream);
+
+/* Device addresses of the resident state buffers (for address-stability checks,
+ * 9B/test_gated_delta_l1.py:81-92).  rec: [max_slots, nv, dk, dv] fp32. */
+int gdn_layer_state_buffers(gdn_layer* layer, void** rec, void** conv, void** ring_pos);
+
+/* Stage timing with HIP events recorded on the launch stream at the stage boundaries of every
+ * gdn_layer_forward call (no counterpart in the reference, whose benches read the tt-metal device
+ * profiler, wormhole_n150/qwen3.5_0.8B/bench_decode.py:35-37).  gdn_layer_profile(layer, n) starts
+ * recording for up to n calls (n = 0 stops); gdn_layer_profile_read synchronises on the last event and
+ * writes the summed milliseconds per stage: ms[0] in_proj, ms[1] mixer (conv .. gated RMSNorm),
+ * ms[2] out_proj, ms[3] whole call; *calls = number of calls recorded. */
+int gdn_layer_profile(gdn_layer* layer, int max_calls);
+int gdn_layer_profile_read(gdn_layer* layer, double* ms, int* calls);
+
+/* Width of the fused projection row, conv_dim + nv*dv + 2*nv (q | k | v | z | a | b). */
+int gdn_layer_proj_width(const gdn_layer* layer);
+
+/* ---- per-op entries: the five stages of the layer, on caller-owned device buffers --------------- */
+
+/* in_proj: 9B/gdn_layer.py:255-258 (q|k|v|z) + 259 (a|b) as one projection.
+ * x bf16 [M, H] -> P fp32 [M, gdn_layer_proj_width()] = x [W_qkv; W_z; W_a; W_b]^T. */
+int gdn_in_proj(gdn_layer* layer, const void* x, int M, float* P, void* stream);
+
+/* Front end: 9B/kernels/layer_compute.cpp C1-C4 (74-222) with layer_reader.cpp:103-124,184-197.
+ * Causal conv1d + SiLU of the q|k|v part of P (continuing each slot's conv history, which it advances),
+ * l2norm, g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b).
+ * qn, kn: fp32 [M, nk, dk] (qn scaled by dk^-0.5); v: fp32 [M, nv, dv]; g, beta: fp32 [M, nv]. */
+int gdn_conv_front(gdn_layer* layer, const float* P, int B, int T, const int* slot_ids, float* qn, float* kn,
+                   float* v, float* g, float* beta, void* stream);
+
+/* Recurrence: 9B/kernels/layer_compute.cpp C5 (224-285); 9B/reference.py:28-34.
+ * On normalised inputs from gdn_conv_front, continuing each slot's recurrent state.  o: fp32 [M, nv, dv]. */
+int gdn_delta_rule(gdn_layer* layer, const float* qn, const float* kn, const float* v, const float* g,
+                   const float* beta, int B, int T, const int* slot_ids, float* o, void* stream);
+
+/* Gated RMSNorm: 9B/kernels/layer_compute.cpp C6 (287-395); HF Qwen3_5RMSNormGated.
+ * o fp32 [M, nv*dv], z fp32 rows of stride z_stride (the z block of P) -> y bf16 [M, nv*dv]. */
+int gdn_gated_rmsnorm(gdn_layer* layer, const float* o, const float* z, int z_stride, int M, void* y,
+                      void* stream);
+
+/* out_proj: 9B/gdn_layer.py:272-276.  y bf16 [M, nv*dv] -> out bf16 [M, H]. */
+int gdn_out_proj(gdn_layer* layer, const void* y, int M, void* out, void* stream);
+
+/* ---- standalone ops ------------------------------------------------------------------------------ */
+
+/* Recurrence-only op: mirrors GatedDeltaRuleL1.__call__ (9B/gated_delta_l1.py:260-272, packing 90-122)
+ * and the CPU oracle recurrent_gated_delta_rule (9B/reference.py:11-35).
+ * q, k: fp32 [B, T, Hk, dk]; v: fp32 [B, T, Hv, dv]; g (log decay), beta: fp32 [B, T, Hv];
+ * state: fp32 [B, Hv, dk, dv], read as the initial state and overwritten with the final state;
+ * o: fp32 [B, T, Hv, dv].  use_qk_l2norm: l2-normalise q and k (eps 1e-6); scale <= 0 means dk^-0.5. */
+int gdn_delta_rule_fla(const float* q, const float* k, const float* v, const float* g, const float* beta, int B,
+                       int T, int Hk, int Hv, int dk, int dv, float* state, int use_qk_l2norm, float scale,
+                       float* o, void* stream);
+
+/* Projection y[M, N] = x[M, K] . w[N, K]^T, bf16 inputs, fp32 accumulation (the ttnn.linear call sites
+ * 9B/gdn_layer.py:255, 259, 272).  out_fp32 != 0: y is fp32, else bf16.  K % 128 == 0. */
+int gdn_linear_bf16(const void* x, const void* w, int M, int N, int K, void* y, int out_fp32, void* stream);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* gdn_last_error(void);
+
+/* Library version, major * 10000 + minor * 100 + patch. */
+int gdn_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_H */

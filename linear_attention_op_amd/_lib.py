@@ -1,0 +1,105 @@
+"""ctypes binding of libgdn_hip.so (the C ABI declared in include/gdn.h).
+
+Loading fails loudly when the library is not built: there is no CPU fallback for any op.
+"""
+
+import ctypes
+import os
+import re
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libgdn_hip.so")
+HEADER = os.path.join(os.path.dirname(HERE), "include", "gdn.h")
+
+GDN_OK = 0
+GDN_ERR_INVALID_ARG = -1
+GDN_ERR_UNSUPPORTED = -2
+GDN_ERR_SHAPE = -3
+GDN_ERR_SLOT = -4
+GDN_ERR_HIP = -5
+GDN_ERR_OUT_OF_MEMORY = -6
+
+
+class GdnError(RuntimeError):
+    """A gdn_* call returned a negative status."""
+
+    def __init__(self, code, message):
+        super().__init__(f"gdn error {code}: {message}")
+        self.code = code
+
+
+class GdnValueError(GdnError, ValueError):
+    """Bad argument, shape, slot or unsupported geometry (the reference raises assert / ValueError)."""
+
+
+class GdnDims(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int), ("num_k_heads", ctypes.c_int), ("num_v_heads", ctypes.c_int),
+                ("head_k_dim", ctypes.c_int), ("head_v_dim", ctypes.c_int), ("conv_kernel", ctypes.c_int),
+                ("rms_norm_eps", ctypes.c_float)]
+
+
+class GdnWeights(ctypes.Structure):
+    _fields_ = [("in_proj_qkv", ctypes.c_void_p), ("in_proj_z", ctypes.c_void_p), ("in_proj_a", ctypes.c_void_p),
+                ("in_proj_b", ctypes.c_void_p), ("conv1d", ctypes.c_void_p), ("A_log", ctypes.c_void_p),
+                ("dt_bias", ctypes.c_void_p), ("norm_weight", ctypes.c_void_p), ("out_proj", ctypes.c_void_p)]
+
+
+_V = ctypes.c_void_p
+_I = ctypes.c_int
+_F = ctypes.c_float
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "gdn_layer_create": (_I, [ctypes.POINTER(GdnDims), ctypes.POINTER(GdnWeights), _I, _I, ctypes.POINTER(_V)]),
+    "gdn_layer_destroy": (_I, [_V]),
+    "gdn_layer_forward": (_I, [_V, _V, _I, _I, _V, _V, _V]),
+    "gdn_state_reset": (_I, [_V, _V, _I, _V]),
+    "gdn_state_get": (_I, [_V, _V, _I, _V, _V, _V]),
+    "gdn_state_set": (_I, [_V, _V, _I, _V, _V, _V]),
+    "gdn_layer_state_buffers": (_I, [_V, ctypes.POINTER(_V), ctypes.POINTER(_V), ctypes.POINTER(_V)]),
+    "gdn_layer_proj_width": (_I, [_V]),
+    "gdn_layer_profile": (_I, [_V, _I]),
+    "gdn_layer_profile_read": (_I, [_V, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),
+    "gdn_in_proj": (_I, [_V, _V, _I, _V, _V]),
+    "gdn_conv_front": (_I, [_V, _V, _I, _I, _V, _V, _V, _V, _V, _V, _V]),
+    "gdn_delta_rule": (_I, [_V, _V, _V, _V, _V, _V, _I, _I, _V, _V, _V]),
+    "gdn_gated_rmsnorm": (_I, [_V, _V, _V, _I, _I, _V, _V]),
+    "gdn_out_proj": (_I, [_V, _V, _I, _V, _V]),
+    "gdn_delta_rule_fla": (_I, [_V, _V, _V, _V, _V, _I, _I, _I, _I, _I, _I, _V, _I, _F, _V, _V]),
+    "gdn_linear_bf16": (_I, [_V, _V, _I, _I, _I, _V, _I, _V]),
+    "gdn_last_error": (ctypes.c_char_p, []),
+    "gdn_version": (_I, []),
+}
+
+_lib = None
+
+
+def header_symbols():
+    """Function names declared in include/gdn.h."""
+    with open(HEADER) as f:
+        text = f.read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(gdn_\w+)\s*\(", text, re.M)))
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is not built; run `python -m linear_attention_op_amd.build` "
+                               "(the Gated DeltaNet ops have no CPU fallback)")
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc):
+    if rc != GDN_OK:
+        msg = lib().gdn_last_error().decode(errors="replace")
+        cls = GdnValueError if rc in (GDN_ERR_INVALID_ARG, GDN_ERR_UNSUPPORTED, GDN_ERR_SHAPE, GDN_ERR_SLOT) \
+            else GdnError
+        raise cls(rc, msg)
+    return rc

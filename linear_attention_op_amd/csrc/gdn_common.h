@@ -1,0 +1,136 @@
+// Shared device helpers and internal launcher declarations for the Gated DeltaNet HIP library.
+// gfx950 (CDNA4) only: 64-wide wavefronts, bf16 MFMA, 160 KB LDS per CU.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gdn {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint16_t u16;
+typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+
+constexpr int WAVE = 64;
+
+__device__ __forceinline__ float bf2f(u16 b) { return __uint_as_float((uint32_t)b << 16); }
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ u16 f2bf(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (u16)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (u16)(u >> 16);
+}
+
+__device__ __forceinline__ float warp_sum(float x) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) x += __shfl_xor(x, off, WAVE);
+    return x;
+}
+
+// Sum over lanes that share (lane % width); width is a power of two <= 64.
+template <int WIDTH>
+__device__ __forceinline__ float lane_group_sum(float x) {
+#pragma unroll
+    for (int off = WIDTH; off < WAVE; off <<= 1) x += __shfl_xor(x, off, WAVE);
+    return x;
+}
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float siluf_(float x) { return x / (1.0f + __expf(-x)); }
+// torch.nn.functional.softplus with beta = 1, threshold = 20
+__device__ __forceinline__ float softplusf_(float x) { return x > 20.0f ? x : log1pf(__expf(x)); }
+
+}  // namespace gdn
+
+// ------------------------------------------------------------------------------------------------
+// Internal launchers (each returns a hipError_t of the launch).  Pointers are device pointers.
+// ------------------------------------------------------------------------------------------------
+namespace gdn {
+
+enum OutKind { OUT_F32 = 0, OUT_BF16 = 1 };
+
+// y[M, N] = x[M, K] . w[N, K]^T ; bf16 inputs, fp32 accumulation; K % 128 == 0.
+hipError_t launch_linear(const void* x, const void* w, int M, int N, int K, void* y, int out_kind,
+                         hipStream_t stream);
+
+struct MixerArgs {
+    const float* P;         // [M, NP] fused projection rows (q | k | v | z | a | b)
+    int NP;                 // row stride of P
+    int B, T;               // launch = B sequences x T tokens, rows m = b * T + t
+    const int* slot_ids;    // [B] device, or nullptr for identity
+    int nk, nv;             // heads
+    const float4* conv_w;   // [conv_dim] taps (w0, w1, w2, w3) per channel
+    const float* neg_A;     // [nv]  -exp(A_log)
+    const float* dt_bias;   // [nv]
+    const float* norm_w;    // [dv]
+    float eps;              // RMSNorm eps
+    float* rec_state;       // [slots, nv, dk, dv]
+    float* conv_state;      // [slots, nv, 3, 2dk + dv] ring, per v-head copy
+    int* ring_pos;          // [slots, nv]
+    u16* y;                 // [M, nv * dv] bf16 gated RMSNorm output
+    float* o_tap;           // optional [M, nv * dv] recurrence output (nullptr: not written)
+};
+hipError_t launch_mixer(const MixerArgs& a, int dk, int dv, hipStream_t stream);
+
+struct FrontArgs {
+    const float* P;
+    int NP;
+    int B, T;
+    const int* slot_ids;
+    int nk, nv, dk, dv;
+    const float4* conv_w;
+    const float* neg_A;
+    const float* dt_bias;
+    const float* conv_state;  // ring (read only here)
+    const int* ring_pos;
+    float* qn;                // [M, nk, dk]  l2norm(q) * dk^-0.5
+    float* kn;                // [M, nk, dk]  l2norm(k)
+    float* v;                 // [M, nv, dv]
+    float* g;                 // [M, nv]
+    float* beta;              // [M, nv]
+};
+hipError_t launch_conv_front(const FrontArgs& a, hipStream_t stream);
+// Write the last min(T, 3) pre-conv inputs of each sequence into its ring and advance the ring.
+hipError_t launch_conv_commit(const float* P, int NP, int B, int T, const int* slot_ids, int nk, int nv, int dk,
+                              int dv, float* conv_state, int* ring_pos, hipStream_t stream);
+
+// Recurrence over T tokens for B sequences from pre-normalised q/k (qn already scaled).
+struct DeltaArgs {
+    const float* q;        // [B*T, Hk, dk]
+    const float* k;        // [B*T, Hk, dk]
+    const float* v;        // [B*T, Hv, dv]
+    const float* g;        // [B*T, Hv]
+    const float* beta;     // [B*T, Hv]
+    int B, T, Hk, Hv;
+    const int* slot_ids;   // state slot of sequence b (nullptr: b)
+    float* state;          // [slots, Hv, dk, dv]
+    float* o;              // [B*T, Hv, dv]
+    int normalize;         // 1: apply l2norm to q/k in the kernel
+    float scale;           // q scale applied in the kernel (1 when q is pre-scaled)
+};
+hipError_t launch_delta_seq(const DeltaArgs& a, int dk, int dv, hipStream_t stream);
+hipError_t launch_delta_chunked(const DeltaArgs& a, int dk, int dv, void* workspace, size_t ws_bytes,
+                                hipStream_t stream);
+size_t delta_chunked_workspace(int B, int T, int Hv, int dk, int dv);
+
+// y = o * rsqrt(mean(o^2) + eps) * w * silu(z), per head of dv; y bf16.
+hipError_t launch_gated_rmsnorm(const float* o, int M, int nv, int dv, const float* z, int z_stride,
+                                const float* w, float eps, u16* y, hipStream_t stream);
+
+// State import / export (time-ordered conv history [n, conv_dim, 3]).
+hipError_t launch_state_export(const float* rec_state, const float* conv_state, const int* ring_pos,
+                               const int* slots, int n, int nk, int nv, int dk, int dv, float* rec_out,
+                               float* conv_out, hipStream_t stream);
+hipError_t launch_state_import(float* rec_state, float* conv_state, int* ring_pos, const int* slots, int n, int nk,
+                               int nv, int dk, int dv, const float* rec_in, const float* conv_in,
+                               hipStream_t stream);
+hipError_t launch_state_zero(float* rec_state, float* conv_state, int* ring_pos, const int* slots, int n, int nv,
+                             int dk, int dv, int ch, hipStream_t stream);
+
+}  // namespace gdn

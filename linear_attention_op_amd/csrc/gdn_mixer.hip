@@ -1,0 +1,376 @@
+// The Gated DeltaNet mixer between the two projections.
+//
+// mixer_kernel: one workgroup per (sequence, v-head) runs, for each token of the launch, the whole
+// middle of the layer -- causal conv1d (4 taps) + SiLU on the head's 2*dk + dv channels, q/k L2 norm,
+// the gating scalars, the delta-rule update of the fp32 dk x dv state and the gated RMSNorm -- with the
+// state held in VGPRs from the first token to the last.  The state is read from HBM once and written
+// once per launch; nothing else of size dk*dv moves.  This is the decode path (and short prefills).
+// It restates, per token, wormhole_n150/qwen3.5_9B/kernels/layer_compute.cpp C1-C6 (74-395) with
+// layer_reader.cpp:103-124,184-197 for the conv history; HF:432-543 for the layer math.
+//
+// conv history: each (slot, v-head) owns a 3-entry ring of its 2*dk + dv pre-conv channels (the q/k
+// channels of its k-head are kept per v-head, so no two workgroups share a ring).  Logical entry j
+// (0 = oldest) lives at physical (pos + j) % 3; after T tokens, pos' = (pos + T) % 3 and only the last
+// min(T, 3) inputs are written, which is the reference's roll (layer_reader.cpp:184-197).
+//
+// conv_front_kernel / conv_commit_kernel / gated_rmsnorm_kernel: the same front end and norm split into
+// token-parallel kernels for long prefills, where the recurrence runs in the chunked form.
+#include "gdn_common.h"
+#include "gdn_delta_core.h"
+
+namespace gdn {
+
+// Map of a head-local conv channel c (q: [0, dk), k: [dk, 2dk), v: [2dk, 2dk + dv)) to its column in
+// the fused projection row (q | k | v | z | a | b).
+__device__ __forceinline__ int conv_col(int c, int kh, int h, int dk, int dv, int Kd) {
+    return c < dk ? kh * dk + c : (c < 2 * dk ? Kd + kh * dk + (c - dk) : 2 * Kd + h * dv + (c - 2 * dk));
+}
+
+template <int DK, int DV>
+__global__ __launch_bounds__(256) void mixer_kernel(MixerArgs a) {
+    constexpr int CH = 2 * DK + DV;
+    constexpr int CPT = (CH + 255) / 256;
+    using Tile = DeltaTile<DK, DV>;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int nv = a.nv, ratio = a.nv / a.nk, kh = h / ratio;
+    const int Kd = a.nk * DK, Vd = nv * DV, CD = 2 * Kd + Vd;
+    const int slot = a.slot_ids ? a.slot_ids[b] : b;
+    const int T = a.T;
+
+    __shared__ float sq[DK], sk[DK], sv[DV];
+    __shared__ float red[4][2][DV];
+    __shared__ float scal[8];
+
+    float* S = a.rec_state + ((size_t)slot * nv + h) * DK * DV;
+    Tile st;
+    st.init(tid);
+    st.load(S);
+
+    // conv channels: taps and the 3-entry history in registers (hx[c][0] oldest)
+    float* ring = a.conv_state + ((size_t)slot * nv + h) * 3 * CH;
+    const int pos = a.ring_pos[slot * nv + h];
+    float hx[CPT][3];
+    float4 tap[CPT];
+    int pcol[CPT];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int ch = tid + 256 * c;
+        pcol[c] = 0;
+        if (ch < CH) {
+            pcol[c] = conv_col(ch, kh, h, DK, DV, Kd);
+            tap[c] = a.conv_w[pcol[c]];
+#pragma unroll
+            for (int j = 0; j < 3; ++j) hx[c][j] = ring[((pos + j) % 3) * CH + ch];
+        }
+    }
+    const float negA = a.neg_A[h], dtb = a.dt_bias[h];
+    float4 nw = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (tid < Tile::CG) nw = *reinterpret_cast<const float4*>(a.norm_w + 4 * tid);
+    const float qscale = rsqrtf((float)DK);
+
+    for (int t = 0; t < T; ++t) {
+        const size_t m = (size_t)b * T + t;
+        const float* Prow = a.P + m * a.NP;
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            const int ch = tid + 256 * c;
+            if (ch < CH) {
+                const float xin = Prow[pcol[c]];
+                const float acc = tap[c].x * hx[c][0] + tap[c].y * hx[c][1] + tap[c].z * hx[c][2] + tap[c].w * xin;
+                hx[c][0] = hx[c][1];
+                hx[c][1] = hx[c][2];
+                hx[c][2] = xin;
+                const float out = siluf_(acc);
+                if (ch < DK)
+                    sq[ch] = out;
+                else if (ch < 2 * DK)
+                    sk[ch - DK] = out;
+                else
+                    sv[ch - 2 * DK] = out;
+            }
+        }
+        __syncthreads();
+        qk_sums<DK>(sq, sk, scal, lane, wave);
+        if (wave == 3 && lane == 0) {
+            const float g = negA * softplusf_(Prow[CD + Vd + h] + dtb);
+            scal[3] = __expf(g);
+            scal[4] = sigmoidf_(Prow[CD + Vd + nv + h]);
+        }
+        __syncthreads();
+        const float rq = rsqrtf(scal[0] + 1e-6f) * qscale;
+        const float rk = rsqrtf(scal[1] + 1e-6f);
+        const float4 o = st.step(sq, sk, sv, red, rq, rk, scal[2] * rq * rk, scal[3], scal[4], lane, wave);
+
+        // gated RMSNorm of this head's o on wave 0 (its lanes < CG hold all dv columns)
+        if (wave == 0) {
+            float ss = lane < Tile::CG ? o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w : 0.f;
+            ss = warp_sum(ss);
+            if (lane < Tile::CG) {
+                const float rstd = rsqrtf(ss / (float)DV + a.eps);
+                const float4 z = *reinterpret_cast<const float4*>(Prow + CD + h * DV + 4 * lane);
+                ushort4 yv;
+                yv.x = f2bf(o.x * rstd * nw.x * siluf_(z.x));
+                yv.y = f2bf(o.y * rstd * nw.y * siluf_(z.y));
+                yv.z = f2bf(o.z * rstd * nw.z * siluf_(z.z));
+                yv.w = f2bf(o.w * rstd * nw.w * siluf_(z.w));
+                *reinterpret_cast<ushort4*>(a.y + m * Vd + h * DV + 4 * lane) = yv;
+                if (a.o_tap) *reinterpret_cast<float4*>(a.o_tap + m * Vd + h * DV + 4 * lane) = o;
+            }
+        }
+        __syncthreads();
+    }
+
+    st.store(S);
+    const int npos = (pos + T) % 3;
+    const int first = T >= 3 ? 0 : 3 - T;  // older entries are the old history, already in place
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) {
+        const int ch = tid + 256 * c;
+        if (ch < CH)
+            for (int j = first; j < 3; ++j) ring[((npos + j) % 3) * CH + ch] = hx[c][j];
+    }
+    if (tid == 0) a.ring_pos[slot * nv + h] = npos;
+}
+
+hipError_t launch_mixer(const MixerArgs& a, int dk, int dv, hipStream_t stream) {
+    const dim3 grid(a.nv, a.B);
+    if (dk == 128 && dv == 128)
+        hipLaunchKernelGGL((mixer_kernel<128, 128>), grid, dim3(256), 0, stream, a);
+    else if (dk == 64 && dv == 64)
+        hipLaunchKernelGGL((mixer_kernel<64, 64>), grid, dim3(256), 0, stream, a);
+    else if (dk == 32 && dv == 32)
+        hipLaunchKernelGGL((mixer_kernel<32, 32>), grid, dim3(256), 0, stream, a);
+    else
+        return hipErrorInvalidValue;
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------------
+// Long-T front end: one workgroup per token row.
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void conv_front_kernel(FrontArgs a) {
+    extern __shared__ float qkbuf[];  // [2 * Kd]: post-conv q | k of this token
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m = blockIdx.x;
+    const int T = a.T;
+    const int b = m / T, t = m - b * T;
+    const int slot = a.slot_ids ? a.slot_ids[b] : b;
+    const int nk = a.nk, nv = a.nv, dk = a.dk, dv = a.dv;
+    const int ratio = nv / nk;
+    const int Kd = nk * dk, Vd = nv * dv, CD = 2 * Kd + Vd, CH = 2 * dk + dv;
+    const float* Prow = a.P + (size_t)m * a.NP;
+
+    for (int col = tid; col < CD; col += 256) {
+        // owner ring of this column: q/k of k-head kh live in the ring of v-head kh * ratio
+        int hcopy, local;
+        if (col < Kd) {
+            const int kh = col / dk;
+            hcopy = kh * ratio, local = col - kh * dk;
+        } else if (col < 2 * Kd) {
+            const int kh = (col - Kd) / dk;
+            hcopy = kh * ratio, local = dk + (col - Kd - kh * dk);
+        } else {
+            const int hh = (col - 2 * Kd) / dv;
+            hcopy = hh, local = 2 * dk + (col - 2 * Kd - hh * dv);
+        }
+        const float4 w = a.conv_w[col];
+        float xs[3];
+#pragma unroll
+        for (int s = 3; s >= 1; --s) {
+            float xv;
+            if (t >= s) {
+                xv = (Prow - (size_t)s * a.NP)[col];
+            } else {
+                const int pos = a.ring_pos[slot * nv + hcopy];
+                const float* ring = a.conv_state + ((size_t)slot * nv + hcopy) * 3 * CH;
+                xv = ring[((pos + 3 + t - s) % 3) * CH + local];  // logical entry 3 + t - s
+            }
+            xs[3 - s] = xv;
+        }
+        const float acc = w.x * xs[0] + w.y * xs[1] + w.z * xs[2] + w.w * Prow[col];
+        const float out = siluf_(acc);
+        if (col < 2 * Kd)
+            qkbuf[col] = out;
+        else
+            a.v[(size_t)m * Vd + (col - 2 * Kd)] = out;
+    }
+    __syncthreads();
+    const float qscale = rsqrtf((float)dk);
+    for (int task = wave; task < 2 * nk; task += 4) {
+        const float* src = qkbuf + task * dk;  // task < nk: q of head task; else k of head task - nk
+        float ss = 0.f;
+        for (int i = lane; i < dk; i += 64) ss += src[i] * src[i];
+        ss = warp_sum(ss);
+        const bool isq = task < nk;
+        const float r = rsqrtf(ss + 1e-6f) * (isq ? qscale : 1.f);
+        float* dst = (isq ? a.qn + (size_t)m * Kd + task * dk : a.kn + (size_t)m * Kd + (task - nk) * dk);
+        for (int i = lane; i < dk; i += 64) dst[i] = src[i] * r;
+    }
+    for (int hh = tid; hh < nv; hh += 256) {
+        const float av = Prow[CD + Vd + hh], bv = Prow[CD + Vd + nv + hh];
+        a.g[(size_t)m * nv + hh] = a.neg_A[hh] * softplusf_(av + a.dt_bias[hh]);
+        a.beta[(size_t)m * nv + hh] = sigmoidf_(bv);
+    }
+}
+
+hipError_t launch_conv_front(const FrontArgs& a, hipStream_t stream) {
+    const int M = a.B * a.T;
+    if (M <= 0) return hipSuccess;
+    const size_t lds = sizeof(float) * 2 * a.nk * a.dk;
+    hipLaunchKernelGGL(conv_front_kernel, dim3(M), dim3(256), lds, stream, a);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(256) void conv_commit_kernel(const float* __restrict__ P, int NP, int T,
+                                                          const int* __restrict__ slot_ids, int nk, int nv, int dk,
+                                                          int dv, float* __restrict__ conv_state,
+                                                          int* __restrict__ ring_pos) {
+    const int h = blockIdx.x, b = blockIdx.y;
+    const int slot = slot_ids ? slot_ids[b] : b;
+    const int kh = h / (nv / nk), Kd = nk * dk, CH = 2 * dk + dv;
+    const int pos = ring_pos[slot * nv + h];
+    float* ring = conv_state + ((size_t)slot * nv + h) * 3 * CH;
+    for (int j = 0; j < 3; ++j) {
+        const int tj = T - 3 + j;
+        if (tj < 0) continue;  // older entries stay where they are
+        const float* Prow = P + ((size_t)b * T + tj) * NP;
+        float* dst = ring + ((pos + T + j) % 3) * CH;
+        for (int c = threadIdx.x; c < CH; c += 256) dst[c] = Prow[conv_col(c, kh, h, dk, dv, Kd)];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) ring_pos[slot * nv + h] = (pos + T) % 3;
+}
+
+hipError_t launch_conv_commit(const float* P, int NP, int B, int T, const int* slot_ids, int nk, int nv, int dk,
+                              int dv, float* conv_state, int* ring_pos, hipStream_t stream) {
+    hipLaunchKernelGGL(conv_commit_kernel, dim3(nv, B), dim3(256), 0, stream, P, NP, T, slot_ids, nk, nv, dk, dv,
+                       conv_state, ring_pos);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------------
+// Gated RMSNorm (HF:167-184; layer_compute.cpp C6 287-395), one workgroup per token row.
+// ------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const float* __restrict__ o, int nv, int dv,
+                                                            const float* __restrict__ z, int z_stride,
+                                                            const float* __restrict__ w, float eps,
+                                                            u16* __restrict__ y) {
+    const int m = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int Vd = nv * dv;
+    const float* orow = o + (size_t)m * Vd;
+    const float* zrow = z + (size_t)m * z_stride;
+    for (int h = wave; h < nv; h += 4) {
+        float ss = 0.f;
+        for (int i = lane; i < dv; i += 64) ss += orow[h * dv + i] * orow[h * dv + i];
+        ss = warp_sum(ss);
+        const float rstd = rsqrtf(ss / (float)dv + eps);
+        for (int i = lane; i < dv; i += 64)
+            y[(size_t)m * Vd + h * dv + i] = f2bf(orow[h * dv + i] * rstd * w[i] * siluf_(zrow[h * dv + i]));
+    }
+}
+
+hipError_t launch_gated_rmsnorm(const float* o, int M, int nv, int dv, const float* z, int z_stride,
+                                const float* w, float eps, u16* y, hipStream_t stream) {
+    if (M <= 0) return hipSuccess;
+    hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3(M), dim3(256), 0, stream, o, nv, dv, z, z_stride, w, eps, y);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------------
+// State import / export / zero.  Export gives the conv history in time order [n, conv_dim, 3]
+// (q/k channels from the ring of the first v-head of each k-head group).
+// ------------------------------------------------------------------------------------------------
+__global__ void state_export_kernel(const float* __restrict__ rec, const float* __restrict__ conv,
+                                    const int* __restrict__ ring_pos, const int* __restrict__ slots, int nk, int nv,
+                                    int dk, int dv, float* __restrict__ rec_out, float* __restrict__ conv_out) {
+    const int i = blockIdx.y;
+    const int slot = slots ? slots[i] : i;
+    const size_t rec_n = (size_t)nv * dk * dv;
+    if (rec_out)
+        for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < rec_n; e += (size_t)gridDim.x * blockDim.x)
+            rec_out[(size_t)i * rec_n + e] = rec[(size_t)slot * rec_n + e];
+    if (!conv_out) return;
+    const int Kd = nk * dk, CD = 2 * Kd + nv * dv, CH = 2 * dk + dv, ratio = nv / nk;
+    for (int col = blockIdx.x * blockDim.x + threadIdx.x; col < CD; col += gridDim.x * blockDim.x) {
+        int hcopy, local;
+        if (col < Kd) {
+            hcopy = (col / dk) * ratio, local = col % dk;
+        } else if (col < 2 * Kd) {
+            hcopy = ((col - Kd) / dk) * ratio, local = dk + (col - Kd) % dk;
+        } else {
+            hcopy = (col - 2 * Kd) / dv, local = 2 * dk + (col - 2 * Kd) % dv;
+        }
+        const int pos = ring_pos[slot * nv + hcopy];
+        const float* ring = conv + ((size_t)slot * nv + hcopy) * 3 * CH;
+        for (int j = 0; j < 3; ++j) conv_out[((size_t)i * CD + col) * 3 + j] = ring[((pos + j) % 3) * CH + local];
+    }
+}
+
+__global__ void state_import_kernel(float* __restrict__ rec, float* __restrict__ conv, int* __restrict__ ring_pos,
+                                    const int* __restrict__ slots, int nk, int nv, int dk, int dv,
+                                    const float* __restrict__ rec_in, const float* __restrict__ conv_in) {
+    const int i = blockIdx.y;
+    const int slot = slots ? slots[i] : i;
+    const size_t rec_n = (size_t)nv * dk * dv;
+    if (rec_in)
+        for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < rec_n; e += (size_t)gridDim.x * blockDim.x)
+            rec[(size_t)slot * rec_n + e] = rec_in[(size_t)i * rec_n + e];
+    const int Kd = nk * dk, CD = 2 * Kd + nv * dv, CH = 2 * dk + dv, ratio = nv / nk;
+    // every v-head ring of this slot restarts at pos 0 with the time-ordered history
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < nv * CH; e += gridDim.x * blockDim.x) {
+        const int h = e / CH, c = e % CH;
+        const int kh = h / ratio;
+        const int col = conv_col(c, kh, h, dk, dv, Kd);
+        float* ring = conv + ((size_t)slot * nv + h) * 3 * CH;
+        for (int j = 0; j < 3; ++j) ring[j * CH + c] = conv_in ? conv_in[((size_t)i * CD + col) * 3 + j] : 0.f;
+    }
+    __syncthreads();
+    if (blockIdx.x == 0)
+        for (int h = threadIdx.x; h < nv; h += blockDim.x) ring_pos[slot * nv + h] = 0;
+}
+
+hipError_t launch_state_export(const float* rec_state, const float* conv_state, const int* ring_pos,
+                               const int* slots, int n, int nk, int nv, int dk, int dv, float* rec_out,
+                               float* conv_out, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(state_export_kernel, dim3(64, n), dim3(256), 0, stream, rec_state, conv_state, ring_pos,
+                       slots, nk, nv, dk, dv, rec_out, conv_out);
+    return hipGetLastError();
+}
+
+hipError_t launch_state_import(float* rec_state, float* conv_state, int* ring_pos, const int* slots, int n, int nk,
+                               int nv, int dk, int dv, const float* rec_in, const float* conv_in,
+                               hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    // ring_pos is reset by block 0 after its own ring writes; the other blocks never read it
+    hipLaunchKernelGGL(state_import_kernel, dim3(64, n), dim3(256), 0, stream, rec_state, conv_state, ring_pos,
+                       slots, nk, nv, dk, dv, rec_in, conv_in);
+    return hipGetLastError();
+}
+
+__global__ void state_zero_kernel(float* __restrict__ rec, float* __restrict__ conv, int* __restrict__ ring_pos,
+                                  const int* __restrict__ slots, int nv, int dk, int dv, int ch) {
+    const int i = blockIdx.y;
+    const int slot = slots ? slots[i] : i;
+    const size_t rec_n = (size_t)nv * dk * dv;
+    const size_t conv_n = (size_t)nv * 3 * ch;
+    for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < rec_n; e += (size_t)gridDim.x * blockDim.x)
+        rec[(size_t)slot * rec_n + e] = 0.f;
+    for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < conv_n; e += (size_t)gridDim.x * blockDim.x)
+        conv[(size_t)slot * conv_n + e] = 0.f;
+    if (blockIdx.x == 0)
+        for (int h = threadIdx.x; h < nv; h += blockDim.x) ring_pos[slot * nv + h] = 0;
+}
+
+hipError_t launch_state_zero(float* rec_state, float* conv_state, int* ring_pos, const int* slots, int n, int nv,
+                             int dk, int dv, int ch, hipStream_t stream) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(state_zero_kernel, dim3(64, n), dim3(256), 0, stream, rec_state, conv_state, ring_pos, slots,
+                       nv, dk, dv, ch);
+    return hipGetLastError();
+}
+
+}  // namespace gdn

@@ -1,0 +1,223 @@
+"""Qwen3.5 Gated DeltaNet layer on one MI355X: host-side mirror of the reference's layer object.
+
+Mirrors Qwen35GatedDeltaNetTT (wormhole_n150/qwen3.5_9B/gdn_layer.py:54-292): built from an HF
+`Qwen3_5GatedDeltaNet` (or a dict of its weights), it owns the weights, the per-sequence states and a
+launch workspace; `layer(x)` runs x [B, T, H] -> [B, T, H] and continues every sequence from its
+state; `reset_state()` / `get_recurrent_state()` as in the reference.  All compute runs in
+libgdn_hip.so through its C ABI; torch only provides device memory and the stream.
+
+Differences from the reference object, by design: state slots (a launch may name which slots its B
+sequences use), bf16 activations at the boundary, and per-op entries for the five stages.
+"""
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+_WEIGHT_KEYS = ("w_qkv", "w_z", "w_a", "w_b", "conv_w", "A_log", "dt_bias", "norm_w", "w_out")
+
+
+def weights_from_hf(layer):
+    """HF Qwen3_5GatedDeltaNet -> (dims kwargs, weights dict of CPU tensors)."""
+    dims = dict(hidden=layer.hidden_size, num_k_heads=layer.num_k_heads, num_v_heads=layer.num_v_heads,
+                head_k_dim=layer.head_k_dim, head_v_dim=layer.head_v_dim, conv_kernel=layer.conv_kernel_size,
+                rms_norm_eps=float(layer.layer_norm_epsilon))
+    w = dict(w_qkv=layer.in_proj_qkv.weight, w_z=layer.in_proj_z.weight, w_a=layer.in_proj_a.weight,
+             w_b=layer.in_proj_b.weight, conv_w=layer.conv1d.weight[:, 0, :], A_log=layer.A_log,
+             dt_bias=layer.dt_bias, norm_w=layer.norm.weight, w_out=layer.out_proj.weight)
+    return dims, {k: v.detach() for k, v in w.items()}
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _slots(slot_ids, device):
+    if slot_ids is None:
+        return None
+    s = torch.as_tensor(slot_ids, dtype=torch.int32, device=device).contiguous()
+    return s
+
+
+class Qwen35GatedDeltaNetHIP:
+    """One GDN layer.  `weights` is an HF Qwen3_5GatedDeltaNet or a dict with keys
+    w_qkv [conv_dim, H], w_z [Vd, H], w_a, w_b [nv, H], conv_w [conv_dim, 4], A_log, dt_bias [nv],
+    norm_w [dv], w_out [H, Vd] (projection weights are used as bf16, the rest as fp32)."""
+
+    def __init__(self, weights, dims=None, batch=1, max_slots=None, max_tokens=16384, device="cuda"):
+        if hasattr(weights, "in_proj_qkv"):
+            dims_hf, weights = weights_from_hf(weights)
+            dims = dims or dims_hf
+        assert dims is not None, "dims are required with a weight dict"
+        missing = [k for k in _WEIGHT_KEYS if k not in weights]
+        if missing:
+            raise ValueError(f"missing weights: {missing}")
+        self.device = torch.device(device)
+        self.dims = dict(dims)
+        self.batch = batch
+        self.max_slots = max_slots or batch
+        self.max_tokens = max_tokens
+        d = self.dims
+        self.hidden = d["hidden"]
+        self.nk, self.nv = d["num_k_heads"], d["num_v_heads"]
+        self.dk, self.dv = d["head_k_dim"], d["head_v_dim"]
+        self.conv_dim = 2 * self.nk * self.dk + self.nv * self.dv
+
+        dev = self.device
+
+        def bf16(t):
+            return torch.as_tensor(t).to(device=dev, dtype=torch.bfloat16).contiguous()
+
+        def f32(t):
+            return torch.as_tensor(t).to(device=dev, dtype=torch.float32).contiguous()
+
+        w = {k: (bf16(weights[k]) if k in ("w_qkv", "w_z", "w_a", "w_b", "w_out") else f32(weights[k]))
+             for k in _WEIGHT_KEYS}
+        cdims = _lib.GdnDims(d["hidden"], d["num_k_heads"], d["num_v_heads"], d["head_k_dim"], d["head_v_dim"],
+                             d.get("conv_kernel", 4), d.get("rms_norm_eps", 1e-6))
+        cw = _lib.GdnWeights(w["w_qkv"].data_ptr(), w["w_z"].data_ptr(), w["w_a"].data_ptr(), w["w_b"].data_ptr(),
+                             w["conv_w"].data_ptr(), w["A_log"].data_ptr(), w["dt_bias"].data_ptr(),
+                             w["norm_w"].data_ptr(), w["w_out"].data_ptr())
+        self._h = ctypes.c_void_p()
+        torch.cuda.synchronize(dev)
+        _lib.check(_lib.lib().gdn_layer_create(ctypes.byref(cdims), ctypes.byref(cw), self.max_slots,
+                                               self.max_tokens, ctypes.byref(self._h)))
+        self.proj_width = _lib.lib().gdn_layer_proj_width(self._h)
+
+    # ---- lifetime ---------------------------------------------------------------------------------
+    def close(self):
+        if getattr(self, "_h", None) and self._h.value:
+            _lib.lib().gdn_layer_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # ---- layer ------------------------------------------------------------------------------------
+    def __call__(self, hidden_states, slot_ids=None):
+        """hidden_states [B, T, H] (any float dtype, used as bf16) -> [B, T, H] bf16, continuing the states
+        of slots `slot_ids` (default 0..B-1).  9B/gdn_layer.py:282-292."""
+        B, T, H = hidden_states.shape
+        if H != self.hidden:
+            raise ValueError(f"hidden {H} != {self.hidden}")
+        x = hidden_states.to(device=self.device, dtype=torch.bfloat16).contiguous()
+        out = torch.empty_like(x)
+        s = _slots(slot_ids, self.device)
+        _lib.check(_lib.lib().gdn_layer_forward(self._h, _ptr(x), B, T, _ptr(s), _ptr(out), _stream()))
+        return out
+
+    def reset_state(self, slot_ids=None):
+        """Zero the conv and recurrent state of `slot_ids` (default: every slot).  9B/gdn_layer.py:137-151."""
+        s = _slots(slot_ids, self.device)
+        n = self.max_slots if s is None else s.numel()
+        _lib.check(_lib.lib().gdn_state_reset(self._h, _ptr(s), n, _stream()))
+
+    def get_recurrent_state(self, slot_ids=None):
+        """[n, nv, dk, dv] fp32 copy of the recurrent states (default: slots 0..batch-1).  9B/gdn_layer.py:153-157."""
+        rec, _ = self.get_state(slot_ids, conv=False)
+        return rec
+
+    def get_conv_state(self, slot_ids=None):
+        """[n, conv_dim, 3] fp32 conv history in time order (entry 2 = newest input)."""
+        _, conv = self.get_state(slot_ids, rec=False)
+        return conv
+
+    def get_state(self, slot_ids=None, rec=True, conv=True):
+        s = _slots(slot_ids, self.device)
+        n = self.batch if s is None else s.numel()
+        r = torch.empty(n, self.nv, self.dk, self.dv, device=self.device) if rec else None
+        c = torch.empty(n, self.conv_dim, 3, device=self.device) if conv else None
+        _lib.check(_lib.lib().gdn_state_get(self._h, _ptr(s), n, _ptr(r), _ptr(c), _stream()))
+        return r, c
+
+    def set_state(self, rec=None, conv=None, slot_ids=None):
+        """Seed slots with rec [n, nv, dk, dv] and conv [n, conv_dim, 3] (None conv = zero history)."""
+        s = _slots(slot_ids, self.device)
+        ref = rec if rec is not None else conv
+        n = ref.shape[0] if s is None else s.numel()
+        r = rec.to(self.device, torch.float32).contiguous() if rec is not None else None
+        c = conv.to(self.device, torch.float32).contiguous() if conv is not None else None
+        _lib.check(_lib.lib().gdn_state_set(self._h, _ptr(s), n, _ptr(r), _ptr(c), _stream()))
+
+    def state_buffers(self):
+        """Device addresses (rec, conv, ring_pos) of the resident state buffers."""
+        r, c, p = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+        _lib.check(_lib.lib().gdn_layer_state_buffers(self._h, ctypes.byref(r), ctypes.byref(c), ctypes.byref(p)))
+        return r.value, c.value, p.value
+
+    def profile(self, max_calls):
+        """Record stage times (HIP events on the launch stream) for the next `max_calls` forward calls."""
+        _lib.check(_lib.lib().gdn_layer_profile(self._h, int(max_calls)))
+
+    def profile_read(self):
+        """-> (dict of summed ms per stage: in_proj, mixer, out_proj, total; number of calls recorded)."""
+        ms = (ctypes.c_double * 4)()
+        n = ctypes.c_int()
+        _lib.check(_lib.lib().gdn_layer_profile_read(self._h, ms, ctypes.byref(n)))
+        return dict(zip(("in_proj", "mixer", "out_proj", "total"), list(ms))), n.value
+
+    # ---- per-op entries ---------------------------------------------------------------------------
+    def in_proj(self, x):
+        """x [M, H] -> P [M, proj_width] fp32 (q | k | v | z | a | b)."""
+        x = x.to(device=self.device, dtype=torch.bfloat16).contiguous()
+        P = torch.empty(x.shape[0], self.proj_width, device=self.device)
+        _lib.check(_lib.lib().gdn_in_proj(self._h, _ptr(x), x.shape[0], _ptr(P), _stream()))
+        return P
+
+    def conv_front(self, P, B, T, slot_ids=None):
+        """P [B*T, proj_width] -> (qn [M,nk,dk], kn [M,nk,dk], v [M,nv,dv], g [M,nv], beta [M,nv]);
+        advances the conv history of the slots."""
+        M = B * T
+        dev = self.device
+        qn = torch.empty(M, self.nk, self.dk, device=dev)
+        kn = torch.empty(M, self.nk, self.dk, device=dev)
+        v = torch.empty(M, self.nv, self.dv, device=dev)
+        g = torch.empty(M, self.nv, device=dev)
+        beta = torch.empty(M, self.nv, device=dev)
+        s = _slots(slot_ids, dev)
+        P = P.contiguous()
+        _lib.check(_lib.lib().gdn_conv_front(self._h, _ptr(P), B, T, _ptr(s), _ptr(qn), _ptr(kn), _ptr(v), _ptr(g),
+                                             _ptr(beta), _stream()))
+        return qn, kn, v, g, beta
+
+    def delta_rule(self, qn, kn, v, g, beta, B, T, slot_ids=None):
+        """Recurrence on the front end's outputs, continuing the slots' states -> o [M, nv, dv] fp32."""
+        o = torch.empty(B * T, self.nv, self.dv, device=self.device)
+        s = _slots(slot_ids, self.device)
+        t = [x.contiguous() for x in (qn, kn, v, g, beta)]
+        _lib.check(_lib.lib().gdn_delta_rule(self._h, *[_ptr(x) for x in t], B, T, _ptr(s), _ptr(o), _stream()))
+        return o
+
+    def gated_rmsnorm(self, o, z):
+        """o [M, nv*dv] fp32, z [M, >= nv*dv] fp32 rows -> y [M, nv*dv] bf16."""
+        M = o.shape[0]
+        o = o.reshape(M, -1).contiguous()
+        y = torch.empty(M, self.nv * self.dv, device=self.device, dtype=torch.bfloat16)
+        _lib.check(_lib.lib().gdn_gated_rmsnorm(self._h, _ptr(o), _ptr(z), z.stride(0), M, _ptr(y), _stream()))
+        return y
+
+    def out_proj(self, y):
+        """y [M, nv*dv] -> out [M, H] bf16."""
+        y = y.to(device=self.device, dtype=torch.bfloat16).contiguous()
+        out = torch.empty(y.shape[0], self.hidden, device=self.device, dtype=torch.bfloat16)
+        _lib.check(_lib.lib().gdn_out_proj(self._h, _ptr(y), y.shape[0], _ptr(out), _stream()))
+        return out
+
+
+def linear(x, w, out_dtype=torch.float32):
+    """y = x @ w.T on the library's bf16 MFMA projection kernels (x [M, K], w [N, K], K % 128 == 0)."""
+    x = x.to(torch.bfloat16).contiguous()
+    w = w.to(torch.bfloat16).contiguous()
+    y = torch.empty(x.shape[0], w.shape[0], device=x.device, dtype=out_dtype)
+    _lib.check(_lib.lib().gdn_linear_bf16(_ptr(x), _ptr(w), x.shape[0], w.shape[0], x.shape[1], _ptr(y),
+                                          int(out_dtype == torch.float32), _stream()))
+    return y

@@ -1,0 +1,74 @@
+"""The C-ABI library loads, exports every entry point include/gdn.h declares, and rejects bad arguments
+on the host before touching a GPU (these calls return before any HIP launch or allocation)."""
+import ctypes
+
+import pytest
+
+from linear_attention_op_amd import _lib
+
+
+def test_header_declares_the_bound_entry_points():
+    declared = _lib.header_symbols()
+    assert set(declared) == set(_lib.SIGNATURES), (sorted(set(declared) ^ set(_lib.SIGNATURES)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    for name in _lib.header_symbols():
+        assert hasattr(L, name), name
+    assert L.gdn_version() >= 100
+
+
+def _dims(**kw):
+    d = dict(hidden=1024, num_k_heads=16, num_v_heads=16, head_k_dim=128, head_v_dim=128, conv_kernel=4,
+             rms_norm_eps=1e-6)
+    d.update(kw)
+    return _lib.GdnDims(*d.values())
+
+
+@pytest.mark.parametrize("kw, code", [
+    (dict(head_k_dim=96, head_v_dim=96), _lib.GDN_ERR_UNSUPPORTED),
+    (dict(head_v_dim=64), _lib.GDN_ERR_UNSUPPORTED),
+    (dict(num_v_heads=24), _lib.GDN_ERR_UNSUPPORTED),
+    (dict(conv_kernel=3), _lib.GDN_ERR_UNSUPPORTED),
+    (dict(hidden=1000), _lib.GDN_ERR_UNSUPPORTED),
+    (dict(hidden=0), _lib.GDN_ERR_INVALID_ARG),
+])
+def test_create_rejects_bad_geometry(kw, code):
+    L = _lib.lib()
+    h = ctypes.c_void_p()
+    w = _lib.GdnWeights(*([1] * 9))  # never dereferenced: geometry is checked first
+    rc = L.gdn_layer_create(ctypes.byref(_dims(**kw)), ctypes.byref(w), 1, 1, ctypes.byref(h))
+    assert rc == code
+    assert h.value is None
+    assert L.gdn_last_error()
+
+
+def test_null_arguments_are_errors_not_crashes():
+    L = _lib.lib()
+    h = ctypes.c_void_p()
+    assert L.gdn_layer_create(None, None, 1, 1, ctypes.byref(h)) == _lib.GDN_ERR_INVALID_ARG
+    w = _lib.GdnWeights(*([0] * 9))
+    assert L.gdn_layer_create(ctypes.byref(_dims()), ctypes.byref(w), 1, 1, ctypes.byref(h)) == \
+        _lib.GDN_ERR_INVALID_ARG
+    assert L.gdn_layer_forward(None, None, 1, 1, None, None, None) == _lib.GDN_ERR_INVALID_ARG
+    assert L.gdn_state_get(None, None, 1, None, None, None) == _lib.GDN_ERR_INVALID_ARG
+    assert L.gdn_layer_destroy(None) == _lib.GDN_OK
+
+
+def test_linear_and_recurrence_shape_checks():
+    L = _lib.lib()
+    p = ctypes.c_void_p(16)  # non-null, never dereferenced
+    assert L.gdn_linear_bf16(p, p, 4, 8, 100, p, 1, None) == _lib.GDN_ERR_UNSUPPORTED
+    assert L.gdn_linear_bf16(p, p, 0, 8, 128, p, 1, None) == _lib.GDN_ERR_SHAPE
+    args = [p] * 5
+    assert L.gdn_delta_rule_fla(*args, 1, 1, 2, 3, 128, 128, p, 1, 0.0, p, None) == _lib.GDN_ERR_UNSUPPORTED
+    assert L.gdn_delta_rule_fla(*args, 1, 1, 2, 4, 100, 100, p, 1, 0.0, p, None) == _lib.GDN_ERR_UNSUPPORTED
+    assert L.gdn_delta_rule_fla(*args, 1, 0, 2, 4, 128, 128, p, 1, 0.0, p, None) == _lib.GDN_ERR_SHAPE
+
+
+def test_errors_raise_value_error_in_python():
+    with pytest.raises(ValueError):
+        _lib.check(_lib.GDN_ERR_SHAPE)
+    with pytest.raises(_lib.GdnError):
+        _lib.check(_lib.GDN_ERR_HIP)

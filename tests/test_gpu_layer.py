@@ -1,0 +1,284 @@
+"""GPU parity of the whole layer and of its five per-op entries, through the C ABI.
+
+Truth: the HF golden vectors (tiny geometry, the reference's (B, T) grid and prefill -> decode
+continuation, 9B/test_gdn_layer.py:42-73) and the CPU oracle on the same seeded inputs at the real
+0.8B and 9B shapes.  Bars: layer output (bf16) rel-L2 <= 1e-2, recurrent state (fp32) <= 1e-3, conv
+history bit-exact (it is a copy of projection outputs; the integer ring indexing must match the
+reference's shift / roll rules).
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from linear_attention_op_amd import Qwen35GatedDeltaNetHIP
+from linear_attention_op_amd import synthetic as syn
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU")]
+
+G = os.path.join(os.path.dirname(__file__), "golden")
+OUT_TOL = 1e-2
+STATE_TOL = 1e-3
+
+
+def rel(a, b):
+    a = np.asarray(a.float().cpu() if torch.is_tensor(a) else a, dtype=np.float64)
+    b = np.asarray(b.float().cpu() if torch.is_tensor(b) else b, dtype=np.float64)
+    return float(np.linalg.norm(a - b) / np.linalg.norm(b))
+
+
+def load(name):
+    return dict(np.load(os.path.join(G, name)))
+
+
+def odims(d):
+    return oracle.dims(d["hidden"], d["num_k_heads"], d["num_v_heads"], d["head_k_dim"], d["head_v_dim"])
+
+
+TINY = syn.SHAPES["tiny"]
+
+
+# ---- HF golden vectors ------------------------------------------------------------------------------
+@pytest.mark.parametrize("B, T", [(1, 1), (1, 40), (4, 9), (2, 70)])
+@pytest.mark.parametrize("max_tokens", [16384, 32])
+def test_layer_matches_hf(B, T, max_tokens):
+    """T = 70 > 64 takes the token-parallel front end; max_tokens = 32 splits the launch (state carried)."""
+    print(f"layer vs HF B={B} T={T} max_tokens={max_tokens}", flush=True)
+    w = load("tiny_weights.npz")
+    f = load(f"tiny_layer_B{B}_T{T}.npz")
+    layer = Qwen35GatedDeltaNetHIP(w, dims=TINY, batch=B, max_tokens=max(max_tokens, B))
+    out = layer(torch.from_numpy(f["x"]))
+    rec, conv = layer.get_state()
+    torch.cuda.synchronize()
+    assert rel(out, f["out"]) < OUT_TOL
+    assert rel(rec, f["rec_state"]) < STATE_TOL
+    assert rel(conv, f["conv_state"]) < 1e-5
+
+
+def test_prefill_then_decode_matches_hf():
+    """Prefill 20 tokens, then 5 single-token calls (9B/test_gdn_layer.py:52-63)."""
+    f = load("tiny_continue.npz")
+    layer = Qwen35GatedDeltaNetHIP(f, dims=TINY, batch=1)
+    x = torch.from_numpy(f["x"])
+    outs = [layer(x[:, :20])] + [layer(x[:, t:t + 1]) for t in range(20, 25)]
+    rec, conv = layer.get_state()
+    torch.cuda.synchronize()
+    out = torch.cat(outs, 1)
+    assert rel(out[:, :20], f["out_full"][:, :20]) < OUT_TOL
+    assert rel(out[:, 20:], f["out_full"][:, 20:]) < OUT_TOL
+    assert rel(rec, f["rec_state"]) < STATE_TOL
+
+
+def test_state_addresses_are_stable_and_reset_zeroes():
+    f = load("tiny_continue.npz")
+    layer = Qwen35GatedDeltaNetHIP(f, dims=TINY, batch=1)
+    addr = layer.state_buffers()
+    x = torch.from_numpy(f["x"])
+    for t in range(8):
+        layer(x[:, t:t + 1])
+    assert layer.state_buffers() == addr
+    layer.reset_state()
+    rec, conv = layer.get_state()
+    torch.cuda.synchronize()
+    assert float(rec.abs().max()) == 0.0 and float(conv.abs().max()) == 0.0
+
+
+# ---- per-op entries against the oracle's ops -------------------------------------------------------
+@pytest.fixture(scope="module")
+def layer08():
+    d = syn.SHAPES["0.8b"]
+    w, gen = syn.make_weights(d, seed=11)
+    return d, w, syn.to_numpy(w), gen
+
+
+def test_per_op_pipeline_matches_oracle(layer08):
+    d, w, wn, gen = layer08
+    B, T = 2, 5
+    x, s0 = syn.make_inputs(d, B, T, gen, state_std=0.01)
+    layer = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B)
+    layer.set_state(rec=s0.cuda())
+    M = B * T
+    P = layer.in_proj(x.reshape(M, -1))
+    wcat = np.concatenate([wn["w_qkv"], wn["w_z"], wn["w_a"], wn["w_b"]])
+    assert rel(P, oracle.linear(x.reshape(M, -1).numpy(), wcat)) < 1e-5
+
+    Pn = P.cpu().numpy()
+    conv0 = np.zeros((B, syn.conv_dim(d), 3), np.float32)
+    want = oracle.conv_front(odims(d), Pn, B, T, wn, conv0)
+    got = layer.conv_front(P, B, T)
+    for a, b in zip(got, want):
+        assert rel(a, b) < 1e-5
+    conv = layer.get_conv_state()
+    assert np.array_equal(conv.cpu().numpy(), conv0)  # bit-exact history
+
+    qn, kn, v, g, beta = got
+    o = layer.delta_rule(qn, kn, v, g, beta, B, T)
+    ct = [t.cpu().numpy() for t in got]
+    q4 = ct[0].reshape(B, T, d["num_k_heads"], -1)
+    k4 = ct[1].reshape(B, T, d["num_k_heads"], -1)
+    v4 = ct[2].reshape(B, T, d["num_v_heads"], -1)
+    want_o, want_s = oracle.recurrent_gated_delta_rule(q4, k4, v4, ct[3].reshape(B, T, -1), ct[4].reshape(B, T, -1),
+                                                       s0.numpy(), use_qk_l2norm=False, scale=1.0)
+    assert rel(o.reshape(B, T, d["num_v_heads"], -1), want_o) < STATE_TOL
+    assert rel(layer.get_recurrent_state(), want_s) < STATE_TOL
+
+    Vd = d["num_v_heads"] * d["head_v_dim"]
+    z = P[:, syn.conv_dim(d):syn.conv_dim(d) + Vd]
+    y = layer.gated_rmsnorm(o.reshape(M, -1), z)
+    want_y = oracle.gated_rmsnorm(o.reshape(-1, d["head_v_dim"]).cpu().numpy(),
+                                  z.reshape(-1, d["head_v_dim"]).cpu().numpy(), wn["norm_w"]).reshape(M, -1)
+    assert rel(y, want_y) < 5e-3
+    out = layer.out_proj(y)
+    assert rel(out, oracle.linear(y.float().cpu().numpy(), wn["w_out"])) < 5e-3
+
+
+@pytest.mark.parametrize("Ts", [(1, 2, 3, 4, 5, 1, 1), (3, 1, 70, 2)])
+def test_conv_ring_is_bit_exact_across_launches(layer08, Ts):
+    """Launch lengths below, at and above the 3-entry history, continuing one ring (layer_reader.cpp
+    shift 111-120 / roll 189-194 rules in the oracle)."""
+    d, w, wn, gen = layer08
+    B = 2
+    layer = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B)
+    conv = np.zeros((B, syn.conv_dim(d), 3), np.float32)
+    for T in Ts:
+        x, _ = syn.make_inputs(d, B, T, gen)
+        P = layer.in_proj(x.reshape(B * T, -1))
+        got = layer.conv_front(P, B, T)
+        want = oracle.conv_front(odims(d), P.cpu().numpy(), B, T, wn, conv)
+        assert np.array_equal(layer.get_conv_state().cpu().numpy(), conv), f"T={T}"
+        assert rel(got[2], want[2]) < 1e-5
+
+
+def test_fused_and_split_paths_agree(layer08):
+    """The fused decode mixer and the per-op pipeline give the same layer output and states."""
+    d, w, wn, gen = layer08
+    B, T = 3, 4
+    x, s0 = syn.make_inputs(d, B, T, gen, state_std=0.01)
+    a = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B)
+    b = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B)
+    a.set_state(rec=s0.cuda())
+    b.set_state(rec=s0.cuda())
+    out_a = a(x)
+    M = B * T
+    P = b.in_proj(x.reshape(M, -1))
+    qn, kn, v, g, beta = b.conv_front(P, B, T)
+    o = b.delta_rule(qn, kn, v, g, beta, B, T)
+    Vd = d["num_v_heads"] * d["head_v_dim"]
+    y = b.gated_rmsnorm(o.reshape(M, -1), P[:, syn.conv_dim(d):syn.conv_dim(d) + Vd])
+    out_b = b.out_proj(y).reshape(B, T, -1)
+    torch.cuda.synchronize()
+    assert rel(out_a, out_b) < 2e-3
+    assert rel(a.get_recurrent_state(), b.get_recurrent_state()) < 1e-5
+    assert torch.equal(a.get_conv_state(), b.get_conv_state())
+
+
+def test_slot_indirection(layer08):
+    """Sequences can live in any slots; results follow the slots, not the batch position."""
+    d, w, wn, gen = layer08
+    B, T = 3, 2
+    x, s0 = syn.make_inputs(d, B, T, gen, state_std=0.01)
+    ref = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B)
+    ref.set_state(rec=s0.cuda())
+    out_ref = ref(x)
+    lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B, max_slots=5)
+    slots = [4, 0, 2]
+    lay.set_state(rec=s0.cuda(), slot_ids=slots)
+    out = lay(x, slot_ids=slots)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_ref)
+    assert torch.equal(lay.get_recurrent_state(slots), ref.get_recurrent_state())
+
+
+# ---- the benchmark configurations against the oracle -----------------------------------------------
+def run_oracle_steps(d, wn, xs, s0):
+    B = xs.shape[0]
+    rec = s0.numpy().copy()
+    conv = np.zeros((B, syn.conv_dim(d), 3), np.float32)
+    out = oracle.layer_forward(odims(d), wn, xs.numpy(), rec, conv)
+    return out, rec, conv
+
+
+def test_config_08b_decode_b1():
+    """0.8B shape, decode batch 1, one step, seed 0: weights N(0, 0.02) bf16, S0 ~ N(0, 0.01), conv zeros."""
+    d = syn.SHAPES["0.8b"]
+    w, gen = syn.make_weights(d, seed=0)
+    x, s0 = syn.make_inputs(d, 1, 1, gen, state_std=0.01)
+    layer = Qwen35GatedDeltaNetHIP(w, dims=d, batch=1)
+    layer.set_state(rec=s0.cuda())
+    out = layer(x)
+    rec, conv = layer.get_state()
+    torch.cuda.synchronize()
+    want, wrec, wconv = run_oracle_steps(d, syn.to_numpy(w), x, s0)
+    print(f"0.8B B=1: out {rel(out, want):.2e} state {rel(rec, wrec):.2e}", flush=True)
+    assert rel(out, want) < OUT_TOL
+    assert rel(rec, wrec) < STATE_TOL
+    assert np.array_equal(conv.cpu().numpy(), wconv) or rel(conv, wconv) < 1e-6
+
+
+def test_config_08b_decode_b32_256_steps():
+    """0.8B shape, decode batch 32, 256 consecutive tokens, seed 1; state checked every step."""
+    d = syn.SHAPES["0.8b"]
+    w, gen = syn.make_weights(d, seed=1)
+    wn = syn.to_numpy(w)
+    B, steps = 32, 256
+    x, s0 = syn.make_inputs(d, B, steps, gen, state_std=0.01)
+    layer = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B)
+    layer.set_state(rec=s0.cuda())
+    rec_o = s0.numpy().copy()
+    conv_o = np.zeros((B, syn.conv_dim(d), 3), np.float32)
+    worst_out = worst_state = 0.0
+    xg = x.cuda()
+    for t in range(steps):
+        out = layer(xg[:, t:t + 1])
+        want = oracle.layer_forward(odims(d), wn, x[:, t:t + 1].numpy(), rec_o, conv_o)
+        rec = layer.get_recurrent_state()
+        worst_out = max(worst_out, rel(out, want))
+        worst_state = max(worst_state, rel(rec, rec_o))
+        if t % 64 == 63:
+            print(f"step {t + 1}: worst out {worst_out:.2e} worst state {worst_state:.2e}", flush=True)
+    assert worst_out < OUT_TOL
+    assert worst_state < STATE_TOL
+
+
+@pytest.fixture(scope="module")
+def layer9b():
+    d = syn.SHAPES["9b"]
+    w, gen = syn.make_weights(d, seed=2)
+    return d, w, syn.to_numpy(w), gen
+
+
+@pytest.mark.parametrize("B", [1, 8, 64])
+def test_config_9b_decode(layer9b, B):
+    """9B shape, decode at batch 1 / 8 / 64 from S0 ~ N(0, 0.01); two steps so the ring advances."""
+    d, w, wn, gen = layer9b
+    print(f"9B decode B={B}", flush=True)
+    x, s0 = syn.make_inputs(d, B, 2, gen, state_std=0.01)
+    layer = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B)
+    layer.set_state(rec=s0.cuda())
+    outs = [layer(x[:, t:t + 1]) for t in range(2)]
+    rec = layer.get_recurrent_state()
+    torch.cuda.synchronize()
+    rec_o = s0.numpy().copy()
+    conv_o = np.zeros((B, syn.conv_dim(d), 3), np.float32)
+    want = [oracle.layer_forward(odims(d), wn, x[:, t:t + 1].numpy(), rec_o, conv_o) for t in range(2)]
+    for o, wv in zip(outs, want):
+        assert rel(o, wv) < OUT_TOL
+    assert rel(rec, rec_o) < STATE_TOL
+
+
+def test_config_9b_prefill_short(layer9b):
+    """9B shape prefill from a zero state at T = 256 against the oracle (long prefills: see the
+    full-size checks of the chunked path)."""
+    d, w, wn, gen = layer9b
+    T = 256
+    x, _ = syn.make_inputs(d, 1, T, gen)
+    layer = Qwen35GatedDeltaNetHIP(w, dims=d, batch=1)
+    out = layer(x)
+    rec = layer.get_recurrent_state()
+    torch.cuda.synchronize()
+    want, rec_o, _ = run_oracle_steps(d, wn, x, torch.zeros(1, d["num_v_heads"], 128, 128))
+    print(f"9B prefill T={T}: out {rel(out, want):.2e} state {rel(rec, rec_o):.2e}", flush=True)
+    assert rel(out, want) < OUT_TOL
+    assert rel(rec, rec_o) < STATE_TOL

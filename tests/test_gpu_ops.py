@@ -1,0 +1,118 @@
+"""GPU parity of the projection kernels and the recurrence-only op, through the C ABI.
+
+Projections: against an fp64 CPU matmul of the same bf16 operands (fp32 output: accumulation noise
+only; bf16 output: one rounding).  Recurrence: the reference's own cases
+(9B/test_gated_delta_l1.py:48-92) against the CPU oracle, plus the HF golden vectors; the bar is the
+fp32-state tolerance, rel-L2 <= 1e-3, for both the output and the final state.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from linear_attention_op_amd import GatedDeltaRuleHIP, GdnValueError, linear
+
+pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not torch.cuda.is_available(), reason="needs a GPU")]
+
+G = os.path.join(os.path.dirname(__file__), "golden")
+STATE_TOL = 1e-3
+
+
+def rel(a, b):
+    a = torch.as_tensor(np.asarray(a.cpu() if torch.is_tensor(a) else a), dtype=torch.float64)
+    b = torch.as_tensor(np.asarray(b.cpu() if torch.is_tensor(b) else b), dtype=torch.float64)
+    return float((a - b).norm() / b.norm())
+
+
+@pytest.mark.parametrize("M, N, K", [
+    (1, 392, 256), (3, 4096, 4096), (16, 12352, 4096), (17, 1024, 2048), (40, 8224, 1024), (64, 12352, 4096),
+    (64, 4096, 4096), (65, 392, 256), (200, 4096, 1024), (512, 12352, 4096), (300, 1000, 128),
+])
+def test_linear(M, N, K):
+    print(f"linear M={M} N={N} K={K}", flush=True)
+    gen = torch.Generator().manual_seed(M * 7 + N)
+    x = torch.randn(M, K, generator=gen).bfloat16()
+    w = (torch.randn(N, K, generator=gen) * 0.02).bfloat16()
+    want = x.double() @ w.double().T
+    y32 = linear(x.cuda(), w.cuda(), torch.float32)
+    y16 = linear(x.cuda(), w.cuda(), torch.bfloat16)
+    torch.cuda.synchronize()
+    assert rel(y32, want) < 1e-5
+    assert rel(y16.float(), want) < 5e-3
+
+
+def make_rec_inputs(B, T, Hk, Hv, dk, dv, seed=0, g_shift=2.0):
+    """The reference's draw order (9B/test_gated_delta_l1.py:17-24)."""
+    gen = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, Hk, dk, generator=gen)
+    k = torch.randn(B, T, Hk, dk, generator=gen)
+    v = torch.randn(B, T, Hv, dv, generator=gen)
+    g = torch.nn.functional.logsigmoid(torch.randn(B, T, Hv, generator=gen) + g_shift)
+    beta = torch.sigmoid(torch.randn(B, T, Hv, generator=gen))
+    return q, k, v, g, beta
+
+
+@pytest.mark.parametrize("B, Hk, Hv, T", [(1, 16, 32, 1), (1, 16, 32, 45), (1, 8, 16, 7), (4, 16, 32, 3)])
+def test_recurrence_matches_oracle(B, Hk, Hv, T):
+    print(f"recurrence B={B} Hk={Hk} Hv={Hv} T={T}", flush=True)
+    dk = dv = 128
+    q, k, v, g, beta = make_rec_inputs(B, T, Hk, Hv, dk, dv)
+    init = torch.randn(B, Hv, dk, dv) * 0.1
+    want_o, want_s = oracle.recurrent_gated_delta_rule(q.numpy(), k.numpy(), v.numpy(), g.numpy(), beta.numpy(),
+                                                       init.numpy())
+    op = GatedDeltaRuleHIP(B * Hv, dk, dv, initial_state=init.reshape(B * Hv, dk, dv).cuda())
+    got_o = op(q, k, v, g, beta)
+    torch.cuda.synchronize()
+    assert rel(got_o, want_o) < STATE_TOL
+    assert rel(op.get_state(), want_s.reshape(B * Hv, dk, dv)) < STATE_TOL
+
+
+def test_long_sequence_slow_decay():
+    """T = 1024 with decay ~0.99 (9B/test_gated_delta_l1.py:69-78)."""
+    B, Hk, Hv, dk, dv, T = 1, 16, 32, 128, 128, 1024
+    q, k, v, _, beta = make_rec_inputs(B, T, Hk, Hv, dk, dv, seed=3)
+    g = torch.nn.functional.logsigmoid(torch.randn(B, T, Hv, generator=torch.Generator().manual_seed(4)) + 5.0)
+    want_o, want_s = oracle.recurrent_gated_delta_rule(q.numpy(), k.numpy(), v.numpy(), g.numpy(), beta.numpy())
+    op = GatedDeltaRuleHIP(B * Hv, dk, dv)
+    got_o = op(q, k, v, g, beta)
+    torch.cuda.synchronize()
+    assert rel(got_o, want_o) < STATE_TOL
+    assert rel(op.get_state(), want_s.reshape(B * Hv, dk, dv)) < STATE_TOL
+
+
+def test_decode_loop_keeps_state_resident():
+    """64 single-token calls: the state buffer never moves (9B/test_gated_delta_l1.py:81-92)."""
+    B, Hk, Hv, dk, dv, steps = 1, 16, 32, 128, 128, 64
+    q, k, v, g, beta = make_rec_inputs(B, steps, Hk, Hv, dk, dv, seed=1)
+    want_o, want_s = oracle.recurrent_gated_delta_rule(q.numpy(), k.numpy(), v.numpy(), g.numpy(), beta.numpy())
+    op = GatedDeltaRuleHIP(B * Hv, dk, dv)
+    addr = op.state.data_ptr()
+    outs = [op(q[:, t:t + 1], k[:, t:t + 1], v[:, t:t + 1], g[:, t:t + 1], beta[:, t:t + 1]) for t in range(steps)]
+    assert op.state.data_ptr() == addr
+    torch.cuda.synchronize()
+    assert rel(torch.cat(outs, 1), want_o) < STATE_TOL
+    assert rel(op.get_state(), want_s.reshape(B * Hv, dk, dv)) < STATE_TOL
+
+
+@pytest.mark.parametrize("name", ["rec_gqa", "rec_real_dims", "rec_slow_decay"])
+def test_recurrence_matches_hf_golden(name):
+    f = dict(np.load(os.path.join(G, name + ".npz")))
+    B, T, Hk, dk = f["q"].shape
+    Hv, dv = f["v"].shape[2:]
+    init = torch.from_numpy(f["init"]).reshape(B * Hv, dk, dv).cuda() if "init" in f else None
+    op = GatedDeltaRuleHIP(B * Hv, dk, dv, initial_state=init)
+    o = op(*[torch.from_numpy(f[n]) for n in ("q", "k", "v", "g", "beta")])
+    torch.cuda.synchronize()
+    assert rel(o, f["o"]) < STATE_TOL
+    assert rel(op.get_state(), f["state"].reshape(B * Hv, dk, dv)) < STATE_TOL
+
+
+def test_unsupported_head_dims_raise():
+    f = dict(np.load(os.path.join(G, "rec_chunk_edge.npz")))  # dk = 16, dv = 24
+    B, T, Hk, dk = f["q"].shape
+    Hv, dv = f["v"].shape[2:]
+    op = GatedDeltaRuleHIP(B * Hv, dk, dv)
+    with pytest.raises(GdnValueError):
+        op(*[torch.from_numpy(f[n]) for n in ("q", "k", "v", "g", "beta")])
