@@ -121,7 +121,9 @@ int gdn_conv_front(gdn_layer* layer, const float* P, int B, int T, const int* sl
                    float* v, float* g, float* beta, void* stream);
 
 /* Recurrence: 9B/kernels/layer_compute.cpp C5 (224-285); 9B/reference.py:28-34.
- * On normalised inputs from gdn_conv_front, continuing each slot's recurrent state.  o: fp32 [M, nv, dv]. */
+ * On normalised inputs from gdn_conv_front, continuing each slot's recurrent state.  o: fp32 [M, nv, dv].
+ * Launches of more than 64 tokens per sequence use the chunk-64 form (HF torch_chunk_gated_delta_rule,
+ * modeling_qwen3_5.py:248-328) when dk == dv == 128, otherwise the token loop. */
 int gdn_delta_rule(gdn_layer* layer, const float* qn, const float* kn, const float* v, const float* g,
                    const float* beta, int B, int T, const int* slot_ids, float* o, void* stream);
 

@@ -17,7 +17,7 @@ LIB = os.path.join(HERE, "libgdn_hip.so")
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
-SOURCES = ["gdn_linear.hip", "gdn_mixer.hip", "gdn_delta.hip", "gdn_api.cpp"]
+SOURCES = ["gdn_linear.hip", "gdn_mixer.hip", "gdn_delta.hip", "gdn_chunk.hip", "gdn_api.cpp"]
 
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-result",

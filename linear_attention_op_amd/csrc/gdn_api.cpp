@@ -123,6 +123,16 @@ int check_dims(const gdn_dims* d) {
 
 hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
+// Recurrence dispatch: launches of more than kFusedMaxT tokens per sequence take the chunk-64 form
+// (when the head size has it and the workspace holds the launch), shorter ones the token loop.
+hipError_t run_delta(gdn_layer* L, const gdn::DeltaArgs& r, hipStream_t st) {
+    const gdn_dims& d = L->d;
+    if (r.T > kFusedMaxT && L->chunk_ws &&
+        gdn::delta_chunked_workspace(r.B, r.T, d.num_v_heads, d.head_k_dim, d.head_v_dim) <= L->chunk_ws_bytes)
+        return gdn::launch_delta_chunked(r, d.head_k_dim, d.head_v_dim, L->chunk_ws, L->chunk_ws_bytes, st);
+    return gdn::launch_delta_seq(r, d.head_k_dim, d.head_v_dim, st);
+}
+
 int run_chunk(gdn_layer* L, const u16* x, int B, int T, const int* slot_ids, u16* out, hipStream_t st) {
     const gdn_dims& d = L->d;
     const int M = B * T;
@@ -153,7 +163,7 @@ int run_chunk(gdn_layer* L, const u16* x, int B, int T, const int* slot_ids, u16
         r.q = L->qn, r.k = L->kn, r.v = L->v, r.g = L->g, r.beta = L->beta;
         r.B = B, r.T = T, r.Hk = d.num_k_heads, r.Hv = d.num_v_heads, r.slot_ids = slot_ids;
         r.state = L->rec, r.o = L->o, r.normalize = 0, r.scale = 1.f;
-        HIP_OK(gdn::launch_delta_seq(r, d.head_k_dim, d.head_v_dim, st));
+        HIP_OK(run_delta(L, r, st));
         HIP_OK(gdn::launch_gated_rmsnorm(L->o, M, d.num_v_heads, d.head_v_dim, L->P + L->CD, L->NP, L->norm_w,
                                          d.rms_norm_eps, L->y, st));
     }
@@ -216,6 +226,15 @@ int gdn_layer_create(const gdn_dims* dims, const gdn_weights* w, int max_slots, 
     take(L->alloc(&L->beta, MT * nv));
     take(L->alloc(&L->o, MT * L->Vd));
     take(L->alloc(&L->y, MT * L->Vd));
+    if (max_tokens > kFusedMaxT && gdn::delta_chunked_supported(dk, dv)) {
+        // chunked-prefill workspace for the worst launch: B sequences of T > kFusedMaxT tokens with
+        // B * T <= max_tokens hold at most max_tokens / 64 + max_tokens / 65 + 1 chunks
+        const int chunks = max_tokens / 64 + max_tokens / (kFusedMaxT + 1) + 1;
+        L->chunk_ws_bytes = gdn::delta_chunked_workspace(1, 64 * chunks, nv, dk, dv);
+        char* p = nullptr;
+        take(L->alloc(&p, L->chunk_ws_bytes));
+        L->chunk_ws = p;
+    }
     if (e != hipSuccess) {
         delete L;
         return fail(e == hipErrorOutOfMemory ? GDN_ERR_OUT_OF_MEMORY : GDN_ERR_HIP, "gdn_layer_create: %s",
@@ -388,7 +407,7 @@ int gdn_delta_rule(gdn_layer* L, const float* qn, const float* kn, const float* 
     r.q = qn, r.k = kn, r.v = v, r.g = g, r.beta = beta;
     r.B = B, r.T = T, r.Hk = d.num_k_heads, r.Hv = d.num_v_heads, r.slot_ids = slot_ids;
     r.state = L->rec, r.o = o, r.normalize = 0, r.scale = 1.f;
-    HIP_OK(gdn::launch_delta_seq(r, d.head_k_dim, d.head_v_dim, as_stream(stream)));
+    HIP_OK(run_delta(L, r, as_stream(stream)));
     return GDN_OK;
 }
 

@@ -1,0 +1,451 @@
+// Chunked (64-token) gated delta rule for prefills: the WY / UT form of the recurrence on bf16 MFMA with
+// the state carried in fp32.  Restates the chunk algorithm of HF torch_chunk_gated_delta_rule
+// (transformers qwen3_5 modeling_qwen3_5.py:248-328, the layer truth the reference tests against,
+// wormhole_n150/qwen3.5_9B/test_gdn_layer.py:42-73); it equals the token-by-token rule of
+// wormhole_n150/qwen3.5_9B/reference.py:28-34 up to rounding.
+//
+// Per (sequence, v-head) and chunk of C = 64 tokens, with G = in-chunk cumulative log decay,
+// Gam_ij = exp(G_i - G_j) (i >= j), normalised q, k, and the chunk's initial state S:
+//     L    = strict_tril(beta k k^T (.) Gam)          T = (I + L)^-1            (fp32 forward substitution)
+//     U    = T (beta V)                               W = T (beta K (.) e^G)
+//     Aqk  = tril(q k^T (.) Gam)                      Q' = Q (.) e^G - Aqk W
+//     O    = Q' S + Aqk U                             (= Q e^G S + Aqk (U - W S))
+//     Vn   = U - W S
+//     S   <- e^{G_last} S + (K (.) e^{G_last - G})^T Vn
+//
+// Two kernels:
+//  * chunk_prep_kernel: every (sequence, v-head, chunk) in parallel.  Everything that does not depend on
+//    S: G, L, T, U, W, Q' and the intra-chunk output Aqk U (written straight into o).
+//  * chunk_state_kernel: the sequential pass over chunks.  A workgroup owns 16 value columns of one
+//    (sequence, v-head) state; its four waves own 32 state rows each, held in MFMA accumulators for the
+//    whole launch (state read once, written once).  Per chunk: W S and Q' S (partials over the waves'
+//    rows, summed through LDS), Vn, O += Q' S, S update.  The next chunk's operands are loaded while the
+//    current one is computed.  Workgroup ids put the 8 column blocks of a head on one XCD so that they
+//    share that XCD's L2 copy of W, Q' and k.
+//
+// Precision: every product that feeds the state or the output goes through split bf16 (hi + lo, three
+// MFMAs, ~2^-17 relative), so the chunked state matches the fp32 sequential rule to ~1e-5.
+#include "gdn_common.h"
+
+namespace gdn {
+
+namespace {
+
+constexpr int CK = 64;  // chunk length
+
+__device__ __forceinline__ void load8(const float* p, float* v) {
+    const float4 a = *reinterpret_cast<const float4*>(p);
+    const float4 b = *reinterpret_cast<const float4*>(p + 4);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+}
+
+struct ChunkWs {
+    float* W;   // [B, Hv, NC, CK, dk]
+    float* Q;   // [B, Hv, NC, CK, dk]   Q'
+    float* U;   // [B, Hv, NC, CK, dv]
+    float* G;   // [B, Hv, NC, 2, CK]    G (in-chunk cumulative log decay), rk (key normaliser)
+    int NC;     // chunks per sequence
+};
+
+// ------------------------------------------------------------------------------------------------
+// chunk_prep_kernel: grid (NC, Hv, B), 256 threads.
+// ------------------------------------------------------------------------------------------------
+template <int DK, int DV>
+__global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws) {
+    static_assert(DK == 128 && DV == 128, "chunked path is specialised for 128-wide heads");
+    constexpr int LDK = DK + 4;  // row stride (floats) of the key tile
+    constexpr int LDT = CK + 4;  // row stride of the 64 x 64 tiles
+    __shared__ __attribute__((aligned(16))) float sK[CK * LDK];
+    __shared__ __attribute__((aligned(16))) float sT[CK * LDT];  // L, then T
+    __shared__ __attribute__((aligned(16))) float sA[CK * LDT];  // Aqk, then M2 = Aqk T
+    __shared__ float sG[CK], sEG[CK], sBeta[CK], sRq[CK], sRk[CK];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    const int T = a.T, Hk = a.Hk, Hv = a.Hv, kh = h / (Hv / Hk);
+    const int t0 = c * CK, len = min(CK, T - t0);
+    const size_t row0 = (size_t)b * T + t0;
+    const int m = lane & 15, grp = lane >> 4;
+    const size_t hc = ((size_t)b * Hv + h) * ws.NC + c;
+
+    // ---- per-token scalars: G = cumsum(g) (padded tokens add 0), beta, q / k normalisers ---------
+    if (wave == 0) {
+        float gv = lane < len ? a.g[(row0 + lane) * Hv + h] : 0.f;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const float y = __shfl_up(gv, off, 64);
+            if (lane >= off) gv += y;
+        }
+        sG[lane] = gv;
+        sEG[lane] = __expf(gv);
+        sBeta[lane] = lane < len ? a.beta[(row0 + lane) * Hv + h] : 0.f;
+    }
+    for (int i = 0; i < 16; ++i) {
+        const int tok = wave * 16 + i;
+        float rq = a.scale, rk = 1.f;
+        if (a.normalize && tok < len) {
+            const float2 qv = *reinterpret_cast<const float2*>(a.q + ((row0 + tok) * Hk + kh) * DK + 2 * lane);
+            const float2 kv = *reinterpret_cast<const float2*>(a.k + ((row0 + tok) * Hk + kh) * DK + 2 * lane);
+            rq = rsqrtf(warp_sum(qv.x * qv.x + qv.y * qv.y) + 1e-6f) * a.scale;
+            rk = rsqrtf(warp_sum(kv.x * kv.x + kv.y * kv.y) + 1e-6f);
+        }
+        if (lane == 0) sRq[tok] = rq, sRk[tok] = rk;
+    }
+    __syncthreads();
+
+    // ---- normalised keys into LDS (rows past the sequence are zero) --------------------------------
+    for (int e = tid; e < CK * DK / 4; e += 256) {
+        const int tok = e / (DK / 4), c4 = (e % (DK / 4)) * 4;
+        float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (tok < len) {
+            kv = *reinterpret_cast<const float4*>(a.k + ((row0 + tok) * Hk + kh) * DK + c4);
+            const float r = sRk[tok];
+            kv.x *= r, kv.y *= r, kv.z *= r, kv.w *= r;
+        }
+        *reinterpret_cast<float4*>(&sK[tok * LDK + c4]) = kv;
+    }
+    __syncthreads();
+
+    // ---- k k^T and q k^T: wave w owns row tile w, column tiles <= w ------------------------------
+    {
+        const int mi = wave;
+        f32x4 akk[4], aqk[4];
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) akk[ni] = aqk[ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+        const int qr = 16 * mi + m;
+        const bool qvalid = qr < len;
+        const float rq = sRq[qr];
+        const float* qrow = a.q + ((row0 + (qvalid ? qr : 0)) * Hk + kh) * DK;
+#pragma unroll
+        for (int s = 0; s < DK / 32; ++s) {
+            const int k0 = 32 * s + 8 * grp;
+            float ka[8], qa[8];
+            load8(&sK[qr * LDK + k0], ka);
+            if (qvalid) {
+                load8(qrow + k0, qa);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) qa[j] *= rq;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) qa[j] = 0.f;
+            }
+            const Split8 A1 = split8(ka), A2 = split8(qa);
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                if (ni > mi) continue;
+                float kb[8];
+                load8(&sK[(16 * ni + m) * LDK + k0], kb);
+                const Split8 Bk = split8(kb);
+                akk[ni] = mfma3(A1, Bk, akk[ni]);
+                aqk[ni] = mfma3(A2, Bk, aqk[ni]);
+            }
+        }
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 16 * mi + 4 * grp + i, cc = 16 * ni + m;
+                float L = 0.f, A = 0.f;
+                if (ni <= mi && cc <= r) {
+                    const float dec = __expf(sG[r] - sG[cc]);
+                    A = aqk[ni][i] * dec;
+                    if (cc < r) L = sBeta[r] * akk[ni][i] * dec;
+                }
+                sT[r * LDT + cc] = L;
+                sA[r * LDT + cc] = A;
+            }
+    }
+    __syncthreads();
+
+    // ---- T = (I + L)^-1 by forward substitution: lane j of wave 0 owns column j ---------------------
+    //      T[i][j] = delta_ij - sum_{k < i} L[i][k] T[k][j]
+    if (wave == 0) {
+        const int j = lane;
+        float t[CK];
+#pragma unroll
+        for (int i = 0; i < CK; ++i) {
+            float acc = (i == j) ? 1.f : 0.f;
+            const float* Li = &sT[i * LDT];
+#pragma unroll
+            for (int k4 = 0; k4 < i / 4; ++k4) {
+                const float4 l4 = *reinterpret_cast<const float4*>(Li + 4 * k4);
+                acc -= l4.x * t[4 * k4] + l4.y * t[4 * k4 + 1] + l4.z * t[4 * k4 + 2] + l4.w * t[4 * k4 + 3];
+            }
+#pragma unroll
+            for (int k = 4 * (i / 4); k < i; ++k) acc -= Li[k] * t[k];
+            t[i] = acc;
+        }
+#pragma unroll
+        for (int i = 0; i < CK; ++i) sT[i * LDT + j] = t[i];
+    }
+    __syncthreads();
+
+    // ---- M2 = Aqk T, in place over Aqk (wave w reads and writes only its own row tile) ----------------
+    {
+        const int mi = wave;
+        f32x4 acc[4];
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) acc[ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            if (32 * s > 16 * mi + 15) continue;  // Aqk row tile mi is zero past column 16 mi + 15
+            const int k0 = 32 * s + 8 * grp;
+            float av[8];
+            load8(&sA[(16 * mi + m) * LDT + k0], av);
+            const Split8 A = split8(av);
+#pragma unroll
+            for (int ni = 0; ni < 4; ++ni) {
+                if (ni > mi || 32 * s + 31 < 16 * ni) continue;  // T column tile ni is zero above row 16 ni
+                float tb[8];
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) tb[jj] = sT[(k0 + jj) * LDT + 16 * ni + m];
+                acc[ni] = mfma3(A, split8(tb), acc[ni]);
+            }
+        }
+#pragma unroll
+        for (int ni = 0; ni < 4; ++ni) {
+            if (ni > mi) continue;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) sA[(16 * mi + 4 * grp + i) * LDT + 16 * ni + m] = acc[ni][i];
+        }
+    }
+    __syncthreads();
+
+    // ---- [T; M2] x [beta V | beta K e^G]: U, W, the intra-chunk output and Q' --------------------------
+    {
+        const int mi = wave;
+        const int nks = (16 * mi + 15 >= 32) ? 2 : 1;  // row tile mi of T and M2 is zero past column 16 mi + 15
+        Split8 At[2], Am[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            if (s >= nks) continue;
+            float tv[8], mv[8];
+            load8(&sT[(16 * mi + m) * LDT + 32 * s + 8 * grp], tv);
+            load8(&sA[(16 * mi + m) * LDT + 32 * s + 8 * grp], mv);
+            At[s] = split8(tv);
+            Am[s] = split8(mv);
+        }
+        float* Ub = ws.U + hc * CK * DV;
+        float* Wb = ws.W + hc * CK * DK;
+        float* Qb = ws.Q + hc * CK * DK;
+        for (int ni = 0; ni < DV / 16 + DK / 16; ++ni) {
+            const bool isv = ni < DV / 16;
+            const int col = 16 * (isv ? ni : ni - DV / 16) + m;
+            f32x4 accT = {0.f, 0.f, 0.f, 0.f}, accM = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 2; ++s) {
+                if (s >= nks) continue;
+                float xb[8];
+#pragma unroll
+                for (int jj = 0; jj < 8; ++jj) {
+                    const int tk = 32 * s + 8 * grp + jj;
+                    if (isv)
+                        xb[jj] = tk < len ? a.v[((row0 + tk) * Hv + h) * DV + col] * sBeta[tk] : 0.f;
+                    else
+                        xb[jj] = sK[tk * LDK + col] * sBeta[tk] * sEG[tk];
+                }
+                const Split8 X = split8(xb);
+                accT = mfma3(At[s], X, accT);
+                accM = mfma3(Am[s], X, accM);
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int r = 16 * mi + 4 * grp + i;
+                if (isv) {
+                    Ub[r * DV + col] = accT[i];
+                    if (r < len) a.o[((row0 + r) * Hv + h) * DV + col] = accM[i];
+                } else {
+                    Wb[r * DK + col] = accT[i];
+                    Qb[r * DK + col] =
+                        r < len ? a.q[((row0 + r) * Hk + kh) * DK + col] * sRq[r] * sEG[r] - accM[i] : 0.f;
+                }
+            }
+        }
+        if (tid < CK) {
+            ws.G[hc * 2 * CK + tid] = sG[tid];
+            ws.G[hc * 2 * CK + CK + tid] = sRk[tid];
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
+// chunk_state_kernel: grid (Hv * DV / 16, B), 256 threads.  blockIdx.x = cb * Hv + h.
+// ------------------------------------------------------------------------------------------------
+template <int DK>
+struct StateOps {
+    float w[4][8];     // W  rows 16 rt + m, k-slots of this wave (see below)
+    float q[4][8];     // Q' rows 16 rt + m, same k-slots
+    float k[2][2][8];  // raw k[token 32 s + 8 grp + j][state row 32 w + 16 rt2 + m]
+    float g[2][8];     // G of those tokens
+    float rk[2][8];    // key normalisers of those tokens
+    float glast;       // G of the chunk's last token
+    float4 u;          // U[token 16 w + lane / 4][n0 + 4 (lane % 4) ..]
+    float4 o;          // intra-chunk output at the same place
+};
+
+template <int DK, int DV>
+__global__ __launch_bounds__(256) void chunk_state_kernel(DeltaArgs a, ChunkWs ws) {
+    static_assert(DK == 128 && DV == 128, "chunked path is specialised for 128-wide heads");
+    __shared__ __attribute__((aligned(16))) float red[4][2][CK][16];  // per-wave partials of W S and Q' S
+    __shared__ __attribute__((aligned(16))) float vn[CK][20];         // Vn for this column block
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int Hv = a.Hv, Hk = a.Hk, T = a.T;
+    const int h = blockIdx.x % Hv, cb = blockIdx.x / Hv, b = blockIdx.y;
+    const int kh = h / (Hv / Hk);
+    const int n0 = 16 * cb;
+    const int slot = a.slot_ids ? a.slot_ids[b] : b;
+    const int m = lane & 15, grp = lane >> 4;
+    const int NC = (T + CK - 1) / CK;
+    const int tk = 16 * wave + (lane >> 2), c4 = 4 * (lane & 3);  // Vn / output element of this lane
+
+    // This wave's state rows: tile 0 = rows 32 w + 4 grp + i, tile 1 = rows 32 w + 16 + 4 grp + i
+    // (i = 0..3), column n0 + m -- the C layout of the 16x16 MFMA, so the update accumulates in place.
+    // As the B operand of W S, k-slot j of lane (m, grp) is state row 32 w + 16 (j / 4) + 4 grp + j % 4:
+    // exactly the rows the lane holds, so W is read with the same k-slot order.
+    float* S = a.state + ((size_t)slot * Hv + h) * DK * DV;
+    f32x4 s0, s1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        s0[i] = S[(size_t)(32 * wave + 4 * grp + i) * DV + n0 + m];
+        s1[i] = S[(size_t)(32 * wave + 16 + 4 * grp + i) * DV + n0 + m];
+    }
+
+    auto load_ops = [&](int c, StateOps<DK>& op) {
+        const size_t hc = ((size_t)b * Hv + h) * ws.NC + c;
+        const int t0 = c * CK, len = min(CK, T - t0);
+        const size_t row0 = (size_t)b * T + t0;
+        const float* Wb = ws.W + hc * CK * DK;
+        const float* Qb = ws.Q + hc * CK * DK;
+        const float* Gb = ws.G + hc * 2 * CK;
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+            const size_t base = (size_t)(16 * rt + m) * DK + 32 * wave + 4 * grp;
+            const float4 w0 = *reinterpret_cast<const float4*>(Wb + base);
+            const float4 w1 = *reinterpret_cast<const float4*>(Wb + base + 16);
+            const float4 q0 = *reinterpret_cast<const float4*>(Qb + base);
+            const float4 q1 = *reinterpret_cast<const float4*>(Qb + base + 16);
+            op.w[rt][0] = w0.x, op.w[rt][1] = w0.y, op.w[rt][2] = w0.z, op.w[rt][3] = w0.w;
+            op.w[rt][4] = w1.x, op.w[rt][5] = w1.y, op.w[rt][6] = w1.z, op.w[rt][7] = w1.w;
+            op.q[rt][0] = q0.x, op.q[rt][1] = q0.y, op.q[rt][2] = q0.z, op.q[rt][3] = q0.w;
+            op.q[rt][4] = q1.x, op.q[rt][5] = q1.y, op.q[rt][6] = q1.z, op.q[rt][7] = q1.w;
+        }
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            load8(Gb + 32 * s + 8 * grp, op.g[s]);
+            load8(Gb + CK + 32 * s + 8 * grp, op.rk[s]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int tok = 32 * s + 8 * grp + j;
+#pragma unroll
+                for (int rt2 = 0; rt2 < 2; ++rt2)
+                    op.k[rt2][s][j] =
+                        tok < len ? a.k[((row0 + tok) * Hk + kh) * DK + 32 * wave + 16 * rt2 + m] : 0.f;
+            }
+        }
+        op.glast = Gb[CK - 1];
+        op.u = *reinterpret_cast<const float4*>(ws.U + hc * CK * DV + (size_t)tk * DV + n0 + c4);
+        op.o = tk < len ? *reinterpret_cast<const float4*>(a.o + ((row0 + tk) * Hv + h) * DV + n0 + c4)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+
+    StateOps<DK> cur, nxt;
+    load_ops(0, cur);
+    for (int c = 0; c < NC; ++c) {
+        if (c + 1 < NC) load_ops(c + 1, nxt);
+        const int t0 = c * CK, len = min(CK, T - t0);
+        const size_t row0 = (size_t)b * T + t0;
+
+        // W S and Q' S over this wave's 32 state rows
+        float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+        const Split8 Sb = split8(sv);
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+            const f32x4 pw = mfma3(split8(cur.w[rt]), Sb, z);
+            const f32x4 pq = mfma3(split8(cur.q[rt]), Sb, z);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                red[wave][0][16 * rt + 4 * grp + i][m] = pw[i];
+                red[wave][1][16 * rt + 4 * grp + i][m] = pq[i];
+            }
+        }
+        lds_barrier();
+
+        // Vn = U - W S and O += Q' S for token tk, columns c4..c4+3
+        {
+            float4 sw = make_float4(0.f, 0.f, 0.f, 0.f), sq = sw;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const float4 x = *reinterpret_cast<const float4*>(&red[w][0][tk][c4]);
+                const float4 y = *reinterpret_cast<const float4*>(&red[w][1][tk][c4]);
+                sw.x += x.x, sw.y += x.y, sw.z += x.z, sw.w += x.w;
+                sq.x += y.x, sq.y += y.y, sq.z += y.z, sq.w += y.w;
+            }
+            *reinterpret_cast<float4*>(&vn[tk][c4]) =
+                make_float4(cur.u.x - sw.x, cur.u.y - sw.y, cur.u.z - sw.z, cur.u.w - sw.w);
+            if (tk < len)
+                *reinterpret_cast<float4*>(a.o + ((row0 + tk) * Hv + h) * DV + n0 + c4) =
+                    make_float4(cur.o.x + sq.x, cur.o.y + sq.y, cur.o.z + sq.z, cur.o.w + sq.w);
+        }
+        lds_barrier();
+
+        // S <- e^{G_last} S + (K e^{G_last - G})^T Vn
+        const float egl = __expf(cur.glast);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s0[i] *= egl, s1[i] *= egl;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            float vb[8], kd[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                vb[j] = vn[32 * s + 8 * grp + j][m];
+                kd[j] = cur.rk[s][j] * __expf(cur.glast - cur.g[s][j]);
+            }
+            const Split8 Vb = split8(vb);
+            float k0[8], k1[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) k0[j] = cur.k[0][s][j] * kd[j], k1[j] = cur.k[1][s][j] * kd[j];
+            s0 = mfma3(split8(k0), Vb, s0);
+            s1 = mfma3(split8(k1), Vb, s1);
+        }
+        cur = nxt;
+    }
+
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        S[(size_t)(32 * wave + 4 * grp + i) * DV + n0 + m] = s0[i];
+        S[(size_t)(32 * wave + 16 + 4 * grp + i) * DV + n0 + m] = s1[i];
+    }
+}
+
+}  // namespace
+
+size_t delta_chunked_workspace(int B, int T, int Hv, int dk, int dv) {
+    const size_t NC = (size_t)(T + CK - 1) / CK;
+    return (size_t)B * Hv * NC * ((size_t)CK * dk * 2 + (size_t)CK * dv + 2 * CK) * sizeof(float);
+}
+
+bool delta_chunked_supported(int dk, int dv) { return dk == 128 && dv == 128; }
+
+hipError_t launch_delta_chunked(const DeltaArgs& a, int dk, int dv, void* workspace, size_t ws_bytes,
+                                hipStream_t stream) {
+    if (!delta_chunked_supported(dk, dv)) return hipErrorInvalidValue;
+    if (a.B <= 0 || a.T <= 0) return hipSuccess;
+    if (!workspace || ws_bytes < delta_chunked_workspace(a.B, a.T, a.Hv, dk, dv)) return hipErrorInvalidValue;
+    ChunkWs ws;
+    ws.NC = (a.T + CK - 1) / CK;
+    const size_t n = (size_t)a.B * a.Hv * ws.NC;
+    float* p = static_cast<float*>(workspace);
+    ws.W = p, p += n * CK * dk;
+    ws.Q = p, p += n * CK * dk;
+    ws.U = p, p += n * CK * dv;
+    ws.G = p;
+    hipLaunchKernelGGL((chunk_prep_kernel<128, 128>), dim3(ws.NC, a.Hv, a.B), dim3(256), 0, stream, a, ws);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((chunk_state_kernel<128, 128>), dim3(a.Hv * (128 / 16), a.B), dim3(256), 0, stream, a, ws);
+    return hipGetLastError();
+}
+
+}  // namespace gdn

@@ -41,6 +41,44 @@ __device__ __forceinline__ float lane_group_sum(float x) {
     return x;
 }
 
+// ---- MFMA (gfx950 bf16) -----------------------------------------------------------------------
+// v_mfma_f32_16x16x32_bf16: lane l holds A[l % 16][8 (l / 16) + j] and B[8 (l / 16) + j][l % 16],
+// j = 0..7; C element i of lane l is C[4 (l / 16) + i][l % 16].
+__device__ __forceinline__ f32x4 mfma16(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+// v_mfma_f32_32x32x16_bf16: lane l holds A[l % 32][8 (l / 32) + j]; C element e of lane l is
+// C[8 (e / 4) + 4 (l / 32) + e % 4][l % 32].
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// fp32 operands on bf16 MFMA at ~fp32 accuracy: x = hi + lo with hi = bf16(x), lo = bf16(x - hi)
+// (relative error ~2^-17), and a.b ~= a_hi.b_hi + a_hi.b_lo + a_lo.b_hi (the lo.lo term is below
+// fp32 rounding).  The small terms are accumulated first.
+struct Split8 {
+    bf16x8 h, l;
+};
+__device__ __forceinline__ Split8 split8(const float* v) {
+    Split8 s;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const __bf16 hi = (__bf16)v[j];
+        s.h[j] = hi;
+        s.l[j] = (__bf16)(v[j] - (float)hi);
+    }
+    return s;
+}
+__device__ __forceinline__ f32x4 mfma3(const Split8& a, const Split8& b, f32x4 c) {
+    c = mfma16(a.l, b.h, c);
+    c = mfma16(a.h, b.l, c);
+    return mfma16(a.h, b.h, c);
+}
+
+// Workgroup barrier for LDS traffic only: unlike __syncthreads() it does not wait for outstanding
+// global loads, so loads issued for the next step stay in flight across it.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
 __device__ __forceinline__ float siluf_(float x) { return x / (1.0f + __expf(-x)); }
 // torch.nn.functional.softplus with beta = 1, threshold = 20
@@ -115,9 +153,11 @@ struct DeltaArgs {
     float scale;           // q scale applied in the kernel (1 when q is pre-scaled)
 };
 hipError_t launch_delta_seq(const DeltaArgs& a, int dk, int dv, hipStream_t stream);
+// Chunk-64 form for long prefills (dk == dv == 128); `workspace` of delta_chunked_workspace() bytes.
 hipError_t launch_delta_chunked(const DeltaArgs& a, int dk, int dv, void* workspace, size_t ws_bytes,
                                 hipStream_t stream);
 size_t delta_chunked_workspace(int B, int T, int Hv, int dk, int dv);
+bool delta_chunked_supported(int dk, int dv);
 
 // y = o * rsqrt(mean(o^2) + eps) * w * silu(z), per head of dv; y bf16.
 hipError_t launch_gated_rmsnorm(const float* o, int M, int nv, int dv, const float* z, int z_stride,
