@@ -6,6 +6,7 @@
 // tokens with the states carried across, like the reference's 128-row launches (gdn_layer.py:282-292).
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -52,8 +53,8 @@ struct gdn_layer {
     int max_slots = 0, max_tokens = 0;
     std::vector<void*> allocs;
 
-    u16* w_in = nullptr;      // [NP, H]  rows q | k | v | z | a | b
-    u16* w_out = nullptr;     // [H, Vd]
+    u16* w_in = nullptr;      // [NP, H]  rows q | k | v | z | a | b, W_FRAG layout
+    u16* w_out = nullptr;     // [H, Vd] W_FRAG layout
     float4* conv_w = nullptr; // [CD] taps
     float* neg_A = nullptr;   // [nv]
     float* dt_bias = nullptr; // [nv]
@@ -64,6 +65,7 @@ struct gdn_layer {
 
     // workspace, sized for max_tokens rows
     u16* x_ws = nullptr;      // [max_tokens, H] gathered input rows when a launch is split
+    u16* x_frag = nullptr;    // [64, H] decode input in W_FRAG layout
     u16* out_ws = nullptr;    // [max_tokens, H]
     float* P = nullptr;       // [max_tokens, NP]
     float* qn = nullptr;      // [max_tokens, Kd]
@@ -138,7 +140,12 @@ int run_chunk(gdn_layer* L, const u16* x, int B, int T, const int* slot_ids, u16
     const int M = B * T;
     hipEvent_t ev[4] = {L->prof_event(0), L->prof_event(1), L->prof_event(2), L->prof_event(3)};
     if (ev[0]) HIP_OK(hipEventRecord(ev[0], st));
-    HIP_OK(gdn::launch_linear(x, L->w_in, M, L->NP, d.hidden, L->P, gdn::OUT_F32, st));
+    // decode-sized launches stream the weights against fragment-tiled activations
+    const bool frag = M <= 64;
+    const bool y_frag = frag && T <= kFusedMaxT;  // the fused mixer writes y straight into W_FRAG layout
+    if (frag) HIP_OK(gdn::launch_frag_tile(x, M, d.hidden, L->x_frag, st));
+    HIP_OK(gdn::launch_linear(frag ? L->x_frag : x, frag ? gdn::W_FRAG : gdn::W_ROW, L->w_in, gdn::W_FRAG, M, L->NP,
+                              d.hidden, L->P, gdn::OUT_F32, st));
     if (ev[1]) HIP_OK(hipEventRecord(ev[1], st));
     if (T <= kFusedMaxT) {
         gdn::MixerArgs a{};
@@ -147,7 +154,7 @@ int run_chunk(gdn_layer* L, const u16* x, int B, int T, const int* slot_ids, u16
         a.conv_w = L->conv_w, a.neg_A = L->neg_A, a.dt_bias = L->dt_bias, a.norm_w = L->norm_w;
         a.eps = d.rms_norm_eps;
         a.rec_state = L->rec, a.conv_state = L->conv, a.ring_pos = L->ring_pos;
-        a.y = L->y, a.o_tap = nullptr;
+        a.y = L->y, a.y_frag = y_frag ? 1 : 0, a.o_tap = nullptr;
         HIP_OK(gdn::launch_mixer(a, d.head_k_dim, d.head_v_dim, st));
     } else {
         gdn::FrontArgs f{};
@@ -168,7 +175,8 @@ int run_chunk(gdn_layer* L, const u16* x, int B, int T, const int* slot_ids, u16
                                          d.rms_norm_eps, L->y, st));
     }
     if (ev[2]) HIP_OK(hipEventRecord(ev[2], st));
-    HIP_OK(gdn::launch_linear(L->y, L->w_out, M, d.hidden, L->Vd, out, gdn::OUT_BF16, st));
+    HIP_OK(gdn::launch_linear(L->y, y_frag ? gdn::W_FRAG : gdn::W_ROW, L->w_out, gdn::W_FRAG, M, d.hidden, L->Vd, out,
+                              gdn::OUT_BF16, st));
     if (ev[3]) {
         HIP_OK(hipEventRecord(ev[3], st));
         ++L->prof_calls;
@@ -207,8 +215,8 @@ int gdn_layer_create(const gdn_dims* dims, const gdn_weights* w, int max_slots, 
     auto take = [&](hipError_t r) {
         if (e == hipSuccess) e = r;
     };
-    take(L->alloc(&L->w_in, (size_t)L->NP * H));
-    take(L->alloc(&L->w_out, (size_t)H * L->Vd));
+    take(L->alloc(&L->w_in, gdn::frag_elems(L->NP, H)));
+    take(L->alloc(&L->w_out, gdn::frag_elems(H, L->Vd)));
     take(L->alloc(&L->conv_w, (size_t)L->CD));
     take(L->alloc(&L->neg_A, (size_t)nv));
     take(L->alloc(&L->dt_bias, (size_t)nv));
@@ -217,6 +225,7 @@ int gdn_layer_create(const gdn_dims* dims, const gdn_weights* w, int max_slots, 
     take(L->alloc(&L->conv, (size_t)max_slots * nv * 3 * L->CH));
     take(L->alloc(&L->ring_pos, (size_t)max_slots * nv));
     take(L->alloc(&L->x_ws, MT * H));
+    take(L->alloc(&L->x_frag, gdn::frag_elems(64, H)));
     take(L->alloc(&L->out_ws, MT * H));
     take(L->alloc(&L->P, MT * L->NP));
     take(L->alloc(&L->qn, MT * L->Kd));
@@ -225,7 +234,7 @@ int gdn_layer_create(const gdn_dims* dims, const gdn_weights* w, int max_slots, 
     take(L->alloc(&L->g, MT * nv));
     take(L->alloc(&L->beta, MT * nv));
     take(L->alloc(&L->o, MT * L->Vd));
-    take(L->alloc(&L->y, MT * L->Vd));
+    take(L->alloc(&L->y, std::max(MT * L->Vd, gdn::frag_elems(64, L->Vd))));  // W_FRAG y pads rows to 16
     if (max_tokens > kFusedMaxT && gdn::delta_chunked_supported(dk, dv)) {
         // chunked-prefill workspace for the worst launch: B sequences of T > kFusedMaxT tokens with
         // B * T <= max_tokens hold at most max_tokens / 64 + max_tokens / 65 + 1 chunks
@@ -241,15 +250,21 @@ int gdn_layer_create(const gdn_dims* dims, const gdn_weights* w, int max_slots, 
                     hipGetErrorString(e));
     }
 
-    // fused in_proj rows: q | k | v (in_proj_qkv), z, a, b -- one weight stream per token
+    // fused in_proj rows: q | k | v (in_proj_qkv), z, a, b -- one weight stream per token.  The HF
+    // row-major weights are staged in a temporary device buffer and re-laid out into fragment blocks.
     const size_t row = (size_t)H * sizeof(u16);
-    e = hipMemcpy(L->w_in, w->in_proj_qkv, L->CD * row, hipMemcpyDefault);
-    if (e == hipSuccess) e = hipMemcpy(L->w_in + (size_t)L->CD * H, w->in_proj_z, L->Vd * row, hipMemcpyDefault);
+    u16* stage = nullptr;
+    e = hipMalloc(&stage, std::max((size_t)L->NP * H, (size_t)H * L->Vd) * sizeof(u16));
+    if (e == hipSuccess) e = hipMemcpy(stage, w->in_proj_qkv, L->CD * row, hipMemcpyDefault);
+    if (e == hipSuccess) e = hipMemcpy(stage + (size_t)L->CD * H, w->in_proj_z, L->Vd * row, hipMemcpyDefault);
+    if (e == hipSuccess) e = hipMemcpy(stage + (size_t)(L->CD + L->Vd) * H, w->in_proj_a, nv * row, hipMemcpyDefault);
     if (e == hipSuccess)
-        e = hipMemcpy(L->w_in + (size_t)(L->CD + L->Vd) * H, w->in_proj_a, nv * row, hipMemcpyDefault);
-    if (e == hipSuccess)
-        e = hipMemcpy(L->w_in + (size_t)(L->CD + L->Vd + nv) * H, w->in_proj_b, nv * row, hipMemcpyDefault);
-    if (e == hipSuccess) e = hipMemcpy(L->w_out, w->out_proj, (size_t)H * L->Vd * sizeof(u16), hipMemcpyDefault);
+        e = hipMemcpy(stage + (size_t)(L->CD + L->Vd + nv) * H, w->in_proj_b, nv * row, hipMemcpyDefault);
+    if (e == hipSuccess) e = gdn::launch_frag_tile(stage, L->NP, H, L->w_in, nullptr);
+    if (e == hipSuccess) e = hipMemcpy(stage, w->out_proj, (size_t)H * L->Vd * sizeof(u16), hipMemcpyDefault);
+    if (e == hipSuccess) e = gdn::launch_frag_tile(stage, H, L->Vd, L->w_out, nullptr);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (stage) (void)hipFree(stage);
     if (e == hipSuccess) e = hipMemcpy(L->conv_w, w->conv1d, (size_t)L->CD * 4 * sizeof(float), hipMemcpyDefault);
     std::vector<float> host(nv);
     if (e == hipSuccess) e = hipMemcpy(host.data(), w->A_log, nv * sizeof(float), hipMemcpyDefault);
@@ -374,7 +389,8 @@ int gdn_layer_proj_width(const gdn_layer* L) { return L ? L->NP : fail(GDN_ERR_I
 int gdn_in_proj(gdn_layer* L, const void* x, int M, float* P, void* stream) {
     if (!L || !x || !P) return fail(GDN_ERR_INVALID_ARG, "gdn_in_proj: NULL argument");
     if (M <= 0) return fail(GDN_ERR_SHAPE, "M=%d", M);
-    HIP_OK(gdn::launch_linear(x, L->w_in, M, L->NP, L->d.hidden, P, gdn::OUT_F32, as_stream(stream)));
+    HIP_OK(gdn::launch_linear(x, gdn::W_ROW, L->w_in, gdn::W_FRAG, M, L->NP, L->d.hidden, P, gdn::OUT_F32,
+                              as_stream(stream)));
     return GDN_OK;
 }
 
@@ -423,7 +439,8 @@ int gdn_gated_rmsnorm(gdn_layer* L, const float* o, const float* z, int z_stride
 int gdn_out_proj(gdn_layer* L, const void* y, int M, void* out, void* stream) {
     if (!L || !y || !out) return fail(GDN_ERR_INVALID_ARG, "gdn_out_proj: NULL argument");
     if (M <= 0) return fail(GDN_ERR_SHAPE, "M=%d", M);
-    HIP_OK(gdn::launch_linear(y, L->w_out, M, L->d.hidden, L->Vd, out, gdn::OUT_BF16, as_stream(stream)));
+    HIP_OK(gdn::launch_linear(y, gdn::W_ROW, L->w_out, gdn::W_FRAG, M, L->d.hidden, L->Vd, out, gdn::OUT_BF16,
+                              as_stream(stream)));
     return GDN_OK;
 }
 
@@ -448,7 +465,8 @@ int gdn_linear_bf16(const void* x, const void* w, int M, int N, int K, void* y, 
     if (!x || !w || !y) return fail(GDN_ERR_INVALID_ARG, "gdn_linear_bf16: NULL argument");
     if (M <= 0 || N <= 0 || K <= 0) return fail(GDN_ERR_SHAPE, "M=%d N=%d K=%d", M, N, K);
     if (K % 128) return fail(GDN_ERR_UNSUPPORTED, "K=%d is not a multiple of 128", K);
-    HIP_OK(gdn::launch_linear(x, w, M, N, K, y, out_fp32 ? gdn::OUT_F32 : gdn::OUT_BF16, as_stream(stream)));
+    HIP_OK(gdn::launch_linear(x, gdn::W_ROW, w, gdn::W_ROW, M, N, K, y, out_fp32 ? gdn::OUT_F32 : gdn::OUT_BF16,
+                              as_stream(stream)));
     return GDN_OK;
 }
 

@@ -92,10 +92,21 @@ __device__ __forceinline__ float softplusf_(float x) { return x > 20.0f ? x : lo
 namespace gdn {
 
 enum OutKind { OUT_F32 = 0, OUT_BF16 = 1 };
+// Weight layouts: W_ROW = row-major [N, K]; W_FRAG = MFMA-fragment blocks (see gdn_linear.hip).
+enum WLayout { W_ROW = 0, W_FRAG = 1 };
 
-// y[M, N] = x[M, K] . w[N, K]^T ; bf16 inputs, fp32 accumulation; K % 128 == 0.
-hipError_t launch_linear(const void* x, const void* w, int M, int N, int K, void* y, int out_kind,
-                         hipStream_t stream);
+// y[M, N] = x[M, K] . w[N, K]^T ; bf16 inputs, fp32 accumulation; K % 128 == 0.  w in layout `wlayout`;
+// x in `xlayout` (W_FRAG activations only for M <= 64).
+hipError_t launch_linear(const void* x, int xlayout, const void* w, int wlayout, int M, int N, int K, void* y,
+                         int out_kind, hipStream_t stream);
+// Elements of an [N, K] matrix in W_FRAG layout (rows padded to a multiple of 16).
+size_t frag_elems(int N, int K);
+// Convert a row-major device matrix [N, K] into W_FRAG layout (frag_elems(N, K) elements).
+hipError_t launch_frag_tile(const void* w, int N, int K, void* wf, hipStream_t stream);
+// Element offset of (row n, column k) of an [N, K] matrix in W_FRAG layout.
+__host__ __device__ __forceinline__ size_t frag_offset(int n, int k, int K) {
+    return ((size_t)(n >> 4) * (K >> 5) + (k >> 5)) * 512 + ((((k >> 3) & 3) << 4) + (n & 15)) * 8 + (k & 7);
+}
 
 struct MixerArgs {
     const float* P;         // [M, NP] fused projection rows (q | k | v | z | a | b)
@@ -112,6 +123,7 @@ struct MixerArgs {
     float* conv_state;      // [slots, nv, 3, 2dk + dv] ring, per v-head copy
     int* ring_pos;          // [slots, nv]
     u16* y;                 // [M, nv * dv] bf16 gated RMSNorm output
+    int y_frag;             // 1: y in W_FRAG layout (rows padded to 16; M <= 64), 0: row-major
     float* o_tap;           // optional [M, nv * dv] recurrence output (nullptr: not written)
 };
 hipError_t launch_mixer(const MixerArgs& a, int dk, int dv, hipStream_t stream);

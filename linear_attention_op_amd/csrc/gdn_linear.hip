@@ -2,17 +2,25 @@
 // Replaces the ttnn.linear call sites of the reference layer (wormhole_n150/qwen3.5_9B/gdn_layer.py:255-259
 // in_proj and a/b projection, :272-276 out_proj).
 //
-// Two kernels, both on bf16 MFMA with fp32 accumulation:
-//  * linear_skinny_kernel (M <= 64, decode): HBM-bound weight streaming.  A workgroup owns NTS*16 rows
-//    of w and all M rows of x; its NW waves split K, so every weight byte is read exactly once and
-//    in flight from many waves at a time.  The wave partials are summed through LDS.  Both operands of
-//    v_mfma_f32_16x16x32_bf16 are loaded straight from global memory: a lane holds 8 consecutive k of
-//    one row, and since the MFMA sums over k, any k order shared by A and B gives the same dot product.
-//  * linear_tiled_kernel (M > 64, prefill): 128x128x64 LDS-tiled GEMM on v_mfma_f32_32x32x16_bf16,
-//    four waves in a 2x2 grid of 64x64 warp tiles, register-staged double buffering.
+// Weight layouts.  W_ROW is the HF row-major [N, K].  W_FRAG is the layout the layer keeps its weights in:
+// [ceil(N/16)][K/32] blocks of 512 bf16, block (nt, kq) holding for lane l = 16 g + r the 8 values
+// W[16 nt + r][32 kq + 8 g + j] at offset 8 l + j -- exactly the A operand of v_mfma_f32_16x16x32_bf16,
+// so one fragment load is 1 KB of contiguous memory and a wave streams its rows sequentially.
+//
+// Kernels (bf16 MFMA, fp32 accumulation):
+//  * gemv_kernel (M <= 64, decode): HBM-bound weight streaming.  A workgroup owns 16 NTS rows of w; its
+//    NW waves split K, each streaming W and x fragments through a register ring PD k-steps deep (no
+//    barriers in the loop), then the partials are summed through LDS and written once, coalesced.
+//    Activations may come in the same fragment layout (rows padded to 16 with zeros), which turns
+//    every x load into 1 KB of contiguous memory as well.
+//  * gemm_kernel (M > 64, prefill): 128x128x64 LDS-tiled GEMM on v_mfma_f32_32x32x16_bf16, 4 waves of
+//    64x64, register-staged double buffering; tiles are rasterised per XCD in groups of 8 M-tiles so that
+//    workgroups running together on one XCD share A and B tiles in its L2.
 #include "gdn_common.h"
 
 namespace gdn {
+
+namespace {
 
 template <int OUT>
 __device__ __forceinline__ void store_out(void* y, size_t idx, float v) {
@@ -23,108 +31,128 @@ __device__ __forceinline__ void store_out(void* y, size_t idx, float v) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// Skinny: M <= MT * 16 <= 64
+// Layout conversion W_ROW -> W_FRAG (rows past N are zero).  One 16-byte piece per thread.
 // ------------------------------------------------------------------------------------------------
-template <int NTS, int MT, int NW, int OUT>
-__global__ __launch_bounds__(NW * 64) void linear_skinny_kernel(const u16* __restrict__ x, const u16* __restrict__ w,
-                                                                int M, int N, int K, void* __restrict__ y) {
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int n0 = blockIdx.x * (NTS * 16);
-    const int kw = K / NW;
-    const int kbeg = wave * kw;
-    const int r = lane & 15;
-    const int g = lane >> 4;
+__global__ void frag_tile_kernel(const u16* __restrict__ w, int N, int K, u16* __restrict__ wf) {
+    const size_t e = (size_t)blockIdx.x * 256 + threadIdx.x;
+    const size_t pieces = (size_t)((N + 15) / 16) * (K / 32) * 64;
+    if (e >= pieces) return;
+    const int l = (int)(e % 64);
+    const size_t blk = e / 64;
+    const int kq = (int)(blk % (K / 32)), nt = (int)(blk / (K / 32));
+    const int n = 16 * nt + (l & 15), k = 32 * kq + 8 * (l >> 4);
+    u16x8 v = {};
+    if (n < N) v = *reinterpret_cast<const u16x8*>(w + (size_t)n * K + k);
+    *reinterpret_cast<u16x8*>(wf + e * 8) = v;
+}
 
+// ------------------------------------------------------------------------------------------------
+// GEMV: M <= 16 MT
+// ------------------------------------------------------------------------------------------------
+template <int NTS, int MT, int NW, int PD, int OUT, int WL, int XL>
+__global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x, const u16* __restrict__ w, int M,
+                                                      int N, int K, void* __restrict__ y) {
+    constexpr int BN = NTS * 16, BM = MT * 16;
+    __shared__ float red[NW][BM][BN + 1];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int KQ = K >> 5;
+    const int kq_per = (KQ + NW - 1) / NW;
+    const int kq0 = min(KQ, wave * kq_per);
+    const int nsteps = min(KQ, kq0 + kq_per) - kq0;
+    const int n0 = blockIdx.x * BN;
+    const int NT = (N + 15) >> 4;
+
+    // fragment base pointers and per-k-step strides
     const u16* wp[NTS];
 #pragma unroll
-    for (int nt = 0; nt < NTS; ++nt) {
-        const int n = min(n0 + nt * 16 + r, N - 1);
-        wp[nt] = w + (size_t)n * K + kbeg + 8 * g;
+    for (int t = 0; t < NTS; ++t) {
+        if (WL == W_FRAG)
+            wp[t] = w + ((size_t)min((n0 >> 4) + t, NT - 1) * KQ + kq0) * 512 + lane * 8;
+        else
+            wp[t] = w + (size_t)min(n0 + 16 * t + r, N - 1) * K + 32 * kq0 + 8 * g;
     }
+    constexpr size_t WSTEP = WL == W_FRAG ? 512 : 32;
+    // x: row-major rows (zero past M), or fragment blocks (rows past M stored as zeros)
     const u16* xp[MT];
     bool xv[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-        const int m = mt * 16 + r;
-        xv[mt] = m < M;
-        xp[mt] = x + (size_t)min(m, M - 1) * K + kbeg + 8 * g;
+        if (XL == W_FRAG) {
+            xv[mt] = true;
+            xp[mt] = x + ((size_t)mt * KQ + kq0) * 512 + lane * 8;
+        } else {
+            xv[mt] = 16 * mt + r < M;
+            xp[mt] = x + (size_t)min(16 * mt + r, M - 1) * K + 32 * kq0 + 8 * g;
+        }
     }
+    constexpr size_t XSTEP = XL == W_FRAG ? 512 : 32;
 
+    bf16x8 wb[PD][NTS], xb[PD][MT];
+    const bf16x8 zero8 = {};
+#pragma unroll
+    for (int j = 0; j < PD; ++j) {
+        if (j < nsteps) {
+#pragma unroll
+            for (int t = 0; t < NTS; ++t) wb[j][t] = *reinterpret_cast<const bf16x8*>(wp[t] + j * WSTEP);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) xb[j][mt] = xv[mt] ? *reinterpret_cast<const bf16x8*>(xp[mt] + j * XSTEP) : zero8;
+        }
+    }
     f32x4 acc[NTS][MT];
 #pragma unroll
-    for (int nt = 0; nt < NTS; ++nt)
+    for (int t = 0; t < NTS; ++t)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const bf16x8 zero8 = {};
-    // main loop: 4 k-steps of 32 per iteration, all loads issued before the MFMAs that consume them
-    constexpr int U = 4;
-    int k = 0;
-    for (; k + 32 * U <= kw; k += 32 * U) {
-        bf16x8 a[U][NTS], b[U][MT];
+    for (int s0 = 0; s0 < nsteps; s0 += PD) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
+        for (int j = 0; j < PD; ++j) {
+            const int s = s0 + j;
+            if (s < nsteps) {
 #pragma unroll
-            for (int nt = 0; nt < NTS; ++nt) a[u][nt] = *reinterpret_cast<const bf16x8*>(wp[nt] + k + 32 * u);
+                for (int t = 0; t < NTS; ++t)
 #pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-                b[u][mt] = xv[mt] ? *reinterpret_cast<const bf16x8*>(xp[mt] + k + 32 * u) : zero8;
+                    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = mfma16(wb[j][t], xb[j][mt], acc[t][mt]);
+                if (s + PD < nsteps) {
+#pragma unroll
+                    for (int t = 0; t < NTS; ++t)
+                        wb[j][t] = *reinterpret_cast<const bf16x8*>(wp[t] + (size_t)(s + PD) * WSTEP);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt)
+                        xb[j][mt] = xv[mt] ? *reinterpret_cast<const bf16x8*>(xp[mt] + (size_t)(s + PD) * XSTEP) : zero8;
+                }
+            }
         }
-#pragma unroll
-        for (int u = 0; u < U; ++u)
-#pragma unroll
-            for (int nt = 0; nt < NTS; ++nt)
-#pragma unroll
-                for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = mfma16(a[u][nt], b[u][mt], acc[nt][mt]);
-    }
-    for (; k < kw; k += 32) {
-        bf16x8 a[NTS], b[MT];
-#pragma unroll
-        for (int nt = 0; nt < NTS; ++nt) a[nt] = *reinterpret_cast<const bf16x8*>(wp[nt] + k);
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt) b[mt] = xv[mt] ? *reinterpret_cast<const bf16x8*>(xp[mt] + k) : zero8;
-#pragma unroll
-        for (int nt = 0; nt < NTS; ++nt)
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = mfma16(a[nt], b[mt], acc[nt][mt]);
     }
 
-    // C layout of 16x16 MFMA: lane l, element i -> row (of w) 4*(l/16) + i, column (of x) l % 16.
-    constexpr int PER_WAVE = NTS * MT * 4 * 64;
-    __shared__ float red[NW * PER_WAVE];
+    // C element i of lane (r, g) in acc[t][mt]: w row n0 + 16 t + 4 g + i, x row 16 mt + r
 #pragma unroll
-    for (int nt = 0; nt < NTS; ++nt)
+    for (int t = 0; t < NTS; ++t)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) red[wave * PER_WAVE + ((nt * MT + mt) * 4 + i) * 64 + lane] = acc[nt][mt][i];
+            for (int i = 0; i < 4; ++i) red[wave][16 * mt + r][16 * t + 4 * g + i] = acc[t][mt][i];
     __syncthreads();
-
-    // one output per (m, n_local); n_local fastest so the stores to y rows are contiguous
-    constexpr int NL = NTS * 16;
-    for (int idx = threadIdx.x; idx < MT * 16 * NL; idx += NW * 64) {
-        const int nl = idx % NL;
-        const int m = idx / NL;
-        const int n = n0 + nl;
+    for (int e = threadIdx.x; e < BM * BN; e += NW * 64) {
+        const int m = e / BN, nl = e % BN, n = n0 + nl;
         if (m >= M || n >= N) continue;
-        const int nt = nl >> 4, nn = nl & 15;
-        const int src = ((nt * MT + (m >> 4)) * 4 + (nn & 3)) * 64 + (m & 15) + 16 * (nn >> 2);
         float s = 0.f;
 #pragma unroll
-        for (int wv = 0; wv < NW; ++wv) s += red[wv * PER_WAVE + src];
+        for (int wv = 0; wv < NW; ++wv) s += red[wv][m][nl];
         store_out<OUT>(y, (size_t)m * N + n, s);
     }
 }
 
 // ------------------------------------------------------------------------------------------------
-// Tiled: 128 x 128 x 64 block tile, 4 waves (2 x 2), 32x32x16 MFMA
+// GEMM: 128 x 128 x 64 block tile, 4 waves (2 x 2), 32x32x16 MFMA
 // ------------------------------------------------------------------------------------------------
-constexpr int TBM = 128, TBN = 128, TBK = 64, TPAD = 8, TLD = TBK + TPAD;
+constexpr int TBM = 128, TBN = 128, TBK = 64, TPAD = 8, TLD = TBK + TPAD, GROUP_M = 8;
 
-template <int OUT>
-__global__ __launch_bounds__(256) void linear_tiled_kernel(const u16* __restrict__ x, const u16* __restrict__ w,
-                                                           int M, int N, int K, void* __restrict__ y) {
+template <int OUT, int WL>
+__global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, const u16* __restrict__ w, int M, int N,
+                                                   int K, void* __restrict__ y) {
     __shared__ __attribute__((aligned(16))) u16 As[2][TBM * TLD];
     __shared__ __attribute__((aligned(16))) u16 Bs[2][TBN * TLD];
 
@@ -133,25 +161,43 @@ __global__ __launch_bounds__(256) void linear_tiled_kernel(const u16* __restrict
     const int wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
 
-    // Map workgroups to tiles so that consecutive workgroups (which the dispatcher spreads over the
-    // 8 XCDs round-robin) walk N fastest inside a band of M tiles.
-    const int tiles_n = (N + TBN - 1) / TBN;
-    const int tm = blockIdx.x / tiles_n, tn = blockIdx.x % tiles_n;
+    // Tile order.  The dispatcher hands workgroup ids to the 8 XCDs round-robin; give XCD x the
+    // contiguous tile range [x per, (x + 1) per) and walk it in groups of GROUP_M M-tiles (M fastest),
+    // so the workgroups in flight on one XCD cover a compact block of tiles and share its L2.
+    const int TM = (M + TBM - 1) / TBM, TN = (N + TBN - 1) / TBN, total = TM * TN;
+    const int id = blockIdx.x, per = total / 8;
+    const int t = id < 8 * per ? (id % 8) * per + id / 8 : id;
+    const int gsz = GROUP_M * TN;
+    const int first_m = (t / gsz) * GROUP_M;
+    const int gm = min(TM - first_m, GROUP_M);
+    const int tm = first_m + (t % gsz) % gm, tn = (t % gsz) / gm;
     const int m0 = tm * TBM, n0 = tn * TBN;
 
-    // global -> register staging: 1024 16-byte chunks per operand tile, 4 per thread
+    // global -> register staging: 1024 16-byte pieces per operand tile, 4 per thread
     u16x8 ra[4], rb[4];
     const u16* ag[4];
     const u16* bg[4];
-    int soff[4];
+    int soffa[4], soffb[4];
+    const int NT = (N + 15) >> 4;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int c = tid + 256 * j;
         const int row = c >> 3, col = (c & 7) * 8;
         ag[j] = x + (size_t)min(m0 + row, M - 1) * K + col;
-        bg[j] = w + (size_t)min(n0 + row, N - 1) * K + col;
-        soff[j] = row * TLD + col;
+        soffa[j] = row * TLD + col;
+        if (WL == W_FRAG) {
+            // piece c of the 16 fragment blocks (8 n-tiles x 2 k-steps) covering this 128 x 64 tile
+            const int blk = c >> 6, l = c & 63;
+            const int ntl = blk >> 1, kql = blk & 1;
+            bg[j] = w + ((size_t)min((n0 >> 4) + ntl, NT - 1) * (K >> 5) + kql) * 512 + l * 8;
+            soffb[j] = (16 * ntl + (l & 15)) * TLD + 32 * kql + 8 * (l >> 4);
+        } else {
+            bg[j] = w + (size_t)min(n0 + row, N - 1) * K + col;
+            soffb[j] = row * TLD + col;
+        }
     }
+    // k advance per 64-wide step: row-major 64 elements, fragment layout 2 blocks
+    constexpr size_t BSTEP = WL == W_FRAG ? 1024 : TBK;
 
     f32x16 acc[2][2];
 #pragma unroll
@@ -169,8 +215,8 @@ __global__ __launch_bounds__(256) void linear_tiled_kernel(const u16* __restrict
     }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        *reinterpret_cast<u16x8*>(&As[0][soff[j]]) = ra[j];
-        *reinterpret_cast<u16x8*>(&Bs[0][soff[j]]) = rb[j];
+        *reinterpret_cast<u16x8*>(&As[0][soffa[j]]) = ra[j];
+        *reinterpret_cast<u16x8*>(&Bs[0][soffb[j]]) = rb[j];
     }
     __syncthreads();
 
@@ -182,7 +228,7 @@ __global__ __launch_bounds__(256) void linear_tiled_kernel(const u16* __restrict
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 ra[j] = *reinterpret_cast<const u16x8*>(ag[j] + (size_t)(kt + 1) * TBK);
-                rb[j] = *reinterpret_cast<const u16x8*>(bg[j] + (size_t)(kt + 1) * TBK);
+                rb[j] = *reinterpret_cast<const u16x8*>(bg[j] + (size_t)(kt + 1) * BSTEP);
             }
         }
 #pragma unroll
@@ -202,8 +248,8 @@ __global__ __launch_bounds__(256) void linear_tiled_kernel(const u16* __restrict
         if (kt + 1 < nk) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                *reinterpret_cast<u16x8*>(&As[cur ^ 1][soff[j]]) = ra[j];
-                *reinterpret_cast<u16x8*>(&Bs[cur ^ 1][soff[j]]) = rb[j];
+                *reinterpret_cast<u16x8*>(&As[cur ^ 1][soffa[j]]) = ra[j];
+                *reinterpret_cast<u16x8*>(&Bs[cur ^ 1][soffb[j]]) = rb[j];
             }
         }
         __syncthreads();
@@ -224,43 +270,80 @@ __global__ __launch_bounds__(256) void linear_tiled_kernel(const u16* __restrict
         }
 }
 
-template <int NTS, int MT, int NW>
-static hipError_t skinny(const void* x, const void* w, int M, int N, int K, void* y, int out_kind,
-                         hipStream_t stream) {
+template <int NTS, int MT, int NW, int WL, int XL>
+hipError_t gemv(const void* x, const void* w, int M, int N, int K, void* y, int out_kind, hipStream_t stream) {
+    constexpr int PD = 4;
     const dim3 grid((N + NTS * 16 - 1) / (NTS * 16));
     const dim3 block(NW * 64);
     if (out_kind == OUT_F32)
-        hipLaunchKernelGGL((linear_skinny_kernel<NTS, MT, NW, OUT_F32>), grid, block, 0, stream,
-                           (const u16*)x, (const u16*)w, M, N, K, y);
+        hipLaunchKernelGGL((gemv_kernel<NTS, MT, NW, PD, OUT_F32, WL, XL>), grid, block, 0, stream, (const u16*)x,
+                           (const u16*)w, M, N, K, y);
     else
-        hipLaunchKernelGGL((linear_skinny_kernel<NTS, MT, NW, OUT_BF16>), grid, block, 0, stream,
-                           (const u16*)x, (const u16*)w, M, N, K, y);
-    return hipGetLastError();
-}
-
-template <int MT>
-static hipError_t skinny_mt(const void* x, const void* w, int M, int N, int K, void* y, int out_kind,
-                            hipStream_t stream) {
-    // Enough workgroups to cover the 256 CUs: 32-row tiles for wide outputs, 16-row tiles otherwise.
-    if (N >= 8192) return skinny<2, MT, 4>(x, w, M, N, K, y, out_kind, stream);
-    return skinny<1, MT, 4>(x, w, M, N, K, y, out_kind, stream);
-}
-
-hipError_t launch_linear(const void* x, const void* w, int M, int N, int K, void* y, int out_kind,
-                         hipStream_t stream) {
-    if (M <= 0 || N <= 0) return hipSuccess;
-    if (M <= 16) return skinny_mt<1>(x, w, M, N, K, y, out_kind, stream);
-    if (M <= 32) return skinny_mt<2>(x, w, M, N, K, y, out_kind, stream);
-    if (M <= 48) return skinny_mt<3>(x, w, M, N, K, y, out_kind, stream);
-    if (M <= 64) return skinny_mt<4>(x, w, M, N, K, y, out_kind, stream);
-    const dim3 grid(((M + TBM - 1) / TBM) * ((N + TBN - 1) / TBN));
-    if (out_kind == OUT_F32)
-        hipLaunchKernelGGL((linear_tiled_kernel<OUT_F32>), grid, dim3(256), 0, stream, (const u16*)x, (const u16*)w,
-                           M, N, K, y);
-    else
-        hipLaunchKernelGGL((linear_tiled_kernel<OUT_BF16>), grid, dim3(256), 0, stream, (const u16*)x,
+        hipLaunchKernelGGL((gemv_kernel<NTS, MT, NW, PD, OUT_BF16, WL, XL>), grid, block, 0, stream, (const u16*)x,
                            (const u16*)w, M, N, K, y);
     return hipGetLastError();
+}
+
+// Shape choice: enough workgroups to spread over the 256 CUs (NTS = rows / 16 per workgroup) and
+// enough waves per workgroup to keep >= 8 k-steps of 32 per wave.  Measured on the 9B shape at M = 64:
+// in_proj (N 12352, K 4096) NTS 4 / NW 4, out_proj (N 4096, K 4096) NTS 1 / NW 8.
+template <int MT, int WL, int XL>
+hipError_t gemv_mt(const void* x, const void* w, int M, int N, int K, void* y, int out_kind, hipStream_t stream) {
+    const int NT = (N + 15) / 16, KQ = K / 32;
+    if (NT >= 4 * 160) {
+        if (KQ >= 64) return gemv<4, MT, 4, WL, XL>(x, w, M, N, K, y, out_kind, stream);
+        return gemv<4, MT, 2, WL, XL>(x, w, M, N, K, y, out_kind, stream);
+    }
+    if (NT >= 2 * 160) {
+        if (KQ >= 64) return gemv<2, MT, 8, WL, XL>(x, w, M, N, K, y, out_kind, stream);
+        return gemv<2, MT, 4, WL, XL>(x, w, M, N, K, y, out_kind, stream);
+    }
+    if (KQ >= 64) return gemv<1, MT, 8, WL, XL>(x, w, M, N, K, y, out_kind, stream);
+    return gemv<1, MT, 4, WL, XL>(x, w, M, N, K, y, out_kind, stream);
+}
+
+template <int WL, int XL>
+hipError_t gemv_m(const void* x, const void* w, int M, int N, int K, void* y, int out_kind, hipStream_t stream) {
+    if (M <= 16) return gemv_mt<1, WL, XL>(x, w, M, N, K, y, out_kind, stream);
+    if (M <= 32) return gemv_mt<2, WL, XL>(x, w, M, N, K, y, out_kind, stream);
+    if (M <= 48) return gemv_mt<3, WL, XL>(x, w, M, N, K, y, out_kind, stream);
+    return gemv_mt<4, WL, XL>(x, w, M, N, K, y, out_kind, stream);
+}
+
+template <int WL>
+hipError_t linear_wl(const void* x, int xlayout, const void* w, int M, int N, int K, void* y, int out_kind,
+                     hipStream_t stream) {
+    if (M <= 64) {
+        if (xlayout == W_FRAG) return gemv_m<WL, W_FRAG>(x, w, M, N, K, y, out_kind, stream);
+        return gemv_m<WL, W_ROW>(x, w, M, N, K, y, out_kind, stream);
+    }
+    if (xlayout != W_ROW) return hipErrorInvalidValue;  // the GEMM reads row-major activations
+    const dim3 grid(((M + TBM - 1) / TBM) * ((N + TBN - 1) / TBN));
+    if (out_kind == OUT_F32)
+        hipLaunchKernelGGL((gemm_kernel<OUT_F32, WL>), grid, dim3(256), 0, stream, (const u16*)x, (const u16*)w, M,
+                           N, K, y);
+    else
+        hipLaunchKernelGGL((gemm_kernel<OUT_BF16, WL>), grid, dim3(256), 0, stream, (const u16*)x, (const u16*)w,
+                           M, N, K, y);
+    return hipGetLastError();
+}
+
+}  // namespace
+
+size_t frag_elems(int N, int K) { return (size_t)((N + 15) / 16) * 16 * K; }
+
+hipError_t launch_frag_tile(const void* w, int N, int K, void* wf, hipStream_t stream) {
+    const size_t pieces = frag_elems(N, K) / 8;
+    hipLaunchKernelGGL(frag_tile_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, stream, (const u16*)w,
+                       N, K, (u16*)wf);
+    return hipGetLastError();
+}
+
+hipError_t launch_linear(const void* x, int xlayout, const void* w, int wlayout, int M, int N, int K, void* y,
+                         int out_kind, hipStream_t stream) {
+    if (M <= 0 || N <= 0) return hipSuccess;
+    if (wlayout == W_FRAG) return linear_wl<W_FRAG>(x, xlayout, w, M, N, K, y, out_kind, stream);
+    return linear_wl<W_ROW>(x, xlayout, w, M, N, K, y, out_kind, stream);
 }
 
 }  // namespace gdn

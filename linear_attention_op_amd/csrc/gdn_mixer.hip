@@ -115,7 +115,8 @@ __global__ __launch_bounds__(256) void mixer_kernel(MixerArgs a) {
                 yv.y = f2bf(o.y * rstd * nw.y * siluf_(z.y));
                 yv.z = f2bf(o.z * rstd * nw.z * siluf_(z.z));
                 yv.w = f2bf(o.w * rstd * nw.w * siluf_(z.w));
-                *reinterpret_cast<ushort4*>(a.y + m * Vd + h * DV + 4 * lane) = yv;
+                const size_t yo = a.y_frag ? frag_offset((int)m, h * DV + 4 * lane, Vd) : m * Vd + h * DV + 4 * lane;
+                *reinterpret_cast<ushort4*>(a.y + yo) = yv;
                 if (a.o_tap) *reinterpret_cast<float4*>(a.o_tap + m * Vd + h * DV + 4 * lane) = o;
             }
         }
