@@ -67,7 +67,7 @@ typedef struct gdn_weights {
 
 /* 9B/gdn_layer.py:55-78 (__init__), 90-127 (_prepare_weights), 137-151 (reset_state).
  * Copies the weights into the fused in_proj layout [q|k|v|z|a|b, H], allocates `max_slots` zeroed
- * state slots (recurrent [nv, dk, dv] fp32 + conv ring) and a workspace for launches of up to
+ * state slots (recurrent [nv, dk, dv] fp32 + conv history) and a workspace for launches of up to
  * `max_tokens` rows (longer launches are split, 9B/gdn_layer.py:282-292). */
 int gdn_layer_create(const gdn_dims* dims, const gdn_weights* weights, int max_slots, int max_tokens,
                      gdn_layer** out);
@@ -92,8 +92,9 @@ int gdn_state_get(gdn_layer* layer, const int* slot_ids, int n, float* rec, floa
 int gdn_state_set(gdn_layer* layer, const int* slot_ids, int n, const float* rec, const float* conv, void* stream);
 
 /* Device addresses of the resident state buffers (for address-stability checks,
- * 9B/test_gated_delta_l1.py:81-92).  rec: [max_slots, nv, dk, dv] fp32. */
-int gdn_layer_state_buffers(gdn_layer* layer, void** rec, void** conv, void** ring_pos);
+ * 9B/test_gated_delta_l1.py:81-92).  rec: [max_slots, nv, dk, dv] fp32; conv: [max_slots, nv, 3, 2dk + dv]
+ * fp32, the last 3 pre-conv inputs of each v-head's channels in time order (entry 2 = newest). */
+int gdn_layer_state_buffers(gdn_layer* layer, void** rec, void** conv);
 
 /* Stage timing with HIP events recorded on the launch stream at the stage boundaries of every
  * gdn_layer_forward call (no counterpart in the reference, whose benches read the tt-metal device

@@ -60,8 +60,7 @@ struct gdn_layer {
     float* dt_bias = nullptr; // [nv]
     float* norm_w = nullptr;  // [dv]
     float* rec = nullptr;     // [slots, nv, dk, dv]
-    float* conv = nullptr;    // [slots, nv, 3, CH]
-    int* ring_pos = nullptr;  // [slots, nv]
+    float* conv = nullptr;    // [slots, nv, 3, CH] conv history, time order
 
     // workspace, sized for max_tokens rows
     u16* x_ws = nullptr;      // [max_tokens, H] gathered input rows when a launch is split
@@ -153,7 +152,7 @@ int run_chunk(gdn_layer* L, const u16* x, int B, int T, const int* slot_ids, u16
         a.nk = d.num_k_heads, a.nv = d.num_v_heads;
         a.conv_w = L->conv_w, a.neg_A = L->neg_A, a.dt_bias = L->dt_bias, a.norm_w = L->norm_w;
         a.eps = d.rms_norm_eps;
-        a.rec_state = L->rec, a.conv_state = L->conv, a.ring_pos = L->ring_pos;
+        a.rec_state = L->rec, a.conv_state = L->conv;
         a.y = L->y, a.y_frag = y_frag ? 1 : 0, a.o_tap = nullptr;
         HIP_OK(gdn::launch_mixer(a, d.head_k_dim, d.head_v_dim, st));
     } else {
@@ -161,11 +160,11 @@ int run_chunk(gdn_layer* L, const u16* x, int B, int T, const int* slot_ids, u16
         f.P = L->P, f.NP = L->NP, f.B = B, f.T = T, f.slot_ids = slot_ids;
         f.nk = d.num_k_heads, f.nv = d.num_v_heads, f.dk = d.head_k_dim, f.dv = d.head_v_dim;
         f.conv_w = L->conv_w, f.neg_A = L->neg_A, f.dt_bias = L->dt_bias;
-        f.conv_state = L->conv, f.ring_pos = L->ring_pos;
+        f.conv_state = L->conv;
         f.qn = L->qn, f.kn = L->kn, f.v = L->v, f.g = L->g, f.beta = L->beta;
         HIP_OK(gdn::launch_conv_front(f, st));
         HIP_OK(gdn::launch_conv_commit(L->P, L->NP, B, T, slot_ids, d.num_k_heads, d.num_v_heads, d.head_k_dim,
-                                       d.head_v_dim, L->conv, L->ring_pos, st));
+                                       d.head_v_dim, L->conv, st));
         gdn::DeltaArgs r{};
         r.q = L->qn, r.k = L->kn, r.v = L->v, r.g = L->g, r.beta = L->beta;
         r.B = B, r.T = T, r.Hk = d.num_k_heads, r.Hv = d.num_v_heads, r.slot_ids = slot_ids;
@@ -223,7 +222,6 @@ int gdn_layer_create(const gdn_dims* dims, const gdn_weights* w, int max_slots, 
     take(L->alloc(&L->norm_w, (size_t)dv));
     take(L->alloc(&L->rec, (size_t)max_slots * nv * dk * dv));
     take(L->alloc(&L->conv, (size_t)max_slots * nv * 3 * L->CH));
-    take(L->alloc(&L->ring_pos, (size_t)max_slots * nv));
     take(L->alloc(&L->x_ws, MT * H));
     take(L->alloc(&L->x_frag, gdn::frag_elems(64, H)));
     take(L->alloc(&L->out_ws, MT * H));
@@ -274,7 +272,7 @@ int gdn_layer_create(const gdn_dims* dims, const gdn_weights* w, int max_slots, 
     }
     if (e == hipSuccess) e = hipMemcpy(L->dt_bias, w->dt_bias, nv * sizeof(float), hipMemcpyDefault);
     if (e == hipSuccess) e = hipMemcpy(L->norm_w, w->norm_weight, dv * sizeof(float), hipMemcpyDefault);
-    if (e == hipSuccess) e = gdn::launch_state_zero(L->rec, L->conv, L->ring_pos, nullptr, max_slots, nv, dk, dv,
+    if (e == hipSuccess) e = gdn::launch_state_zero(L->rec, L->conv, nullptr, max_slots, nv, dk, dv,
                                                     L->CH, nullptr);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
@@ -324,7 +322,7 @@ int gdn_state_reset(gdn_layer* L, const int* slot_ids, int n, void* stream) {
     if (!L) return fail(GDN_ERR_INVALID_ARG, "layer is NULL");
     if (n < 0 || (!slot_ids && n > L->max_slots)) return fail(GDN_ERR_SLOT, "bad slot count %d", n);
     const gdn_dims& d = L->d;
-    HIP_OK(gdn::launch_state_zero(L->rec, L->conv, L->ring_pos, slot_ids, n, d.num_v_heads, d.head_k_dim,
+    HIP_OK(gdn::launch_state_zero(L->rec, L->conv, slot_ids, n, d.num_v_heads, d.head_k_dim,
                                   d.head_v_dim, L->CH, as_stream(stream)));
     return GDN_OK;
 }
@@ -333,7 +331,7 @@ int gdn_state_get(gdn_layer* L, const int* slot_ids, int n, float* rec, float* c
     if (!L || (!rec && !conv)) return fail(GDN_ERR_INVALID_ARG, "gdn_state_get: NULL argument");
     if (n < 0 || (!slot_ids && n > L->max_slots)) return fail(GDN_ERR_SLOT, "bad slot count %d", n);
     const gdn_dims& d = L->d;
-    HIP_OK(gdn::launch_state_export(L->rec, L->conv, L->ring_pos, slot_ids, n, d.num_k_heads, d.num_v_heads,
+    HIP_OK(gdn::launch_state_export(L->rec, L->conv, slot_ids, n, d.num_k_heads, d.num_v_heads,
                                     d.head_k_dim, d.head_v_dim, rec, conv, as_stream(stream)));
     return GDN_OK;
 }
@@ -342,16 +340,15 @@ int gdn_state_set(gdn_layer* L, const int* slot_ids, int n, const float* rec, co
     if (!L) return fail(GDN_ERR_INVALID_ARG, "layer is NULL");
     if (n < 0 || (!slot_ids && n > L->max_slots)) return fail(GDN_ERR_SLOT, "bad slot count %d", n);
     const gdn_dims& d = L->d;
-    HIP_OK(gdn::launch_state_import(L->rec, L->conv, L->ring_pos, slot_ids, n, d.num_k_heads, d.num_v_heads,
+    HIP_OK(gdn::launch_state_import(L->rec, L->conv, slot_ids, n, d.num_k_heads, d.num_v_heads,
                                     d.head_k_dim, d.head_v_dim, rec, conv, as_stream(stream)));
     return GDN_OK;
 }
 
-int gdn_layer_state_buffers(gdn_layer* L, void** rec, void** conv, void** ring_pos) {
+int gdn_layer_state_buffers(gdn_layer* L, void** rec, void** conv) {
     if (!L) return fail(GDN_ERR_INVALID_ARG, "layer is NULL");
     if (rec) *rec = L->rec;
     if (conv) *conv = L->conv;
-    if (ring_pos) *ring_pos = L->ring_pos;
     return GDN_OK;
 }
 
@@ -405,11 +402,11 @@ int gdn_conv_front(gdn_layer* L, const float* P, int B, int T, const int* slot_i
     f.P = P, f.NP = L->NP, f.B = B, f.T = T, f.slot_ids = slot_ids;
     f.nk = d.num_k_heads, f.nv = d.num_v_heads, f.dk = d.head_k_dim, f.dv = d.head_v_dim;
     f.conv_w = L->conv_w, f.neg_A = L->neg_A, f.dt_bias = L->dt_bias;
-    f.conv_state = L->conv, f.ring_pos = L->ring_pos;
+    f.conv_state = L->conv;
     f.qn = qn, f.kn = kn, f.v = v, f.g = g, f.beta = beta;
     HIP_OK(gdn::launch_conv_front(f, st));
     HIP_OK(gdn::launch_conv_commit(P, L->NP, B, T, slot_ids, d.num_k_heads, d.num_v_heads, d.head_k_dim,
-                                   d.head_v_dim, L->conv, L->ring_pos, st));
+                                   d.head_v_dim, L->conv, st));
     return GDN_OK;
 }
 

@@ -120,8 +120,7 @@ struct MixerArgs {
     const float* norm_w;    // [dv]
     float eps;              // RMSNorm eps
     float* rec_state;       // [slots, nv, dk, dv]
-    float* conv_state;      // [slots, nv, 3, 2dk + dv] ring, per v-head copy
-    int* ring_pos;          // [slots, nv]
+    float* conv_state;      // [slots, nv, 3, 2dk + dv] time-ordered history, per v-head copy
     u16* y;                 // [M, nv * dv] bf16 gated RMSNorm output
     int y_frag;             // 1: y in W_FRAG layout (rows padded to 16; M <= 64), 0: row-major
     float* o_tap;           // optional [M, nv * dv] recurrence output (nullptr: not written)
@@ -137,8 +136,7 @@ struct FrontArgs {
     const float4* conv_w;
     const float* neg_A;
     const float* dt_bias;
-    const float* conv_state;  // ring (read only here)
-    const int* ring_pos;
+    const float* conv_state;  // history (read only here)
     float* qn;                // [M, nk, dk]  l2norm(q) * dk^-0.5
     float* kn;                // [M, nk, dk]  l2norm(k)
     float* v;                 // [M, nv, dv]
@@ -146,9 +144,9 @@ struct FrontArgs {
     float* beta;              // [M, nv]
 };
 hipError_t launch_conv_front(const FrontArgs& a, hipStream_t stream);
-// Write the last min(T, 3) pre-conv inputs of each sequence into its ring and advance the ring.
+// Roll each sequence's conv history forward over the T inputs of this launch.
 hipError_t launch_conv_commit(const float* P, int NP, int B, int T, const int* slot_ids, int nk, int nv, int dk,
-                              int dv, float* conv_state, int* ring_pos, hipStream_t stream);
+                              int dv, float* conv_state, hipStream_t stream);
 
 // Recurrence over T tokens for B sequences from pre-normalised q/k (qn already scaled).
 struct DeltaArgs {
@@ -176,13 +174,11 @@ hipError_t launch_gated_rmsnorm(const float* o, int M, int nv, int dv, const flo
                                 const float* w, float eps, u16* y, hipStream_t stream);
 
 // State import / export (time-ordered conv history [n, conv_dim, 3]).
-hipError_t launch_state_export(const float* rec_state, const float* conv_state, const int* ring_pos,
-                               const int* slots, int n, int nk, int nv, int dk, int dv, float* rec_out,
-                               float* conv_out, hipStream_t stream);
-hipError_t launch_state_import(float* rec_state, float* conv_state, int* ring_pos, const int* slots, int n, int nk,
-                               int nv, int dk, int dv, const float* rec_in, const float* conv_in,
-                               hipStream_t stream);
-hipError_t launch_state_zero(float* rec_state, float* conv_state, int* ring_pos, const int* slots, int n, int nv,
-                             int dk, int dv, int ch, hipStream_t stream);
+hipError_t launch_state_export(const float* rec_state, const float* conv_state, const int* slots, int n, int nk,
+                               int nv, int dk, int dv, float* rec_out, float* conv_out, hipStream_t stream);
+hipError_t launch_state_import(float* rec_state, float* conv_state, const int* slots, int n, int nk, int nv, int dk,
+                               int dv, const float* rec_in, const float* conv_in, hipStream_t stream);
+hipError_t launch_state_zero(float* rec_state, float* conv_state, const int* slots, int n, int nv, int dk, int dv,
+                             int ch, hipStream_t stream);
 
 }  // namespace gdn

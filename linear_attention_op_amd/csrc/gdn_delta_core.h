@@ -1,4 +1,4 @@
-// One token of the gated delta rule on a workgroup-resident fp32 state tile (256 threads).
+// One token of the gated delta rule on a workgroup-resident fp32 state tile (NTH threads).
 //
 // Thread (rg, cg) = (tid / CG, tid % CG) holds rows rg + RG*i (i < RPT) and columns 4cg..4cg+3 of the
 // dk x dv state S (S[k][v], v contiguous), so a float4 load per row reads whole rows across the wave.
@@ -14,12 +14,13 @@
 
 namespace gdn {
 
-template <int DK, int DV>
+template <int DK, int DV, int NTH = 256>
 struct DeltaTile {
     static constexpr int CG = DV / 4;
-    static constexpr int RG = 256 / CG;
+    static constexpr int RG = NTH / CG;
     static constexpr int RPT = DK / RG;
-    static_assert(CG * RG == 256 && RPT * RG == DK && CG <= 64, "state tiling");
+    static constexpr int NWAVES = NTH / 64;
+    static_assert(CG * RG == NTH && RPT * RG == DK && CG <= 64, "state tiling");
 
     float4 s[RPT];
     int cg, rg;
@@ -37,8 +38,8 @@ struct DeltaTile {
         for (int i = 0; i < RPT; ++i) *reinterpret_cast<float4*>(S + (size_t)(rg + RG * i) * DV + 4 * cg) = s[i];
     }
 
-    // red: LDS scratch [4][2][DV].  Returns o for this thread's 4 columns (every thread gets its columns).
-    // Ends with the state updated; the caller must __syncthreads() before reusing sq/sk/sv/red.
+    // red: LDS scratch [NWAVES][2][DV].  Returns o for this thread's 4 columns (every thread gets its
+    // columns).  Ends with the state updated; the caller must __syncthreads() before reusing sq/sk/sv/red.
     __device__ __forceinline__ float4 step(const float* sq, const float* sk, const float* sv, float (*red)[2][DV],
                                            float rq, float rk, float qk, float d, float beta, int lane, int wave) {
         float4 pk = make_float4(0.f, 0.f, 0.f, 0.f), pq = pk;
@@ -59,7 +60,7 @@ struct DeltaTile {
         __syncthreads();
         float4 kS = make_float4(0.f, 0.f, 0.f, 0.f), qS = kS;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < NWAVES; ++w) {
             const float4 u = *reinterpret_cast<const float4*>(&red[w][0][4 * cg]);
             const float4 q = *reinterpret_cast<const float4*>(&red[w][1][4 * cg]);
             kS.x += u.x, kS.y += u.y, kS.z += u.z, kS.w += u.w;

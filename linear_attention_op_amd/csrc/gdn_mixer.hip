@@ -8,10 +8,14 @@
 // It restates, per token, wormhole_n150/qwen3.5_9B/kernels/layer_compute.cpp C1-C6 (74-395) with
 // layer_reader.cpp:103-124,184-197 for the conv history; HF:432-543 for the layer math.
 //
-// conv history: each (slot, v-head) owns a 3-entry ring of its 2*dk + dv pre-conv channels (the q/k
-// channels of its k-head are kept per v-head, so no two workgroups share a ring).  Logical entry j
-// (0 = oldest) lives at physical (pos + j) % 3; after T tokens, pos' = (pos + T) % 3 and only the last
-// min(T, 3) inputs are written, which is the reference's roll (layer_reader.cpp:184-197).
+// Load order matters: vector-memory loads complete in order, so every load the first token's conv,
+// norms and gating need (history, taps, the projection row, z) is issued before the 64 KB state; that
+// front-end work then runs while the state is still arriving.
+//
+// conv history: each (slot, v-head) keeps its 2*dk + dv pre-conv channels for the last 3 tokens in time
+// order, [3][2*dk + dv], entry 0 oldest (the q/k channels of its k-head are kept per v-head, so no two
+// workgroups share a history).  After a launch of T tokens entry j holds the input at time T - 3 + j:
+// the reference's roll (layer_reader.cpp:184-197).
 //
 // conv_front_kernel / conv_commit_kernel / gated_rmsnorm_kernel: the same front end and norm split into
 // token-parallel kernels for long prefills, where the recurrence runs in the chunked form.
@@ -34,26 +38,20 @@ __global__ __launch_bounds__(256) void mixer_kernel(MixerArgs a) {
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int h = blockIdx.x, b = blockIdx.y;
-    const int nv = a.nv, ratio = a.nv / a.nk, kh = h / ratio;
+    const int nv = a.nv, kh = h / (nv / a.nk);
     const int Kd = a.nk * DK, Vd = nv * DV, CD = 2 * Kd + Vd;
     const int slot = a.slot_ids ? a.slot_ids[b] : b;
     const int T = a.T;
 
     __shared__ float sq[DK], sk[DK], sv[DV];
     __shared__ float red[4][2][DV];
-    __shared__ float scal[8];
 
-    float* S = a.rec_state + ((size_t)slot * nv + h) * DK * DV;
-    Tile st;
-    st.init(tid);
-    st.load(S);
-
-    // conv channels: taps and the 3-entry history in registers (hx[c][0] oldest)
-    float* ring = a.conv_state + ((size_t)slot * nv + h) * 3 * CH;
-    const int pos = a.ring_pos[slot * nv + h];
-    float hx[CPT][3];
+    // ---- state-independent loads first: history, taps, the first token's projection values --------
+    float* hist = a.conv_state + ((size_t)slot * nv + h) * 3 * CH;
+    float hx[CPT][3], xin[CPT];
     float4 tap[CPT];
     int pcol[CPT];
+    const float* Prow = a.P + (size_t)b * T * a.NP;
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
         const int ch = tid + 256 * c;
@@ -62,26 +60,35 @@ __global__ __launch_bounds__(256) void mixer_kernel(MixerArgs a) {
             pcol[c] = conv_col(ch, kh, h, DK, DV, Kd);
             tap[c] = a.conv_w[pcol[c]];
 #pragma unroll
-            for (int j = 0; j < 3; ++j) hx[c][j] = ring[((pos + j) % 3) * CH + ch];
+            for (int j = 0; j < 3; ++j) hx[c][j] = hist[j * CH + ch];
+            xin[c] = Prow[pcol[c]];
         }
     }
+    float av = Prow[CD + Vd + h], bv = Prow[CD + Vd + nv + h];
+    float4 zv = make_float4(0.f, 0.f, 0.f, 0.f), nw = zv;
+    if (tid < Tile::CG) {
+        zv = *reinterpret_cast<const float4*>(Prow + CD + h * DV + 4 * tid);
+        nw = *reinterpret_cast<const float4*>(a.norm_w + 4 * tid);
+    }
     const float negA = a.neg_A[h], dtb = a.dt_bias[h];
-    float4 nw = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (tid < Tile::CG) nw = *reinterpret_cast<const float4*>(a.norm_w + 4 * tid);
+
+    // ---- then the state ----------------------------------------------------------------------------
+    float* S = a.rec_state + ((size_t)slot * nv + h) * DK * DV;
+    Tile st;
+    st.init(tid);
+    st.load(S);
     const float qscale = rsqrtf((float)DK);
 
     for (int t = 0; t < T; ++t) {
         const size_t m = (size_t)b * T + t;
-        const float* Prow = a.P + m * a.NP;
 #pragma unroll
         for (int c = 0; c < CPT; ++c) {
             const int ch = tid + 256 * c;
             if (ch < CH) {
-                const float xin = Prow[pcol[c]];
-                const float acc = tap[c].x * hx[c][0] + tap[c].y * hx[c][1] + tap[c].z * hx[c][2] + tap[c].w * xin;
+                const float acc = tap[c].x * hx[c][0] + tap[c].y * hx[c][1] + tap[c].z * hx[c][2] + tap[c].w * xin[c];
                 hx[c][0] = hx[c][1];
                 hx[c][1] = hx[c][2];
-                hx[c][2] = xin;
+                hx[c][2] = xin[c];
                 const float out = siluf_(acc);
                 if (ch < DK)
                     sq[ch] = out;
@@ -91,17 +98,32 @@ __global__ __launch_bounds__(256) void mixer_kernel(MixerArgs a) {
                     sv[ch - 2 * DK] = out;
             }
         }
-        __syncthreads();
-        qk_sums<DK>(sq, sk, scal, lane, wave);
-        if (wave == 3 && lane == 0) {
-            const float g = negA * softplusf_(Prow[CD + Vd + h] + dtb);
-            scal[3] = __expf(g);
-            scal[4] = sigmoidf_(Prow[CD + Vd + nv + h]);
+        // next token's projection values (issued now, consumed one token later)
+        float av_n = 0.f, bv_n = 0.f;
+        float4 zv_n = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (t + 1 < T) {
+            const float* Pn = Prow + (size_t)(t + 1) * a.NP;
+#pragma unroll
+            for (int c = 0; c < CPT; ++c)
+                if (tid + 256 * c < CH) xin[c] = Pn[pcol[c]];
+            av_n = Pn[CD + Vd + h], bv_n = Pn[CD + Vd + nv + h];
+            if (tid < Tile::CG) zv_n = *reinterpret_cast<const float4*>(Pn + CD + h * DV + 4 * tid);
         }
         __syncthreads();
-        const float rq = rsqrtf(scal[0] + 1e-6f) * qscale;
-        const float rk = rsqrtf(scal[1] + 1e-6f);
-        const float4 o = st.step(sq, sk, sv, red, rq, rk, scal[2] * rq * rk, scal[3], scal[4], lane, wave);
+
+        // |q|^2, |k|^2 and q.k, computed by every wave (no second barrier)
+        float pqq = 0.f, pkk = 0.f, pqk = 0.f;
+#pragma unroll
+        for (int i = lane; i < DK; i += 64) {
+            const float qv = sq[i], kv = sk[i];
+            pqq += qv * qv, pkk += kv * kv, pqk += qv * kv;
+        }
+        pqq = warp_sum(pqq), pkk = warp_sum(pkk), pqk = warp_sum(pqk);
+        const float rq = rsqrtf(pqq + 1e-6f) * qscale;
+        const float rk = rsqrtf(pkk + 1e-6f);
+        const float d = __expf(negA * softplusf_(av + dtb));
+        const float beta = sigmoidf_(bv);
+        const float4 o = st.step(sq, sk, sv, red, rq, rk, pqk * rq * rk, d, beta, lane, wave);
 
         // gated RMSNorm of this head's o on wave 0 (its lanes < CG hold all dv columns)
         if (wave == 0) {
@@ -109,30 +131,30 @@ __global__ __launch_bounds__(256) void mixer_kernel(MixerArgs a) {
             ss = warp_sum(ss);
             if (lane < Tile::CG) {
                 const float rstd = rsqrtf(ss / (float)DV + a.eps);
-                const float4 z = *reinterpret_cast<const float4*>(Prow + CD + h * DV + 4 * lane);
                 ushort4 yv;
-                yv.x = f2bf(o.x * rstd * nw.x * siluf_(z.x));
-                yv.y = f2bf(o.y * rstd * nw.y * siluf_(z.y));
-                yv.z = f2bf(o.z * rstd * nw.z * siluf_(z.z));
-                yv.w = f2bf(o.w * rstd * nw.w * siluf_(z.w));
+                yv.x = f2bf(o.x * rstd * nw.x * siluf_(zv.x));
+                yv.y = f2bf(o.y * rstd * nw.y * siluf_(zv.y));
+                yv.z = f2bf(o.z * rstd * nw.z * siluf_(zv.z));
+                yv.w = f2bf(o.w * rstd * nw.w * siluf_(zv.w));
                 const size_t yo = a.y_frag ? frag_offset((int)m, h * DV + 4 * lane, Vd) : m * Vd + h * DV + 4 * lane;
                 *reinterpret_cast<ushort4*>(a.y + yo) = yv;
                 if (a.o_tap) *reinterpret_cast<float4*>(a.o_tap + m * Vd + h * DV + 4 * lane) = o;
             }
         }
-        __syncthreads();
+        if (t + 1 < T) {
+            __syncthreads();  // the next token rewrites sq / sk / sv / red
+            av = av_n, bv = bv_n, zv = zv_n;
+        }
     }
 
     st.store(S);
-    const int npos = (pos + T) % 3;
-    const int first = T >= 3 ? 0 : 3 - T;  // older entries are the old history, already in place
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
         const int ch = tid + 256 * c;
         if (ch < CH)
-            for (int j = first; j < 3; ++j) ring[((npos + j) % 3) * CH + ch] = hx[c][j];
+#pragma unroll
+            for (int j = 0; j < 3; ++j) hist[j * CH + ch] = hx[c][j];
     }
-    if (tid == 0) a.ring_pos[slot * nv + h] = npos;
 }
 
 hipError_t launch_mixer(const MixerArgs& a, int dk, int dv, hipStream_t stream) {
@@ -164,7 +186,7 @@ __global__ __launch_bounds__(256) void conv_front_kernel(FrontArgs a) {
     const float* Prow = a.P + (size_t)m * a.NP;
 
     for (int col = tid; col < CD; col += 256) {
-        // owner ring of this column: q/k of k-head kh live in the ring of v-head kh * ratio
+        // history holding this column: q/k of k-head kh are read from the copy of v-head kh * ratio
         int hcopy, local;
         if (col < Kd) {
             const int kh = col / dk;
@@ -184,9 +206,8 @@ __global__ __launch_bounds__(256) void conv_front_kernel(FrontArgs a) {
             if (t >= s) {
                 xv = (Prow - (size_t)s * a.NP)[col];
             } else {
-                const int pos = a.ring_pos[slot * nv + hcopy];
-                const float* ring = a.conv_state + ((size_t)slot * nv + hcopy) * 3 * CH;
-                xv = ring[((pos + 3 + t - s) % 3) * CH + local];  // logical entry 3 + t - s
+                const float* hist = a.conv_state + ((size_t)slot * nv + hcopy) * 3 * CH;
+                xv = hist[(3 + t - s) * CH + local];  // input at time t - s < 0 is history entry 3 + t - s
             }
             xs[3 - s] = xv;
         }
@@ -226,28 +247,30 @@ hipError_t launch_conv_front(const FrontArgs& a, hipStream_t stream) {
 
 __global__ __launch_bounds__(256) void conv_commit_kernel(const float* __restrict__ P, int NP, int T,
                                                           const int* __restrict__ slot_ids, int nk, int nv, int dk,
-                                                          int dv, float* __restrict__ conv_state,
-                                                          int* __restrict__ ring_pos) {
+                                                          int dv, float* __restrict__ conv_state) {
+    // new entry j = input at time T - 3 + j: a projection row of this launch, or (T < 3) old entry T + j
     const int h = blockIdx.x, b = blockIdx.y;
     const int slot = slot_ids ? slot_ids[b] : b;
     const int kh = h / (nv / nk), Kd = nk * dk, CH = 2 * dk + dv;
-    const int pos = ring_pos[slot * nv + h];
-    float* ring = conv_state + ((size_t)slot * nv + h) * 3 * CH;
-    for (int j = 0; j < 3; ++j) {
-        const int tj = T - 3 + j;
-        if (tj < 0) continue;  // older entries stay where they are
-        const float* Prow = P + ((size_t)b * T + tj) * NP;
-        float* dst = ring + ((pos + T + j) % 3) * CH;
-        for (int c = threadIdx.x; c < CH; c += 256) dst[c] = Prow[conv_col(c, kh, h, dk, dv, Kd)];
+    float* hist = conv_state + ((size_t)slot * nv + h) * 3 * CH;
+    for (int c = threadIdx.x; c < CH; c += 256) {
+        const int col = conv_col(c, kh, h, dk, dv, Kd);
+        const float old[3] = {hist[c], hist[CH + c], hist[2 * CH + c]};
+        float nw[3];
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const int tj = T - 3 + j;
+            nw[j] = tj >= 0 ? P[((size_t)b * T + tj) * NP + col] : old[T + j];
+        }
+#pragma unroll
+        for (int j = 0; j < 3; ++j) hist[j * CH + c] = nw[j];
     }
-    __syncthreads();
-    if (threadIdx.x == 0) ring_pos[slot * nv + h] = (pos + T) % 3;
 }
 
 hipError_t launch_conv_commit(const float* P, int NP, int B, int T, const int* slot_ids, int nk, int nv, int dk,
-                              int dv, float* conv_state, int* ring_pos, hipStream_t stream) {
+                              int dv, float* conv_state, hipStream_t stream) {
     hipLaunchKernelGGL(conv_commit_kernel, dim3(nv, B), dim3(256), 0, stream, P, NP, T, slot_ids, nk, nv, dk, dv,
-                       conv_state, ring_pos);
+                       conv_state);
     return hipGetLastError();
 }
 
@@ -282,11 +305,11 @@ hipError_t launch_gated_rmsnorm(const float* o, int M, int nv, int dv, const flo
 
 // ------------------------------------------------------------------------------------------------
 // State import / export / zero.  Export gives the conv history in time order [n, conv_dim, 3]
-// (q/k channels from the ring of the first v-head of each k-head group).
+// (q/k channels from the copy of the first v-head of each k-head group).
 // ------------------------------------------------------------------------------------------------
 __global__ void state_export_kernel(const float* __restrict__ rec, const float* __restrict__ conv,
-                                    const int* __restrict__ ring_pos, const int* __restrict__ slots, int nk, int nv,
-                                    int dk, int dv, float* __restrict__ rec_out, float* __restrict__ conv_out) {
+                                    const int* __restrict__ slots, int nk, int nv, int dk, int dv,
+                                    float* __restrict__ rec_out, float* __restrict__ conv_out) {
     const int i = blockIdx.y;
     const int slot = slots ? slots[i] : i;
     const size_t rec_n = (size_t)nv * dk * dv;
@@ -304,15 +327,14 @@ __global__ void state_export_kernel(const float* __restrict__ rec, const float* 
         } else {
             hcopy = (col - 2 * Kd) / dv, local = 2 * dk + (col - 2 * Kd) % dv;
         }
-        const int pos = ring_pos[slot * nv + hcopy];
-        const float* ring = conv + ((size_t)slot * nv + hcopy) * 3 * CH;
-        for (int j = 0; j < 3; ++j) conv_out[((size_t)i * CD + col) * 3 + j] = ring[((pos + j) % 3) * CH + local];
+        const float* hist = conv + ((size_t)slot * nv + hcopy) * 3 * CH;
+        for (int j = 0; j < 3; ++j) conv_out[((size_t)i * CD + col) * 3 + j] = hist[j * CH + local];
     }
 }
 
-__global__ void state_import_kernel(float* __restrict__ rec, float* __restrict__ conv, int* __restrict__ ring_pos,
-                                    const int* __restrict__ slots, int nk, int nv, int dk, int dv,
-                                    const float* __restrict__ rec_in, const float* __restrict__ conv_in) {
+__global__ void state_import_kernel(float* __restrict__ rec, float* __restrict__ conv, const int* __restrict__ slots,
+                                    int nk, int nv, int dk, int dv, const float* __restrict__ rec_in,
+                                    const float* __restrict__ conv_in) {
     const int i = blockIdx.y;
     const int slot = slots ? slots[i] : i;
     const size_t rec_n = (size_t)nv * dk * dv;
@@ -320,40 +342,32 @@ __global__ void state_import_kernel(float* __restrict__ rec, float* __restrict__
         for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < rec_n; e += (size_t)gridDim.x * blockDim.x)
             rec[(size_t)slot * rec_n + e] = rec_in[(size_t)i * rec_n + e];
     const int Kd = nk * dk, CD = 2 * Kd + nv * dv, CH = 2 * dk + dv, ratio = nv / nk;
-    // every v-head ring of this slot restarts at pos 0 with the time-ordered history
     for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < nv * CH; e += gridDim.x * blockDim.x) {
         const int h = e / CH, c = e % CH;
-        const int kh = h / ratio;
-        const int col = conv_col(c, kh, h, dk, dv, Kd);
-        float* ring = conv + ((size_t)slot * nv + h) * 3 * CH;
-        for (int j = 0; j < 3; ++j) ring[j * CH + c] = conv_in ? conv_in[((size_t)i * CD + col) * 3 + j] : 0.f;
+        const int col = conv_col(c, h / ratio, h, dk, dv, Kd);
+        float* hist = conv + ((size_t)slot * nv + h) * 3 * CH;
+        for (int j = 0; j < 3; ++j) hist[j * CH + c] = conv_in ? conv_in[((size_t)i * CD + col) * 3 + j] : 0.f;
     }
-    __syncthreads();
-    if (blockIdx.x == 0)
-        for (int h = threadIdx.x; h < nv; h += blockDim.x) ring_pos[slot * nv + h] = 0;
 }
 
-hipError_t launch_state_export(const float* rec_state, const float* conv_state, const int* ring_pos,
-                               const int* slots, int n, int nk, int nv, int dk, int dv, float* rec_out,
-                               float* conv_out, hipStream_t stream) {
+hipError_t launch_state_export(const float* rec_state, const float* conv_state, const int* slots, int n, int nk,
+                               int nv, int dk, int dv, float* rec_out, float* conv_out, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(state_export_kernel, dim3(64, n), dim3(256), 0, stream, rec_state, conv_state, ring_pos,
-                       slots, nk, nv, dk, dv, rec_out, conv_out);
+    hipLaunchKernelGGL(state_export_kernel, dim3(64, n), dim3(256), 0, stream, rec_state, conv_state, slots, nk, nv,
+                       dk, dv, rec_out, conv_out);
     return hipGetLastError();
 }
 
-hipError_t launch_state_import(float* rec_state, float* conv_state, int* ring_pos, const int* slots, int n, int nk,
-                               int nv, int dk, int dv, const float* rec_in, const float* conv_in,
-                               hipStream_t stream) {
+hipError_t launch_state_import(float* rec_state, float* conv_state, const int* slots, int n, int nk, int nv, int dk,
+                               int dv, const float* rec_in, const float* conv_in, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
-    // ring_pos is reset by block 0 after its own ring writes; the other blocks never read it
-    hipLaunchKernelGGL(state_import_kernel, dim3(64, n), dim3(256), 0, stream, rec_state, conv_state, ring_pos,
-                       slots, nk, nv, dk, dv, rec_in, conv_in);
+    hipLaunchKernelGGL(state_import_kernel, dim3(64, n), dim3(256), 0, stream, rec_state, conv_state, slots, nk, nv,
+                       dk, dv, rec_in, conv_in);
     return hipGetLastError();
 }
 
-__global__ void state_zero_kernel(float* __restrict__ rec, float* __restrict__ conv, int* __restrict__ ring_pos,
-                                  const int* __restrict__ slots, int nv, int dk, int dv, int ch) {
+__global__ void state_zero_kernel(float* __restrict__ rec, float* __restrict__ conv, const int* __restrict__ slots,
+                                  int nv, int dk, int dv, int ch) {
     const int i = blockIdx.y;
     const int slot = slots ? slots[i] : i;
     const size_t rec_n = (size_t)nv * dk * dv;
@@ -362,15 +376,13 @@ __global__ void state_zero_kernel(float* __restrict__ rec, float* __restrict__ c
         rec[(size_t)slot * rec_n + e] = 0.f;
     for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < conv_n; e += (size_t)gridDim.x * blockDim.x)
         conv[(size_t)slot * conv_n + e] = 0.f;
-    if (blockIdx.x == 0)
-        for (int h = threadIdx.x; h < nv; h += blockDim.x) ring_pos[slot * nv + h] = 0;
 }
 
-hipError_t launch_state_zero(float* rec_state, float* conv_state, int* ring_pos, const int* slots, int n, int nv,
-                             int dk, int dv, int ch, hipStream_t stream) {
+hipError_t launch_state_zero(float* rec_state, float* conv_state, const int* slots, int n, int nv, int dk, int dv,
+                             int ch, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(state_zero_kernel, dim3(64, n), dim3(256), 0, stream, rec_state, conv_state, ring_pos, slots,
-                       nv, dk, dv, ch);
+    hipLaunchKernelGGL(state_zero_kernel, dim3(64, n), dim3(256), 0, stream, rec_state, conv_state, slots, nv, dk,
+                       dv, ch);
     return hipGetLastError();
 }
 

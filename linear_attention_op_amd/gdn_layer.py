@@ -149,10 +149,10 @@ class Qwen35GatedDeltaNetHIP:
         _lib.check(_lib.lib().gdn_state_set(self._h, _ptr(s), n, _ptr(r), _ptr(c), _stream()))
 
     def state_buffers(self):
-        """Device addresses (rec, conv, ring_pos) of the resident state buffers."""
-        r, c, p = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
-        _lib.check(_lib.lib().gdn_layer_state_buffers(self._h, ctypes.byref(r), ctypes.byref(c), ctypes.byref(p)))
-        return r.value, c.value, p.value
+        """Device addresses (rec, conv) of the resident state buffers."""
+        r, c = ctypes.c_void_p(), ctypes.c_void_p()
+        _lib.check(_lib.lib().gdn_layer_state_buffers(self._h, ctypes.byref(r), ctypes.byref(c)))
+        return r.value, c.value
 
     def profile(self, max_calls):
         """Record stage times (HIP events on the launch stream) for the next `max_calls` forward calls."""

@@ -51,7 +51,7 @@ def test_chunked_layer_matches_oracle_08b(B, T):
     assert rel(out, want) < OUT_TOL
     assert rel(rec, rec_o) < STATE_TOL
     # the history copies projection outputs (GPU fp32 accumulation vs the oracle's fp64): equal to
-    # rounding; the ring indexing itself is pinned bit-exact in test_gpu_layer
+    # rounding; the shift / roll indexing itself is pinned bit-exact in test_gpu_layer
     assert rel(conv, conv_o) < 1e-6
 
 

@@ -3,7 +3,7 @@
 Truth: the HF golden vectors (tiny geometry, the reference's (B, T) grid and prefill -> decode
 continuation, 9B/test_gdn_layer.py:42-73) and the CPU oracle on the same seeded inputs at the real
 0.8B and 9B shapes.  Bars: layer output (bf16) rel-L2 <= 1e-2, recurrent state (fp32) <= 1e-3, conv
-history bit-exact (it is a copy of projection outputs; the integer ring indexing must match the
+history bit-exact (it is a copy of projection outputs; the integer shift / roll indexing must match the
 reference's shift / roll rules).
 """
 import os
@@ -136,7 +136,7 @@ def test_per_op_pipeline_matches_oracle(layer08):
 
 @pytest.mark.parametrize("Ts", [(1, 2, 3, 4, 5, 1, 1), (3, 1, 70, 2)])
 def test_conv_ring_is_bit_exact_across_launches(layer08, Ts):
-    """Launch lengths below, at and above the 3-entry history, continuing one ring (layer_reader.cpp
+    """Launch lengths below, at and above the 3-entry history, continuing one history (layer_reader.cpp
     shift 111-120 / roll 189-194 rules in the oracle)."""
     d, w, wn, gen = layer08
     B = 2
@@ -251,7 +251,7 @@ def layer9b():
 
 @pytest.mark.parametrize("B", [1, 8, 64])
 def test_config_9b_decode(layer9b, B):
-    """9B shape, decode at batch 1 / 8 / 64 from S0 ~ N(0, 0.01); two steps so the ring advances."""
+    """9B shape, decode at batch 1 / 8 / 64 from S0 ~ N(0, 0.01); two steps so the history rolls."""
     d, w, wn, gen = layer9b
     print(f"9B decode B={B}", flush=True)
     x, s0 = syn.make_inputs(d, B, 2, gen, state_std=0.01)
