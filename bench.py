@@ -94,6 +94,8 @@ def main():
     ap.add_argument("--prefill-steps", type=int, default=3)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--graph", type=int, default=0,
+                    help="1: replay the decode step from HIP graphs; 0: launch eagerly (faster here: 104 vs 112 us)")
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
 
@@ -129,18 +131,48 @@ def main():
     xs = [(torch.randn(B, 1, d["hidden"], device=dev)).to(torch.bfloat16) for _ in range(4)]
     torch.cuda.synchronize()
 
+    # eager warm-up, then one HIP graph per layer copy for the decode step (the counterpart of the
+    # reference's traced decode, wormhole_n150/qwen3.5_0.8B/bench_decode.py:44-60)
     for i in range(args.warmup):
         layers[i % L](xs[i % 4])
     torch.cuda.synchronize()
-    for lay in layers:
-        lay.profile(args.steps)
+    steps_fn = []
+    if args.graph:
+        xin = [xs[i % 4].clone() for i in range(L)]
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for i in range(L):
+                layers[i](xin[i])
+        torch.cuda.current_stream().wait_stream(side)
+        graphs = []
+        for i in range(L):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                layers[i](xin[i])
+            graphs.append(g)
+        for i in range(args.warmup):
+            graphs[i % L].replay()
+        steps_fn = [g.replay for g in graphs]
+    else:
+        steps_fn = [(lambda i=i: layers[i](xs[i % 4])) for i in range(L)]
     torch.cuda.synchronize()
+
+    # timed region: exactly `steps` decode steps, synchronised on both sides
     t0 = time.perf_counter()
     for i in range(args.steps):
-        layers[i % L](xs[i % 4])
+        steps_fn[i % L]()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
 
+    # stage breakdown: the same steps run eagerly with HIP events recorded on the launch stream at the
+    # stage boundaries (in_proj | mixer | out_proj)
+    for lay in layers:
+        lay.profile(args.steps)
+    torch.cuda.synchronize()
+    for i in range(args.steps):
+        layers[i % L](xs[i % 4])
+    torch.cuda.synchronize()
     stage = {"in_proj": 0.0, "mixer": 0.0, "out_proj": 0.0, "total": 0.0}
     calls = 0
     for lay in layers:
@@ -165,7 +197,8 @@ def main():
                   "event_step_us": stage_avg_ms["total"] * 1e3,
                   "event_frac": step_bytes / (stage_avg_ms["total"] / 1e3) / HBM_PEAK,
                   "stage_us": {k: v * 1e3 for k, v in stage_avg_ms.items()}}
-    print(f"[bench] decode B={B}: {ms_per_step * 1e3:.1f} us/step wall, stages (us) "
+    print(f"[bench] decode B={B}: {ms_per_step * 1e3:.1f} us/step wall ({'graph' if args.graph else 'eager'}), "
+          f"eager stages (us) "
           f"{ {k: round(v * 1e3, 1) for k, v in stage_avg_ms.items()} }", file=sys.stderr, flush=True)
     for lay in layers[1:]:
         lay.close()
@@ -206,7 +239,7 @@ def main():
         "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": f"9B-shape GDN layer decode, batch {B}, one token per sequence per step, "
-                               f"rotating over {L} layer copies",
+                               f"rotating over {L} layer copies" + (", HIP-graph replay" if args.graph else ""),
                    "hidden": d["hidden"], "num_k_heads": d["num_k_heads"], "num_v_heads": d["num_v_heads"],
                    "head_dim": 128, "batch": B, "state_dtype": "fp32", "weights": "bf16 N(0,0.02) seed 2"},
         "roofline": roofline, "layer_roofline": layer_roof, "prefill": prefill, "cpu_baseline": cpu,
