@@ -15,13 +15,14 @@
 //
 // Two kernels:
 //  * chunk_prep_kernel: every (sequence, v-head, chunk) in parallel.  Everything that does not depend on
-//    S: G, L, T, U, W, Q' and the intra-chunk output Aqk U (written straight into o).
+//    S: G, L, T, U, W, Q', the decay-scaled transposed keys and the intra-chunk output Aqk U (written
+//    straight into o).
 //  * chunk_state_kernel: the sequential pass over chunks.  A workgroup owns 16 value columns of one
 //    (sequence, v-head) state; its four waves own 32 state rows each, held in MFMA accumulators for the
 //    whole launch (state read once, written once).  Per chunk: W S and Q' S (partials over the waves'
 //    rows, summed through LDS), Vn, O += Q' S, S update.  The next chunk's operands are loaded while the
 //    current one is computed.  Workgroup ids put the 8 column blocks of a head on one XCD so that they
-//    share that XCD's L2 copy of W, Q' and k.
+//    share that XCD's L2 copy of W, Q' and the keys.
 //
 // Precision: every product that feeds the state or the output goes through split bf16 (hi + lo, three
 // MFMAs, ~2^-17 relative), so the chunked state matches the fp32 sequential rule to ~1e-5.
@@ -43,22 +44,40 @@ struct ChunkWs {
     float* W;   // [B, Hv, NC, CK, dk]
     float* Q;   // [B, Hv, NC, CK, dk]   Q'
     float* U;   // [B, Hv, NC, CK, dv]
-    float* G;   // [B, Hv, NC, 2, CK]    G (in-chunk cumulative log decay), rk (key normaliser)
+    float* K;   // [B, Hv, NC, dk, CK]   normalised keys, transposed, scaled by e^{G_last - G}
+    float* G;   // [B, Hv, NC, CK]       G (in-chunk cumulative log decay)
     int NC;     // chunks per sequence
 };
 
 // ------------------------------------------------------------------------------------------------
 // chunk_prep_kernel: grid (NC, Hv, B), 256 threads.
+//
+// Phases (wave w of 4):
+//   0. issue the chunk's loads: keys and queries (coalesced float4) and values (kept in registers until
+//      the last phase), g, beta.
+//   1. per-token normalisers (32-lane reductions), normalised keys -> sK, queries -> sQ (aliases the
+//      L / Aqk tiles, which are not written yet), G = cumsum(g).
+//   2. k k^T and q k^T (wave w: row tile w, column tiles <= w) -> L into sL, Aqk into sA.
+//   3. T = (I + L)^-1, blocked: the four 16 x 16 diagonal blocks by forward substitution (one wave
+//      each), then T_ij = -T_ii sum_{k=j}^{i-1} L_ik T_kj by distance i - j = 1, 2, 3 -> sT.
+//   4. M2 = Aqk T in place over Aqk.
+//   5. [T; M2] x (beta K e^G): W and Q' = Q e^G - Aqk W; the transposed key tile for the state pass.
+//   6. beta V over the key tile; [T; M2] x (beta V): U and the intra-chunk output.
 // ------------------------------------------------------------------------------------------------
 template <int DK, int DV>
 __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws) {
     static_assert(DK == 128 && DV == 128, "chunked path is specialised for 128-wide heads");
-    constexpr int LDK = DK + 4;  // row stride (floats) of the key tile
+    constexpr int LDK = DK + 4;  // row stride (floats) of the 64 x 128 tiles
     constexpr int LDT = CK + 4;  // row stride of the 64 x 64 tiles
-    __shared__ __attribute__((aligned(16))) float sK[CK * LDK];
-    __shared__ __attribute__((aligned(16))) float sT[CK * LDT];  // L, then T
-    __shared__ __attribute__((aligned(16))) float sA[CK * LDT];  // Aqk, then M2 = Aqk T
-    __shared__ float sG[CK], sEG[CK], sBeta[CK], sRq[CK], sRk[CK];
+    constexpr int LDX = 17;      // row stride of the 16 x 16 scratch blocks
+    __shared__ __attribute__((aligned(16))) float sK[CK * LDK];          // keys, then beta V
+    __shared__ __attribute__((aligned(16))) float sLA[2 * CK * LDT];     // queries, then L | Aqk (M2)
+    __shared__ __attribute__((aligned(16))) float sT[CK * LDT];          // T
+    __shared__ __attribute__((aligned(16))) float sX[4][16 * LDX];       // per-wave 16 x 16 scratch
+    __shared__ float sG[CK], sEG[CK], sBeta[CK];
+    float* sQ = sLA;                 // [CK][LDK] fits in the 2 * CK * LDT floats of sLA
+    float* sL = sLA;                 // [CK][LDT]
+    float* sA = sLA + CK * LDT;      // [CK][LDT]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
@@ -68,9 +87,40 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
     const int m = lane & 15, grp = lane >> 4;
     const size_t hc = ((size_t)b * Hv + h) * ws.NC + c;
 
-    // ---- per-token scalars: G = cumsum(g) (padded tokens add 0), beta, q / k normalisers ---------
+    // ---- 0. loads: piece e = tid + 256 j of a 64 x 128 tile is row e / 32 (= tid / 32 + 8 j), float4 e % 32
+    const int prow = tid >> 5, pc4 = (tid & 31) * 4;
+    float4 kr[8], qr[8], vr[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int tok = prow + 8 * j;
+        const bool ok = tok < len;
+        const size_t row = row0 + (ok ? tok : 0);
+        const size_t qk = (row * Hk + kh) * DK + pc4;
+        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+        kr[j] = ok ? *reinterpret_cast<const float4*>(a.k + qk) : z;
+        qr[j] = ok ? *reinterpret_cast<const float4*>(a.q + qk) : z;
+        vr[j] = ok ? *reinterpret_cast<const float4*>(a.v + (row * Hv + h) * DV + pc4) : z;
+    }
+    float gv = 0.f, bv = 0.f;
+    if (wave == 0 && lane < len) gv = a.g[(row0 + lane) * Hv + h], bv = a.beta[(row0 + lane) * Hv + h];
+
+    // ---- 1. normalisers (the 32 lanes of a half-wave hold one row), sK, sQ, G ---------------------------
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int tok = prow + 8 * j;
+        float sk = kr[j].x * kr[j].x + kr[j].y * kr[j].y + kr[j].z * kr[j].z + kr[j].w * kr[j].w;
+        float sq = qr[j].x * qr[j].x + qr[j].y * qr[j].y + qr[j].z * qr[j].z + qr[j].w * qr[j].w;
+#pragma unroll
+        for (int off = 1; off < 32; off <<= 1) sk += __shfl_xor(sk, off, 64), sq += __shfl_xor(sq, off, 64);
+        const float rk = a.normalize ? rsqrtf(sk + 1e-6f) : 1.f;
+        const float rq = (a.normalize ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
+        float4 kn = kr[j], qn = qr[j];
+        kn.x *= rk, kn.y *= rk, kn.z *= rk, kn.w *= rk;
+        qn.x *= rq, qn.y *= rq, qn.z *= rq, qn.w *= rq;
+        *reinterpret_cast<float4*>(&sK[tok * LDK + pc4]) = kn;
+        *reinterpret_cast<float4*>(&sQ[tok * LDK + pc4]) = qn;
+    }
     if (wave == 0) {
-        float gv = lane < len ? a.g[(row0 + lane) * Hv + h] : 0.f;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
             const float y = __shfl_up(gv, off, 64);
@@ -78,57 +128,29 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
         }
         sG[lane] = gv;
         sEG[lane] = __expf(gv);
-        sBeta[lane] = lane < len ? a.beta[(row0 + lane) * Hv + h] : 0.f;
-    }
-    for (int i = 0; i < 16; ++i) {
-        const int tok = wave * 16 + i;
-        float rq = a.scale, rk = 1.f;
-        if (a.normalize && tok < len) {
-            const float2 qv = *reinterpret_cast<const float2*>(a.q + ((row0 + tok) * Hk + kh) * DK + 2 * lane);
-            const float2 kv = *reinterpret_cast<const float2*>(a.k + ((row0 + tok) * Hk + kh) * DK + 2 * lane);
-            rq = rsqrtf(warp_sum(qv.x * qv.x + qv.y * qv.y) + 1e-6f) * a.scale;
-            rk = rsqrtf(warp_sum(kv.x * kv.x + kv.y * kv.y) + 1e-6f);
-        }
-        if (lane == 0) sRq[tok] = rq, sRk[tok] = rk;
+        sBeta[lane] = bv;
     }
     __syncthreads();
 
-    // ---- normalised keys into LDS (rows past the sequence are zero) --------------------------------
-    for (int e = tid; e < CK * DK / 4; e += 256) {
-        const int tok = e / (DK / 4), c4 = (e % (DK / 4)) * 4;
-        float4 kv = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (tok < len) {
-            kv = *reinterpret_cast<const float4*>(a.k + ((row0 + tok) * Hk + kh) * DK + c4);
-            const float r = sRk[tok];
-            kv.x *= r, kv.y *= r, kv.z *= r, kv.w *= r;
-        }
-        *reinterpret_cast<float4*>(&sK[tok * LDK + c4]) = kv;
-    }
-    __syncthreads();
-
-    // ---- k k^T and q k^T: wave w owns row tile w, column tiles <= w ------------------------------
+    // ---- 2. k k^T and q k^T: wave w owns row tile w, column tiles <= w ------------------------------
+    // the queries this wave needs later for Q' (rows 16 w + 4 grp + i, columns 16 n + m) are read now,
+    // before sQ is overwritten
+    float qe[DK / 16][4];
+#pragma unroll
+    for (int n = 0; n < DK / 16; ++n)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) qe[n][i] = sQ[(16 * wave + 4 * grp + i) * LDK + 16 * n + m];
     {
         const int mi = wave;
         f32x4 akk[4], aqk[4];
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni) akk[ni] = aqk[ni] = f32x4{0.f, 0.f, 0.f, 0.f};
-        const int qr = 16 * mi + m;
-        const bool qvalid = qr < len;
-        const float rq = sRq[qr];
-        const float* qrow = a.q + ((row0 + (qvalid ? qr : 0)) * Hk + kh) * DK;
 #pragma unroll
         for (int s = 0; s < DK / 32; ++s) {
             const int k0 = 32 * s + 8 * grp;
             float ka[8], qa[8];
-            load8(&sK[qr * LDK + k0], ka);
-            if (qvalid) {
-                load8(qrow + k0, qa);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) qa[j] *= rq;
-            } else {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) qa[j] = 0.f;
-            }
+            load8(&sK[(16 * mi + m) * LDK + k0], ka);
+            load8(&sQ[(16 * mi + m) * LDK + k0], qa);
             const Split8 A1 = split8(ka), A2 = split8(qa);
 #pragma unroll
             for (int ni = 0; ni < 4; ++ni) {
@@ -140,6 +162,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
                 aqk[ni] = mfma3(A2, Bk, aqk[ni]);
             }
         }
+        __syncthreads();  // every wave is done with sQ before L / Aqk overwrite it
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
@@ -151,36 +174,66 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
                     A = aqk[ni][i] * dec;
                     if (cc < r) L = sBeta[r] * akk[ni][i] * dec;
                 }
-                sT[r * LDT + cc] = L;
+                sL[r * LDT + cc] = L;
                 sA[r * LDT + cc] = A;
             }
     }
     __syncthreads();
 
-    // ---- T = (I + L)^-1 by forward substitution: lane j of wave 0 owns column j ---------------------
-    //      T[i][j] = delta_ij - sum_{k < i} L[i][k] T[k][j]
-    if (wave == 0) {
-        const int j = lane;
-        float t[CK];
+    // ---- 3. T = (I + L)^-1 ---------------------------------------------------------------------------
+    // 3a. diagonal block w: lane c < 16 owns column c, rows by forward substitution
+    if (lane < 16) {
+        const int o = 16 * wave;
+        float t[16];
 #pragma unroll
-        for (int i = 0; i < CK; ++i) {
-            float acc = (i == j) ? 1.f : 0.f;
-            const float* Li = &sT[i * LDT];
+        for (int r = 0; r < 16; ++r) {
+            float acc = (r == lane) ? 1.f : 0.f;
 #pragma unroll
-            for (int k4 = 0; k4 < i / 4; ++k4) {
-                const float4 l4 = *reinterpret_cast<const float4*>(Li + 4 * k4);
-                acc -= l4.x * t[4 * k4] + l4.y * t[4 * k4 + 1] + l4.z * t[4 * k4 + 2] + l4.w * t[4 * k4 + 3];
-            }
-#pragma unroll
-            for (int k = 4 * (i / 4); k < i; ++k) acc -= Li[k] * t[k];
-            t[i] = acc;
+            for (int k = 0; k < r; ++k) acc -= sL[(o + r) * LDT + o + k] * t[k];
+            t[r] = acc;
         }
 #pragma unroll
-        for (int i = 0; i < CK; ++i) sT[i * LDT + j] = t[i];
+        for (int r = 0; r < 16; ++r) sT[(o + r) * LDT + o + lane] = t[r];
+    }
+    // upper blocks of T are zero
+    for (int e = tid; e < CK * CK; e += 256) {
+        const int r = e / CK, cc = e % CK;
+        if ((cc >> 4) > (r >> 4)) sT[r * LDT + cc] = 0.f;
     }
     __syncthreads();
+    // 3b. T_ij = -T_ii X, X = sum_{k=j}^{i-1} L_ik T_kj.  Lane (r4, cc) = (lane / 16, lane % 16) makes
+    //     rows 4 r4 .. 4 r4 + 3 of column cc of the block.
+#pragma unroll
+    for (int dist = 1; dist < 4; ++dist) {
+        const int j = wave, i = wave + dist;
+        if (i < 4) {
+            const int r4 = lane >> 4, cc = lane & 15;
+            float x[4] = {0.f, 0.f, 0.f, 0.f};
+            for (int k = j; k < i; ++k)
+#pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    const float tkj = sT[(16 * k + q) * LDT + 16 * j + cc];
+#pragma unroll
+                    for (int rr = 0; rr < 4; ++rr) x[rr] += sL[(16 * i + 4 * r4 + rr) * LDT + 16 * k + q] * tkj;
+                }
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) sX[wave][(4 * r4 + rr) * LDX + cc] = x[rr];
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+            float y[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const float xq = sX[wave][q * LDX + cc];
+#pragma unroll
+                for (int rr = 0; rr < 4; ++rr) y[rr] += sT[(16 * i + 4 * r4 + rr) * LDT + 16 * i + q] * xq;
+            }
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) sT[(16 * i + 4 * r4 + rr) * LDT + 16 * j + cc] = -y[rr];
+        }
+        __syncthreads();
+    }
 
-    // ---- M2 = Aqk T, in place over Aqk (wave w reads and writes only its own row tile) ----------------
+    // ---- 4. M2 = Aqk T, in place over Aqk (wave w reads and writes only its own row tile) ----------------
     {
         const int mi = wave;
         f32x4 acc[4];
@@ -211,26 +264,40 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
     }
     __syncthreads();
 
-    // ---- [T; M2] x [beta V | beta K e^G]: U, W, the intra-chunk output and Q' --------------------------
-    {
-        const int mi = wave;
-        const int nks = (16 * mi + 15 >= 32) ? 2 : 1;  // row tile mi of T and M2 is zero past column 16 mi + 15
-        Split8 At[2], Am[2];
+    // ---- 5, 6. [T; M2] x (beta K e^G | beta V) -----------------------------------------------------------
+    const int mi = wave;
+    const int nks = (16 * mi + 15 >= 32) ? 2 : 1;  // row tile mi of T and M2 is zero past column 16 mi + 15
+    Split8 At[2], Am[2];
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            if (s >= nks) continue;
-            float tv[8], mv[8];
-            load8(&sT[(16 * mi + m) * LDT + 32 * s + 8 * grp], tv);
-            load8(&sA[(16 * mi + m) * LDT + 32 * s + 8 * grp], mv);
-            At[s] = split8(tv);
-            Am[s] = split8(mv);
+    for (int s = 0; s < 2; ++s) {
+        if (s >= nks) continue;
+        float tv[8], mv[8];
+        load8(&sT[(16 * mi + m) * LDT + 32 * s + 8 * grp], tv);
+        load8(&sA[(16 * mi + m) * LDT + 32 * s + 8 * grp], mv);
+        At[s] = split8(tv);
+        Am[s] = split8(mv);
+    }
+    float* Ub = ws.U + hc * CK * DV;
+    float* Wb = ws.W + hc * CK * DK;
+    float* Qb = ws.Q + hc * CK * DK;
+    float* Kt = ws.K + hc * DK * CK;
+    const float glast = sG[CK - 1];
+    for (int phase = 0; phase < 2; ++phase) {
+        if (phase == 1) {
+            // beta V replaces the keys (every wave is past its last key read: barrier below)
+            __syncthreads();
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int tok = prow + 8 * j;
+                const float bt = sBeta[tok];
+                *reinterpret_cast<float4*>(&sK[tok * LDK + pc4]) =
+                    make_float4(vr[j].x * bt, vr[j].y * bt, vr[j].z * bt, vr[j].w * bt);
+            }
+            __syncthreads();
         }
-        float* Ub = ws.U + hc * CK * DV;
-        float* Wb = ws.W + hc * CK * DK;
-        float* Qb = ws.Q + hc * CK * DK;
-        for (int ni = 0; ni < DV / 16 + DK / 16; ++ni) {
-            const bool isv = ni < DV / 16;
-            const int col = 16 * (isv ? ni : ni - DV / 16) + m;
+#pragma unroll 1
+        for (int n = 0; n < 8; ++n) {
+            const int col = 16 * n + m;
             f32x4 accT = {0.f, 0.f, 0.f, 0.f}, accM = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
@@ -239,10 +306,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
 #pragma unroll
                 for (int jj = 0; jj < 8; ++jj) {
                     const int tk = 32 * s + 8 * grp + jj;
-                    if (isv)
-                        xb[jj] = tk < len ? a.v[((row0 + tk) * Hv + h) * DV + col] * sBeta[tk] : 0.f;
-                    else
-                        xb[jj] = sK[tk * LDK + col] * sBeta[tk] * sEG[tk];
+                    xb[jj] = phase == 0 ? sK[tk * LDK + col] * sBeta[tk] * sEG[tk] : sK[tk * LDK + col];
                 }
                 const Split8 X = split8(xb);
                 accT = mfma3(At[s], X, accT);
@@ -251,21 +315,24 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int r = 16 * mi + 4 * grp + i;
-                if (isv) {
+                if (phase == 0) {
+                    Wb[r * DK + col] = accT[i];
+                    Qb[r * DK + col] = r < len ? qe[n][i] * sEG[r] - accM[i] : 0.f;
+                } else {
                     Ub[r * DV + col] = accT[i];
                     if (r < len) a.o[((row0 + r) * Hv + h) * DV + col] = accM[i];
-                } else {
-                    Wb[r * DK + col] = accT[i];
-                    Qb[r * DK + col] =
-                        r < len ? a.q[((row0 + r) * Hk + kh) * DK + col] * sRq[r] * sEG[r] - accM[i] : 0.f;
                 }
             }
         }
-        if (tid < CK) {
-            ws.G[hc * 2 * CK + tid] = sG[tid];
-            ws.G[hc * 2 * CK + CK + tid] = sRk[tid];
+        if (phase == 0) {
+            // transposed, decay-scaled keys for the state pass: Kt[r][tok] = k[tok][r] e^{G_last - G_tok}
+            for (int e = tid; e < DK * CK; e += 256) {
+                const int r = e / CK, tok = e % CK;
+                Kt[e] = sK[tok * LDK + r] * __expf(glast - sG[tok]);
+            }
         }
     }
+    if (tid < CK) ws.G[hc * CK + tid] = sG[tid];
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -275,9 +342,7 @@ template <int DK>
 struct StateOps {
     float w[4][8];     // W  rows 16 rt + m, k-slots of this wave (see below)
     float q[4][8];     // Q' rows 16 rt + m, same k-slots
-    float k[2][2][8];  // raw k[token 32 s + 8 grp + j][state row 32 w + 16 rt2 + m]
-    float g[2][8];     // G of those tokens
-    float rk[2][8];    // key normalisers of those tokens
+    float k[2][2][8];  // Kt[state row 32 w + 16 rt2 + m][token 32 s + 8 grp + j]
     float glast;       // G of the chunk's last token
     float4 u;          // U[token 16 w + lane / 4][n0 + 4 (lane % 4) ..]
     float4 o;          // intra-chunk output at the same place
@@ -290,9 +355,8 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(DeltaArgs a, ChunkWs w
     __shared__ __attribute__((aligned(16))) float vn[CK][20];         // Vn for this column block
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int Hv = a.Hv, Hk = a.Hk, T = a.T;
+    const int Hv = a.Hv, T = a.T;
     const int h = blockIdx.x % Hv, cb = blockIdx.x / Hv, b = blockIdx.y;
-    const int kh = h / (Hv / Hk);
     const int n0 = 16 * cb;
     const int slot = a.slot_ids ? a.slot_ids[b] : b;
     const int m = lane & 15, grp = lane >> 4;
@@ -317,7 +381,7 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(DeltaArgs a, ChunkWs w
         const size_t row0 = (size_t)b * T + t0;
         const float* Wb = ws.W + hc * CK * DK;
         const float* Qb = ws.Q + hc * CK * DK;
-        const float* Gb = ws.G + hc * 2 * CK;
+        const float* Kt = ws.K + hc * DK * CK;
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
             const size_t base = (size_t)(16 * rt + m) * DK + 32 * wave + 4 * grp;
@@ -331,19 +395,10 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(DeltaArgs a, ChunkWs w
             op.q[rt][4] = q1.x, op.q[rt][5] = q1.y, op.q[rt][6] = q1.z, op.q[rt][7] = q1.w;
         }
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            load8(Gb + 32 * s + 8 * grp, op.g[s]);
-            load8(Gb + CK + 32 * s + 8 * grp, op.rk[s]);
+        for (int rt2 = 0; rt2 < 2; ++rt2)
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int tok = 32 * s + 8 * grp + j;
-#pragma unroll
-                for (int rt2 = 0; rt2 < 2; ++rt2)
-                    op.k[rt2][s][j] =
-                        tok < len ? a.k[((row0 + tok) * Hk + kh) * DK + 32 * wave + 16 * rt2 + m] : 0.f;
-            }
-        }
-        op.glast = Gb[CK - 1];
+            for (int s = 0; s < 2; ++s) load8(Kt + (size_t)(32 * wave + 16 * rt2 + m) * CK + 32 * s + 8 * grp, op.k[rt2][s]);
+        op.glast = ws.G[hc * CK + CK - 1];
         op.u = *reinterpret_cast<const float4*>(ws.U + hc * CK * DV + (size_t)tk * DV + n0 + c4);
         op.o = tk < len ? *reinterpret_cast<const float4*>(a.o + ((row0 + tk) * Hv + h) * DV + n0 + c4)
                         : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -396,18 +451,12 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(DeltaArgs a, ChunkWs w
         for (int i = 0; i < 4; ++i) s0[i] *= egl, s1[i] *= egl;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            float vb[8], kd[8];
+            float vb[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                vb[j] = vn[32 * s + 8 * grp + j][m];
-                kd[j] = cur.rk[s][j] * __expf(cur.glast - cur.g[s][j]);
-            }
+            for (int j = 0; j < 8; ++j) vb[j] = vn[32 * s + 8 * grp + j][m];
             const Split8 Vb = split8(vb);
-            float k0[8], k1[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) k0[j] = cur.k[0][s][j] * kd[j], k1[j] = cur.k[1][s][j] * kd[j];
-            s0 = mfma3(split8(k0), Vb, s0);
-            s1 = mfma3(split8(k1), Vb, s1);
+            s0 = mfma3(split8(cur.k[0][s]), Vb, s0);
+            s1 = mfma3(split8(cur.k[1][s]), Vb, s1);
         }
         cur = nxt;
     }
@@ -423,7 +472,7 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(DeltaArgs a, ChunkWs w
 
 size_t delta_chunked_workspace(int B, int T, int Hv, int dk, int dv) {
     const size_t NC = (size_t)(T + CK - 1) / CK;
-    return (size_t)B * Hv * NC * ((size_t)CK * dk * 2 + (size_t)CK * dv + 2 * CK) * sizeof(float);
+    return (size_t)B * Hv * NC * ((size_t)CK * dk * 3 + (size_t)CK * dv + CK) * sizeof(float);
 }
 
 bool delta_chunked_supported(int dk, int dv) { return dk == 128 && dv == 128; }
@@ -440,6 +489,7 @@ hipError_t launch_delta_chunked(const DeltaArgs& a, int dk, int dv, void* worksp
     ws.W = p, p += n * CK * dk;
     ws.Q = p, p += n * CK * dk;
     ws.U = p, p += n * CK * dv;
+    ws.K = p, p += n * CK * dk;
     ws.G = p;
     hipLaunchKernelGGL((chunk_prep_kernel<128, 128>), dim3(ws.NC, a.Hv, a.B), dim3(256), 0, stream, a, ws);
     hipError_t e = hipGetLastError();

@@ -13,9 +13,11 @@
 //    barriers in the loop), then the partials are summed through LDS and written once, coalesced.
 //    Activations may come in the same fragment layout (rows padded to 16 with zeros), which turns
 //    every x load into 1 KB of contiguous memory as well.
-//  * gemm_kernel (M > 64, prefill): 128x128x64 LDS-tiled GEMM on v_mfma_f32_32x32x16_bf16, 4 waves of
-//    64x64, register-staged double buffering; tiles are rasterised per XCD in groups of 8 M-tiles so that
-//    workgroups running together on one XCD share A and B tiles in its L2.
+//  * gemm_kernel / gemm256_kernel (M > 64, prefill): LDS-tiled GEMM on v_mfma_f32_32x32x16_bf16 with
+//    register-staged double buffering, 128x128 tiles (4 waves of 64x64) for small problems and 256x256
+//    tiles (8 waves of 128x64) once there are enough tiles to fill the chip;
+//    tiles are rasterised per XCD in groups of 8 M-tiles so that workgroups running together on one
+//    XCD share A and B tiles in its L2.
 #include "gdn_common.h"
 
 namespace gdn {
@@ -270,6 +272,129 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
         }
 }
 
+
+// ------------------------------------------------------------------------------------------------
+// Large GEMM: 256 x 256 x 64 block tile, 8 waves (2 x 4) of 128 x 64, 32x32x16 MFMA.  A and B tiles are
+// double-buffered in LDS (2 x 72 KB, one workgroup per CU) and staged through registers one k-step
+// ahead; two waves per SIMD hide each other's LDS and MFMA latencies.
+// ------------------------------------------------------------------------------------------------
+constexpr int LBM = 256, LBN = 256, LBK = 64, LLD = LBK + 8;
+
+template <int OUT, int WL>
+__global__ __launch_bounds__(512, 2) void gemm256_kernel(const u16* __restrict__ x, const u16* __restrict__ w, int M,
+                                                         int N, int K, void* __restrict__ y) {
+    __shared__ __attribute__((aligned(16))) u16 As[2][LBM * LLD];
+    __shared__ __attribute__((aligned(16))) u16 Bs[2][LBN * LLD];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = tid >> 6;
+    const int wm = wave >> 2, wn = wave & 3;
+
+    const int TM = (M + LBM - 1) / LBM, TN = (N + LBN - 1) / LBN, total = TM * TN;
+    const int id = blockIdx.x, per = total / 8;
+    const int t = id < 8 * per ? (id % 8) * per + id / 8 : id;
+    const int gsz = GROUP_M * TN;
+    const int first_m = (t / gsz) * GROUP_M;
+    const int gm = min(TM - first_m, GROUP_M);
+    const int tm = first_m + (t % gsz) % gm, tn = (t % gsz) / gm;
+    const int m0 = tm * LBM, n0 = tn * LBN;
+
+    // 2048 16-byte pieces per operand tile, 4 per thread
+    u16x8 ra[4], rb[4];
+    const u16* ag[4];
+    const u16* bg[4];
+    int soffa[4], soffb[4];
+    const int NT = (N + 15) >> 4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int c = tid + 512 * j;
+        const int row = c >> 3, col = (c & 7) * 8;
+        ag[j] = x + (size_t)min(m0 + row, M - 1) * K + col;
+        soffa[j] = row * LLD + col;
+        if (WL == W_FRAG) {
+            const int blk = c >> 6, l = c & 63;
+            const int ntl = blk >> 1, kql = blk & 1;
+            bg[j] = w + ((size_t)min((n0 >> 4) + ntl, NT - 1) * (K >> 5) + kql) * 512 + l * 8;
+            soffb[j] = (16 * ntl + (l & 15)) * LLD + 32 * kql + 8 * (l >> 4);
+        } else {
+            bg[j] = w + (size_t)min(n0 + row, N - 1) * K + col;
+            soffb[j] = row * LLD + col;
+        }
+    }
+    constexpr size_t BSTEP = WL == W_FRAG ? 1024 : LBK;
+
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+    const int nk = K / LBK;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        ra[j] = *reinterpret_cast<const u16x8*>(ag[j]);
+        rb[j] = *reinterpret_cast<const u16x8*>(bg[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        *reinterpret_cast<u16x8*>(&As[0][soffa[j]]) = ra[j];
+        *reinterpret_cast<u16x8*>(&Bs[0][soffb[j]]) = rb[j];
+    }
+    __syncthreads();
+
+    const int fr = lane & 31;
+    const int fk = (lane >> 5) * 8;
+    for (int kt = 0; kt < nk; ++kt) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                ra[j] = *reinterpret_cast<const u16x8*>(ag[j] + (size_t)(kt + 1) * LBK);
+                rb[j] = *reinterpret_cast<const u16x8*>(bg[j] + (size_t)(kt + 1) * BSTEP);
+            }
+        }
+        const u16* Ab = &As[cur][(wm * 128 + fr) * LLD + fk];
+        const u16* Bb = &Bs[cur][(wn * 64 + fr) * LLD + fk];
+#pragma unroll
+        for (int kk = 0; kk < LBK; kk += 16) {
+            bf16x8 a[4], b[2];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const bf16x8*>(Ab + i * 32 * LLD + kk);
+#pragma unroll
+            for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const bf16x8*>(Bb + j * 32 * LLD + kk);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+        }
+        if (kt + 1 < nk) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                *reinterpret_cast<u16x8*>(&As[cur ^ 1][soffa[j]]) = ra[j];
+                *reinterpret_cast<u16x8*>(&Bs[cur ^ 1][soffb[j]]) = rb[j];
+            }
+        }
+        __syncthreads();
+    }
+
+    // C layout of 32x32 MFMA: lane l, element e -> row 8*(e/4) + 4*(l/32) + e%4, column l % 32.
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+            if (col >= N) continue;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int row = m0 + wm * 128 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+                if (row < M) store_out<OUT>(y, (size_t)row * N + col, acc[i][j][e]);
+            }
+        }
+}
+
 template <int NTS, int MT, int NW, int WL, int XL>
 hipError_t gemv(const void* x, const void* w, int M, int N, int K, void* y, int out_kind, hipStream_t stream) {
     constexpr int PD = 4;
@@ -318,6 +443,16 @@ hipError_t linear_wl(const void* x, int xlayout, const void* w, int M, int N, in
         return gemv_m<WL, W_ROW>(x, w, M, N, K, y, out_kind, stream);
     }
     if (xlayout != W_ROW) return hipErrorInvalidValue;  // the GEMM reads row-major activations
+    if ((size_t)M * N >= (size_t)256 * 256 * 256) {  // >= one round of 256 x 256 tiles over the CUs
+        const dim3 grid(((M + LBM - 1) / LBM) * ((N + LBN - 1) / LBN));
+        if (out_kind == OUT_F32)
+            hipLaunchKernelGGL((gemm256_kernel<OUT_F32, WL>), grid, dim3(512), 0, stream, (const u16*)x,
+                               (const u16*)w, M, N, K, y);
+        else
+            hipLaunchKernelGGL((gemm256_kernel<OUT_BF16, WL>), grid, dim3(512), 0, stream, (const u16*)x,
+                               (const u16*)w, M, N, K, y);
+        return hipGetLastError();
+    }
     const dim3 grid(((M + TBM - 1) / TBM) * ((N + TBN - 1) / TBN));
     if (out_kind == OUT_F32)
         hipLaunchKernelGGL((gemm_kernel<OUT_F32, WL>), grid, dim3(256), 0, stream, (const u16*)x, (const u16*)w, M,

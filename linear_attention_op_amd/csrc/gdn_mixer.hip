@@ -171,77 +171,112 @@ hipError_t launch_mixer(const MixerArgs& a, int dk, int dv, hipStream_t stream) 
 }
 
 // ------------------------------------------------------------------------------------------------
-// Long-T front end: one workgroup per token row.
+// Long-T front end.  Grid (ceil(T / FTB), nk + ceil(Vd / 256) + 1, B): workgroup (tb, y, b) covers tokens
+// [FTB tb, FTB tb + FTB) of sequence b and, for y < nk, the q | k channels of k-head y (2 dk <= 256
+// channels, L2-normalised), for nk <= y < nk + ceil(Vd / 256) a block of 256 v channels, and for the
+// last y the gating scalars g, beta.  A thread owns one channel and slides its 3-input window down the
+// tokens, so each projection value is read once per block (plus 3 rows of overlap).
 // ------------------------------------------------------------------------------------------------
+constexpr int FTB = 16;
+
 __global__ __launch_bounds__(256) void conv_front_kernel(FrontArgs a) {
-    extern __shared__ float qkbuf[];  // [2 * Kd]: post-conv q | k of this token
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int m = blockIdx.x;
-    const int T = a.T;
-    const int b = m / T, t = m - b * T;
+    __shared__ float part[FTB][4];  // per-token sums of squares per segment of min(dk, 64) channels
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int T = a.T, b = blockIdx.z, y = blockIdx.y;
+    const int t0 = blockIdx.x * FTB, tn = min(FTB, T - t0);
     const int slot = a.slot_ids ? a.slot_ids[b] : b;
     const int nk = a.nk, nv = a.nv, dk = a.dk, dv = a.dv;
     const int ratio = nv / nk;
     const int Kd = nk * dk, Vd = nv * dv, CD = 2 * Kd + Vd, CH = 2 * dk + dv;
-    const float* Prow = a.P + (size_t)m * a.NP;
+    const size_t row0 = (size_t)b * T + t0;
+    const int nvb = (Vd + 255) / 256;
 
-    for (int col = tid; col < CD; col += 256) {
-        // history holding this column: q/k of k-head kh are read from the copy of v-head kh * ratio
-        int hcopy, local;
-        if (col < Kd) {
-            const int kh = col / dk;
-            hcopy = kh * ratio, local = col - kh * dk;
-        } else if (col < 2 * Kd) {
-            const int kh = (col - Kd) / dk;
-            hcopy = kh * ratio, local = dk + (col - Kd - kh * dk);
-        } else {
-            const int hh = (col - 2 * Kd) / dv;
-            hcopy = hh, local = 2 * dk + (col - 2 * Kd - hh * dv);
+    if (y == nk + nvb) {  // gating scalars of this token block
+        for (int e = tid; e < tn * nv; e += 256) {
+            const int t = e / nv, hh = e % nv;
+            const float* Prow = a.P + (row0 + t) * a.NP;
+            a.g[(row0 + t) * nv + hh] = a.neg_A[hh] * softplusf_(Prow[CD + Vd + hh] + a.dt_bias[hh]);
+            a.beta[(row0 + t) * nv + hh] = sigmoidf_(Prow[CD + Vd + nv + hh]);
         }
+        return;
+    }
+
+    // this thread's channel: projection column, and where its history lives
+    const bool isqk = y < nk;
+    bool active;
+    int col = 0, hcopy = 0, local = 0, vc = 0;
+    if (isqk) {
+        const int kh = y, c = tid;  // c < dk: q channel c; dk <= c < 2 dk: k channel c - dk
+        active = c < 2 * dk;
+        col = c < dk ? kh * dk + c : Kd + kh * dk + (c - dk);
+        hcopy = kh * ratio, local = c;
+    } else {
+        vc = (y - nk) * 256 + tid;
+        active = vc < Vd;
+        const int hh = vc / dv;
+        col = 2 * Kd + vc;
+        hcopy = hh, local = 2 * dk + (vc - hh * dv);
+    }
+    float out[FTB];
+#pragma unroll
+    for (int t = 0; t < FTB; ++t) out[t] = 0.f;
+    if (active) {
         const float4 w = a.conv_w[col];
+        // window: inputs at t0 - 3, t0 - 2, t0 - 1 (history entries for times before 0)
+        const float* hist = a.conv_state + ((size_t)slot * nv + hcopy) * 3 * CH;
         float xs[3];
 #pragma unroll
         for (int s = 3; s >= 1; --s) {
-            float xv;
-            if (t >= s) {
-                xv = (Prow - (size_t)s * a.NP)[col];
-            } else {
-                const float* hist = a.conv_state + ((size_t)slot * nv + hcopy) * 3 * CH;
-                xv = hist[(3 + t - s) * CH + local];  // input at time t - s < 0 is history entry 3 + t - s
-            }
-            xs[3 - s] = xv;
+            const int ts = t0 - s;
+            xs[3 - s] = ts >= 0 ? a.P[(row0 - s) * a.NP + col] : hist[(3 + ts) * CH + local];
         }
-        const float acc = w.x * xs[0] + w.y * xs[1] + w.z * xs[2] + w.w * Prow[col];
-        const float out = siluf_(acc);
-        if (col < 2 * Kd)
-            qkbuf[col] = out;
-        else
-            a.v[(size_t)m * Vd + (col - 2 * Kd)] = out;
+        float x0 = xs[0], x1 = xs[1], x2 = xs[2];
+#pragma unroll
+        for (int t = 0; t < FTB; ++t) {
+            if (t < tn) {
+                const float xin = a.P[(row0 + t) * a.NP + col];
+                out[t] = siluf_(w.x * x0 + w.y * x1 + w.z * x2 + w.w * xin);
+                x0 = x1, x1 = x2, x2 = xin;
+            }
+        }
+    }
+    if (!isqk) {
+        if (active)
+#pragma unroll
+            for (int t = 0; t < FTB; ++t)
+                if (t < tn) a.v[(row0 + t) * Vd + vc] = out[t];
+        return;
+    }
+    // L2 norms of q (channels 0 .. dk-1) and k (dk .. 2dk-1) per token: segments of min(dk, 64) lanes
+    const int seg = dk < 64 ? dk : 64;
+#pragma unroll
+    for (int t = 0; t < FTB; ++t) {
+        float ss = out[t] * out[t];
+        for (int off = 1; off < seg; off <<= 1) ss += __shfl_xor(ss, off, 64);
+        if (active && (lane % seg) == 0) part[t][tid / seg] = ss;
     }
     __syncthreads();
-    const float qscale = rsqrtf((float)dk);
-    for (int task = wave; task < 2 * nk; task += 4) {
-        const float* src = qkbuf + task * dk;  // task < nk: q of head task; else k of head task - nk
-        float ss = 0.f;
-        for (int i = lane; i < dk; i += 64) ss += src[i] * src[i];
-        ss = warp_sum(ss);
-        const bool isq = task < nk;
-        const float r = rsqrtf(ss + 1e-6f) * (isq ? qscale : 1.f);
-        float* dst = (isq ? a.qn + (size_t)m * Kd + task * dk : a.kn + (size_t)m * Kd + (task - nk) * dk);
-        for (int i = lane; i < dk; i += 64) dst[i] = src[i] * r;
-    }
-    for (int hh = tid; hh < nv; hh += 256) {
-        const float av = Prow[CD + Vd + hh], bv = Prow[CD + Vd + nv + hh];
-        a.g[(size_t)m * nv + hh] = a.neg_A[hh] * softplusf_(av + a.dt_bias[hh]);
-        a.beta[(size_t)m * nv + hh] = sigmoidf_(bv);
+    if (!active) return;
+    const bool isq = tid < dk;
+    const int kh = y, c = isq ? tid : tid - dk;
+    const int nseg = dk / seg, s0 = isq ? 0 : nseg;  // q: segments [0, nseg), k: [nseg, 2 nseg)
+    const float qscale = isq ? rsqrtf((float)dk) : 1.f;
+    float* dst = (isq ? a.qn : a.kn) + row0 * Kd + kh * dk + c;
+#pragma unroll
+    for (int t = 0; t < FTB; ++t) {
+        if (t < tn) {
+            float ss = 0.f;
+            for (int j = 0; j < nseg; ++j) ss += part[t][s0 + j];
+            dst[(size_t)t * Kd] = out[t] * rsqrtf(ss + 1e-6f) * qscale;
+        }
     }
 }
 
 hipError_t launch_conv_front(const FrontArgs& a, hipStream_t stream) {
-    const int M = a.B * a.T;
-    if (M <= 0) return hipSuccess;
-    const size_t lds = sizeof(float) * 2 * a.nk * a.dk;
-    hipLaunchKernelGGL(conv_front_kernel, dim3(M), dim3(256), lds, stream, a);
+    if (a.B <= 0 || a.T <= 0) return hipSuccess;
+    if (2 * a.dk > 256) return hipErrorInvalidValue;  // one q | k channel group per workgroup
+    const dim3 grid((a.T + FTB - 1) / FTB, a.nk + (a.nv * a.dv + 255) / 256 + 1, a.B);
+    hipLaunchKernelGGL(conv_front_kernel, grid, dim3(256), 0, stream, a);
     return hipGetLastError();
 }
 

@@ -29,6 +29,7 @@ def rel(a, b):
 @pytest.mark.parametrize("M, N, K", [
     (1, 392, 256), (3, 4096, 4096), (16, 12352, 4096), (17, 1024, 2048), (40, 8224, 1024), (64, 12352, 4096),
     (64, 4096, 4096), (65, 392, 256), (200, 4096, 1024), (512, 12352, 4096), (300, 1000, 128),
+    (2048, 8224, 1024), (4096, 4096, 512), (1030, 16400, 256),
 ])
 def test_linear(M, N, K):
     print(f"linear M={M} N={N} K={K}", flush=True)
@@ -116,3 +117,25 @@ def test_unsupported_head_dims_raise():
     op = GatedDeltaRuleHIP(B * Hv, dk, dv)
     with pytest.raises(GdnValueError):
         op(*[torch.from_numpy(f[n]) for n in ("q", "k", "v", "g", "beta")])
+
+
+@pytest.mark.parametrize("M", [64, 2048])
+def test_in_proj_fragment_weights_against_fp64(M):
+    """The layer's in_proj (weights in MFMA-fragment layout; GEMV at M = 64, 256x256-tile GEMM at
+    M = 2048) against an fp64 product of the same bf16 operands."""
+    from linear_attention_op_amd import Qwen35GatedDeltaNetHIP
+    from linear_attention_op_amd import synthetic as syn
+    d = syn.SHAPES["9b"]
+    w, gen = syn.make_weights(d, seed=5)
+    layer = Qwen35GatedDeltaNetHIP(w, dims=d, batch=1, max_tokens=M)
+    x = torch.randn(M, d["hidden"], generator=gen).bfloat16()
+    P = layer.in_proj(x.cuda())
+    wcat = torch.cat([w["w_qkv"], w["w_z"], w["w_a"], w["w_b"]]).cuda().double()
+    want = x.cuda().double() @ wcat.T
+    torch.cuda.synchronize()
+    assert rel(P, want) < 1e-5
+    y = torch.randn(M, d["num_v_heads"] * 128, generator=gen).bfloat16()
+    out = layer.out_proj(y.cuda())
+    want = y.cuda().double() @ w["w_out"].cuda().double().T
+    torch.cuda.synchronize()
+    assert rel(out.float(), want) < 5e-3
