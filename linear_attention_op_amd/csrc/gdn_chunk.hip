@@ -40,14 +40,23 @@ __device__ __forceinline__ void load8(const float* p, float* v) {
     v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
 }
 
+// The key tile is stored split, as bf16 hi and lo planes (x = hi + lo), which the state pass feeds to
+// the MFMAs without converting; W and Q' are fp32, split by the state pass.
 struct ChunkWs {
     float* W;   // [B, Hv, NC, CK, dk]
     float* Q;   // [B, Hv, NC, CK, dk]   Q'
+    u16* Kh;    // [B, Hv, NC, dk, CK]   normalised keys, transposed, scaled by e^{G_last - G}
+    u16* Kl;
     float* U;   // [B, Hv, NC, CK, dv]
-    float* K;   // [B, Hv, NC, dk, CK]   normalised keys, transposed, scaled by e^{G_last - G}
     float* G;   // [B, Hv, NC, CK]       G (in-chunk cumulative log decay)
     int NC;     // chunks per sequence
 };
+
+__device__ __forceinline__ void split_store(u16* hi, u16* lo, size_t i, float x) {
+    const u16 h = f2bf(x);
+    hi[i] = h;
+    lo[i] = f2bf(x - bf2f(h));
+}
 
 // ------------------------------------------------------------------------------------------------
 // chunk_prep_kernel: grid (NC, Hv, B), 256 threads.
@@ -278,58 +287,66 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
         Am[s] = split8(mv);
     }
     float* Ub = ws.U + hc * CK * DV;
-    float* Wb = ws.W + hc * CK * DK;
-    float* Qb = ws.Q + hc * CK * DK;
-    float* Kt = ws.K + hc * DK * CK;
+    const size_t wq0 = hc * CK * DK, kt0 = hc * DK * CK;
     const float glast = sG[CK - 1];
-    for (int phase = 0; phase < 2; ++phase) {
-        if (phase == 1) {
-            // beta V replaces the keys (every wave is past its last key read: barrier below)
-            __syncthreads();
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int tok = prow + 8 * j;
-                const float bt = sBeta[tok];
-                *reinterpret_cast<float4*>(&sK[tok * LDK + pc4]) =
-                    make_float4(vr[j].x * bt, vr[j].y * bt, vr[j].z * bt, vr[j].w * bt);
-            }
-            __syncthreads();
-        }
 #pragma unroll 1
-        for (int n = 0; n < 8; ++n) {
-            const int col = 16 * n + m;
-            f32x4 accT = {0.f, 0.f, 0.f, 0.f}, accM = {0.f, 0.f, 0.f, 0.f};
+    for (int n = 0; n < 8; ++n) {
+        const int col = 16 * n + m;
+        f32x4 accT = {0.f, 0.f, 0.f, 0.f}, accM = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                if (s >= nks) continue;
-                float xb[8];
+        for (int s = 0; s < 2; ++s) {
+            if (s >= nks) continue;
+            float xb[8];
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj) {
-                    const int tk = 32 * s + 8 * grp + jj;
-                    xb[jj] = phase == 0 ? sK[tk * LDK + col] * sBeta[tk] * sEG[tk] : sK[tk * LDK + col];
-                }
-                const Split8 X = split8(xb);
-                accT = mfma3(At[s], X, accT);
-                accM = mfma3(Am[s], X, accM);
+            for (int jj = 0; jj < 8; ++jj) {
+                const int tk = 32 * s + 8 * grp + jj;
+                xb[jj] = sK[tk * LDK + col] * sBeta[tk] * sEG[tk];
             }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int r = 16 * mi + 4 * grp + i;
-                if (phase == 0) {
-                    Wb[r * DK + col] = accT[i];
-                    Qb[r * DK + col] = r < len ? qe[n][i] * sEG[r] - accM[i] : 0.f;
-                } else {
-                    Ub[r * DV + col] = accT[i];
-                    if (r < len) a.o[((row0 + r) * Hv + h) * DV + col] = accM[i];
-                }
-            }
+            const Split8 X = split8(xb);
+            accT = mfma3(At[s], X, accT);
+            accM = mfma3(Am[s], X, accM);
         }
-        if (phase == 0) {
-            // transposed, decay-scaled keys for the state pass: Kt[r][tok] = k[tok][r] e^{G_last - G_tok}
-            for (int e = tid; e < DK * CK; e += 256) {
-                const int r = e / CK, tok = e % CK;
-                Kt[e] = sK[tok * LDK + r] * __expf(glast - sG[tok]);
-            }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 16 * mi + 4 * grp + i;
+            ws.W[wq0 + (size_t)r * DK + col] = accT[i];
+            ws.Q[wq0 + (size_t)r * DK + col] = r < len ? qe[n][i] * sEG[r] - accM[i] : 0.f;
+        }
+    }
+    // transposed, decay-scaled keys for the state pass: Kt[r][tok] = k[tok][r] e^{G_last - G_tok}
+    for (int e = tid; e < DK * CK; e += 256) {
+        const int r = e / CK, tok = e % CK;
+        split_store(ws.Kh, ws.Kl, kt0 + e, sK[tok * LDK + r] * __expf(glast - sG[tok]));
+    }
+    // beta V replaces the keys
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int tok = prow + 8 * j;
+        const float bt = sBeta[tok];
+        *reinterpret_cast<float4*>(&sK[tok * LDK + pc4]) =
+            make_float4(vr[j].x * bt, vr[j].y * bt, vr[j].z * bt, vr[j].w * bt);
+    }
+    __syncthreads();
+#pragma unroll 1
+    for (int n = 0; n < 8; ++n) {
+        const int col = 16 * n + m;
+        f32x4 accT = {0.f, 0.f, 0.f, 0.f}, accM = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+            if (s >= nks) continue;
+            float xb[8];
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) xb[jj] = sK[(32 * s + 8 * grp + jj) * LDK + col];
+            const Split8 X = split8(xb);
+            accT = mfma3(At[s], X, accT);
+            accM = mfma3(Am[s], X, accM);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 16 * mi + 4 * grp + i;
+            Ub[r * DV + col] = accT[i];
+            if (r < len) a.o[((row0 + r) * Hv + h) * DV + col] = accM[i];
         }
     }
     if (tid < CK) ws.G[hc * CK + tid] = sG[tid];
@@ -340,12 +357,12 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
 // ------------------------------------------------------------------------------------------------
 template <int DK>
 struct StateOps {
-    float w[4][8];     // W  rows 16 rt + m, k-slots of this wave (see below)
-    float q[4][8];     // Q' rows 16 rt + m, same k-slots
-    float k[2][2][8];  // Kt[state row 32 w + 16 rt2 + m][token 32 s + 8 grp + j]
-    float glast;       // G of the chunk's last token
-    float4 u;          // U[token 16 w + lane / 4][n0 + 4 (lane % 4) ..]
-    float4 o;          // intra-chunk output at the same place
+    float w[4][8];          // W  rows 16 rt + m, the 8 k-slots of this lane (see below)
+    float q[4][8];          // Q' rows 16 rt + m, same k-slots
+    bf16x8 kh[2][2], kl[2][2];  // key tile rows 32 w + 16 rt2 + m, tokens 32 s + 8 grp ..
+    float glast;            // G of the chunk's last token
+    float4 u;               // U[token 16 w + lane / 4][n0 + 4 (lane % 4) ..]
+    float4 o;               // intra-chunk output at the same place
 };
 
 template <int DK, int DV>
@@ -379,16 +396,14 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(DeltaArgs a, ChunkWs w
         const size_t hc = ((size_t)b * Hv + h) * ws.NC + c;
         const int t0 = c * CK, len = min(CK, T - t0);
         const size_t row0 = (size_t)b * T + t0;
-        const float* Wb = ws.W + hc * CK * DK;
-        const float* Qb = ws.Q + hc * CK * DK;
-        const float* Kt = ws.K + hc * DK * CK;
+        const size_t wq = hc * CK * DK + 32 * wave + 4 * grp, kt = hc * DK * CK + 8 * grp;
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
-            const size_t base = (size_t)(16 * rt + m) * DK + 32 * wave + 4 * grp;
-            const float4 w0 = *reinterpret_cast<const float4*>(Wb + base);
-            const float4 w1 = *reinterpret_cast<const float4*>(Wb + base + 16);
-            const float4 q0 = *reinterpret_cast<const float4*>(Qb + base);
-            const float4 q1 = *reinterpret_cast<const float4*>(Qb + base + 16);
+            const size_t e = wq + (size_t)(16 * rt + m) * DK;
+            const float4 w0 = *reinterpret_cast<const float4*>(ws.W + e);
+            const float4 w1 = *reinterpret_cast<const float4*>(ws.W + e + 16);
+            const float4 q0 = *reinterpret_cast<const float4*>(ws.Q + e);
+            const float4 q1 = *reinterpret_cast<const float4*>(ws.Q + e + 16);
             op.w[rt][0] = w0.x, op.w[rt][1] = w0.y, op.w[rt][2] = w0.z, op.w[rt][3] = w0.w;
             op.w[rt][4] = w1.x, op.w[rt][5] = w1.y, op.w[rt][6] = w1.z, op.w[rt][7] = w1.w;
             op.q[rt][0] = q0.x, op.q[rt][1] = q0.y, op.q[rt][2] = q0.z, op.q[rt][3] = q0.w;
@@ -397,17 +412,18 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(DeltaArgs a, ChunkWs w
 #pragma unroll
         for (int rt2 = 0; rt2 < 2; ++rt2)
 #pragma unroll
-            for (int s = 0; s < 2; ++s) load8(Kt + (size_t)(32 * wave + 16 * rt2 + m) * CK + 32 * s + 8 * grp, op.k[rt2][s]);
+            for (int s = 0; s < 2; ++s) {
+                const size_t e = kt + (size_t)(32 * wave + 16 * rt2 + m) * CK + 32 * s;
+                op.kh[rt2][s] = *reinterpret_cast<const bf16x8*>(ws.Kh + e);
+                op.kl[rt2][s] = *reinterpret_cast<const bf16x8*>(ws.Kl + e);
+            }
         op.glast = ws.G[hc * CK + CK - 1];
         op.u = *reinterpret_cast<const float4*>(ws.U + hc * CK * DV + (size_t)tk * DV + n0 + c4);
         op.o = tk < len ? *reinterpret_cast<const float4*>(a.o + ((row0 + tk) * Hv + h) * DV + n0 + c4)
                         : make_float4(0.f, 0.f, 0.f, 0.f);
     };
 
-    StateOps<DK> cur, nxt;
-    load_ops(0, cur);
-    for (int c = 0; c < NC; ++c) {
-        if (c + 1 < NC) load_ops(c + 1, nxt);
+    auto step = [&](int c, const StateOps<DK>& cur) {
         const int t0 = c * CK, len = min(CK, T - t0);
         const size_t row0 = (size_t)b * T + t0;
 
@@ -455,10 +471,24 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(DeltaArgs a, ChunkWs w
 #pragma unroll
             for (int j = 0; j < 8; ++j) vb[j] = vn[32 * s + 8 * grp + j][m];
             const Split8 Vb = split8(vb);
-            s0 = mfma3(split8(cur.k[0][s]), Vb, s0);
-            s1 = mfma3(split8(cur.k[1][s]), Vb, s1);
+            s0 = mfma3(Split8{cur.kh[0][s], cur.kl[0][s]}, Vb, s0);
+            s1 = mfma3(Split8{cur.kh[1][s], cur.kl[1][s]}, Vb, s1);
         }
-        cur = nxt;
+    };
+
+    // operands two chunks ahead: a 3-slot ring, unrolled so that every slot is a fixed set of registers
+    StateOps<DK> A, B, C;
+    load_ops(0, A);
+    if (NC > 1) load_ops(1, B);
+    for (int c = 0; c < NC; c += 3) {
+        if (c + 2 < NC) load_ops(c + 2, C);
+        step(c, A);
+        if (c + 1 >= NC) break;
+        if (c + 3 < NC) load_ops(c + 3, A);
+        step(c + 1, B);
+        if (c + 2 >= NC) break;
+        if (c + 4 < NC) load_ops(c + 4, B);
+        step(c + 2, C);
     }
 
 #pragma unroll
@@ -472,6 +502,7 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(DeltaArgs a, ChunkWs w
 
 size_t delta_chunked_workspace(int B, int T, int Hv, int dk, int dv) {
     const size_t NC = (size_t)(T + CK - 1) / CK;
+    // W, Q': fp32; keys: hi + lo bf16 (= 4 bytes per value); U, G: fp32
     return (size_t)B * Hv * NC * ((size_t)CK * dk * 3 + (size_t)CK * dv + CK) * sizeof(float);
 }
 
@@ -485,12 +516,15 @@ hipError_t launch_delta_chunked(const DeltaArgs& a, int dk, int dv, void* worksp
     ChunkWs ws;
     ws.NC = (a.T + CK - 1) / CK;
     const size_t n = (size_t)a.B * a.Hv * ws.NC;
-    float* p = static_cast<float*>(workspace);
-    ws.W = p, p += n * CK * dk;
-    ws.Q = p, p += n * CK * dk;
-    ws.U = p, p += n * CK * dv;
-    ws.K = p, p += n * CK * dk;
-    ws.G = p;
+    float* f = static_cast<float*>(workspace);
+    ws.W = f, f += n * CK * dk;
+    ws.Q = f, f += n * CK * dk;
+    u16* p = reinterpret_cast<u16*>(f);
+    ws.Kh = p, p += n * CK * dk;
+    ws.Kl = p, p += n * CK * dk;
+    f = reinterpret_cast<float*>(p);
+    ws.U = f, f += n * CK * dv;
+    ws.G = f;
     hipLaunchKernelGGL((chunk_prep_kernel<128, 128>), dim3(ws.NC, a.Hv, a.B), dim3(256), 0, stream, a, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
