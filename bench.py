@@ -83,7 +83,82 @@ def cpu_baseline(d, w_np, B, seconds, gen_seed=2):
             "sample": f"{steps} decode steps of the 9B layer at batch {B} (fp64 oracle, {el:.1f} s)"}
 
 
+CAL_BYTES = 1 << 30      # the calibration copy in the counter passes
+
+
+def pmc_child(steps=4):
+    """Workload of one counter pass: a 1 GiB device copy (calibrates the counter against bytes that are
+    known to move), then `steps` decode steps of one 9B-shape layer at batch 64."""
+    import torch
+
+    from linear_attention_op_amd import Qwen35GatedDeltaNetHIP
+    from linear_attention_op_amd import synthetic as syn
+
+    dev = torch.device("cuda", 0)
+    src = torch.ones(CAL_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    d = syn.SHAPES["9b"]
+    w, _ = syn.make_weights(d, seed=2)
+    lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=64, max_tokens=64)
+    lay.set_state(rec=torch.randn(64, d["num_v_heads"], 128, 128, device=dev) * 0.01)
+    x = torch.randn(64, 1, d["hidden"], device=dev).to(torch.bfloat16)
+    for _ in range(steps):
+        lay(x)
+    torch.cuda.synchronize()
+    lay.close()
+
+
+def measure_traffic(kernel="mixer_kernel", timeout=180):
+    """HBM bytes per launch of `kernel` from two rocprofv3 counter passes over `pmc_child` (FETCH_SIZE,
+    then WRITE_SIZE, KiB per dispatch), each scaled by what the same counter reads for the 1 GiB copy.
+    Runs before this process touches the GPU.  Returns (traffic dict, None) or (None, reason)."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        return None, "rocprofv3 not found"
+    out = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        tmp = tempfile.mkdtemp(prefix="gdn_pmc_", dir="/tmp")
+        cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", tmp, "-o", "run", "--",
+               sys.executable, os.path.abspath(__file__), "--pmc-child"]
+        env = dict(os.environ, TMPDIR="/tmp")
+        print(f"[bench] counter pass {counter}", file=sys.stderr, flush=True)
+        try:
+            r = subprocess.run(cmd, cwd="/tmp", env=env, timeout=timeout, stdout=subprocess.DEVNULL,
+                               stderr=subprocess.PIPE, text=True)
+        except subprocess.TimeoutExpired:
+            return None, f"{counter} pass timed out"
+        rows = []
+        for root, _, files in os.walk(tmp):
+            for f in files:
+                if f.endswith("counter_collection.csv"):
+                    with open(os.path.join(root, f)) as fh:
+                        rows += list(csv.DictReader(fh))
+        shutil.rmtree(tmp, ignore_errors=True)
+        if not rows:
+            return None, f"{counter} pass wrote no counters (rc {r.returncode}): {r.stderr[-300:]}"
+        cal = max((float(x["Counter_Value"]) for x in rows if "copyBuffer" in x["Kernel_Name"]), default=0.0)
+        vals = [float(x["Counter_Value"]) for x in rows if kernel in x["Kernel_Name"]]
+        if cal <= 0 or not vals:
+            return None, f"{counter} pass: no calibration copy or no {kernel} dispatch"
+        scale = CAL_BYTES / (cal * 1024)        # bytes per counted KiB
+        out[counter] = {"kib_per_dispatch": sum(vals) / len(vals), "scale": scale, "dispatches": len(vals),
+                        "bytes": sum(vals) / len(vals) * 1024 * scale}
+    return {"bytes": out["FETCH_SIZE"]["bytes"] + out["WRITE_SIZE"]["bytes"], "passes": out}, None
+
+
 def main():
+    if "--pmc-child" in sys.argv:
+        pmc_child()
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
@@ -97,12 +172,18 @@ def main():
     ap.add_argument("--graph", type=int, default=0,
                     help="1: replay the decode step from HIP graphs; 0: launch eagerly (faster here: 104 vs 112 us)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the two rocprofv3 counter passes (required when bench.py itself runs under rocprofv3)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the layer shards by v-head "
               "or by sequence across GPUs only in design); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+
+    traffic, traffic_note = (None, "skipped (--no-traffic)") if args.no_traffic else measure_traffic()
+    if traffic_note:
+        print(f"[bench] traffic: {traffic_note}", file=sys.stderr, flush=True)
 
     import torch
 
@@ -190,8 +271,10 @@ def main():
     mix_bytes = B * mixer_bytes_per_seq(d)
     mix_s = stage_avg_ms["mixer"] / 1e3
     roofline = {"bound": "hbm", "achieved": mix_bytes / mix_s / 1e9, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-                "frac": mix_bytes / mix_s / HBM_PEAK, "traffic": None, "kernel": "mixer_kernel<128,128>",
-                "bytes_per_launch": mix_bytes, "avg_launch_us": stage_avg_ms["mixer"] * 1e3}
+                "frac": mix_bytes / mix_s / HBM_PEAK, "traffic": traffic["bytes"] if traffic else None,
+                "kernel": "mixer_kernel<128,128>", "bytes_per_launch": mix_bytes,
+                "avg_launch_us": stage_avg_ms["mixer"] * 1e3,
+                "traffic_detail": traffic["passes"] if traffic else traffic_note}
     layer_roof = {"bytes_per_step": step_bytes, "achieved_GBps": step_bytes / (ms_per_step / 1e3) / 1e9,
                   "frac": step_bytes / (ms_per_step / 1e3) / HBM_PEAK,
                   "event_step_us": stage_avg_ms["total"] * 1e3,

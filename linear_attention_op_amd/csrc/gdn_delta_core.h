@@ -29,13 +29,21 @@ struct DeltaTile {
         cg = tid % CG;
         rg = tid / CG;
     }
+    // The state is streamed: read once and written once per launch, so both directions use
+    // non-temporal accesses and do not displace the projection weights from the caches.
     __device__ __forceinline__ void load(const float* S) {
 #pragma unroll
-        for (int i = 0; i < RPT; ++i) s[i] = *reinterpret_cast<const float4*>(S + (size_t)(rg + RG * i) * DV + 4 * cg);
+        for (int i = 0; i < RPT; ++i) {
+            const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(S + (size_t)(rg + RG * i) * DV + 4 * cg));
+            s[i] = make_float4(v[0], v[1], v[2], v[3]);
+        }
     }
     __device__ __forceinline__ void store(float* S) const {
 #pragma unroll
-        for (int i = 0; i < RPT; ++i) *reinterpret_cast<float4*>(S + (size_t)(rg + RG * i) * DV + 4 * cg) = s[i];
+        for (int i = 0; i < RPT; ++i) {
+            const f32x4 v = {s[i].x, s[i].y, s[i].z, s[i].w};
+            __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(S + (size_t)(rg + RG * i) * DV + 4 * cg));
+        }
     }
 
     // red: LDS scratch [NWAVES][2][DV].  Returns o for this thread's 4 columns (every thread gets its

@@ -51,6 +51,12 @@ __global__ void frag_tile_kernel(const u16* __restrict__ w, int N, int K, u16* _
 // ------------------------------------------------------------------------------------------------
 // GEMV: M <= 16 MT
 // ------------------------------------------------------------------------------------------------
+// Weight fragments are read once per call: non-temporal loads, so they do not evict the activations
+// every workgroup re-reads.
+__device__ __forceinline__ bf16x8 ldw(const u16* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(p));
+}
+
 template <int NTS, int MT, int NW, int PD, int OUT, int WL, int XL>
 __global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x, const u16* __restrict__ w, int M,
                                                       int N, int K, void* __restrict__ y) {
@@ -97,7 +103,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x
     for (int j = 0; j < PD; ++j) {
         if (j < nsteps) {
 #pragma unroll
-            for (int t = 0; t < NTS; ++t) wb[j][t] = *reinterpret_cast<const bf16x8*>(wp[t] + j * WSTEP);
+            for (int t = 0; t < NTS; ++t) wb[j][t] = ldw(wp[t] + j * WSTEP);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) xb[j][mt] = xv[mt] ? *reinterpret_cast<const bf16x8*>(xp[mt] + j * XSTEP) : zero8;
         }
@@ -119,8 +125,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x
                     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = mfma16(wb[j][t], xb[j][mt], acc[t][mt]);
                 if (s + PD < nsteps) {
 #pragma unroll
-                    for (int t = 0; t < NTS; ++t)
-                        wb[j][t] = *reinterpret_cast<const bf16x8*>(wp[t] + (size_t)(s + PD) * WSTEP);
+                    for (int t = 0; t < NTS; ++t) wb[j][t] = ldw(wp[t] + (size_t)(s + PD) * WSTEP);
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt)
                         xb[j][mt] = xv[mt] ? *reinterpret_cast<const bf16x8*>(xp[mt] + (size_t)(s + PD) * XSTEP) : zero8;
