@@ -18,14 +18,16 @@
 //    S: G, L, T, U, W, Q', the decay-scaled transposed keys and the intra-chunk output Aqk U (written
 //    straight into o).
 //  * chunk_state_kernel: the sequential pass over chunks.  A workgroup owns 16 value columns of one
-//    (sequence, v-head) state; its four waves own 32 state rows each, held in MFMA accumulators for the
+//    (sequence, v-head) state; its eight waves own 16 state rows each, held in MFMA accumulators for the
 //    whole launch (state read once, written once).  Per chunk: W S and Q' S (partials over the waves'
-//    rows, summed through LDS), Vn, O += Q' S, S update.  The next chunk's operands are loaded while the
-//    current one is computed.  Workgroup ids put the 8 column blocks of a head on one XCD so that they
+//    rows, summed through LDS), Vn, O += Q' S, S update.  The operands of the next two chunks are in
+//    flight while the current one is computed.  Workgroup ids put the 8 column blocks of a head on one XCD so that they
 //    share that XCD's L2 copy of W, Q' and the keys.
 //
 // Precision: every product that feeds the state or the output goes through split bf16 (hi + lo, three
 // MFMAs, ~2^-17 relative), so the chunked state matches the fp32 sequential rule to ~1e-5.
+#include <type_traits>
+
 #include "gdn_common.h"
 
 namespace gdn {
@@ -353,23 +355,50 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
 }
 
 // ------------------------------------------------------------------------------------------------
-// chunk_state_kernel: grid (Hv * DV / 16, B), 256 threads.  blockIdx.x = cb * Hv + h.
+// chunk_state_kernel: grid (Hv * DV / 16, B), 512 threads.  blockIdx.x = cb * Hv + h.
 // ------------------------------------------------------------------------------------------------
-template <int DK>
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// v_mfma_f32_16x16x16_bf16: lane l holds A[l % 16][4 (l / 16) + j] and B[4 (l / 16) + j][l % 16], j < 4;
+// C as for the 16x16x32 form.
+__device__ __forceinline__ f32x4 mfma16k16(s16x4 a, s16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+struct Split4 {
+    s16x4 h, l;
+};
+__device__ __forceinline__ Split4 split4(const f32x4 v) {
+    Split4 r;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const __bf16 hi = (__bf16)v[j];
+        r.h[j] = __builtin_bit_cast(short, hi);
+        r.l[j] = __builtin_bit_cast(short, (__bf16)(v[j] - (float)hi));
+    }
+    return r;
+}
+__device__ __forceinline__ f32x4 mfma3k16(const Split4& a, const Split4& b, f32x4 c) {
+    c = mfma16k16(a.l, b.h, c);
+    c = mfma16k16(a.h, b.l, c);
+    return mfma16k16(a.h, b.h, c);
+}
+
+// One chunk's operands for one lane (about 50 VGPRs, so three chunks fit in registers).
 struct StateOps {
-    float w[4][8];          // W  rows 16 rt + m, the 8 k-slots of this lane (see below)
-    float q[4][8];          // Q' rows 16 rt + m, same k-slots
-    bf16x8 kh[2][2], kl[2][2];  // key tile rows 32 w + 16 rt2 + m, tokens 32 s + 8 grp ..
-    float glast;            // G of the chunk's last token
-    float4 u;               // U[token 16 w + lane / 4][n0 + 4 (lane % 4) ..]
-    float4 o;               // intra-chunk output at the same place
+    f32x4 w[4];           // W  [16 rt + m][16 wave + 4 grp + j]
+    f32x4 q[4];           // Q' at the same place
+    bf16x8 kh[2], kl[2];  // key tile [16 wave + m][32 s + 8 grp + j] (hi / lo)
+    float glast;          // G of the chunk's last token
+    float2 u;             // U[tk][n0 + c2 ..]
+    float2 o;             // intra-chunk output at the same place
 };
 
 template <int DK, int DV>
-__global__ __launch_bounds__(256) void chunk_state_kernel(DeltaArgs a, ChunkWs ws) {
+__global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs ws) {
     static_assert(DK == 128 && DV == 128, "chunked path is specialised for 128-wide heads");
-    __shared__ __attribute__((aligned(16))) float red[4][2][CK][16];  // per-wave partials of W S and Q' S
-    __shared__ __attribute__((aligned(16))) float vn[CK][20];         // Vn for this column block
+    constexpr int NWV = 8, VP = 17;
+    __shared__ __attribute__((aligned(16))) float red[NWV][2][CK][16];  // per-wave partials of W S, Q' S
+    __shared__ float vn[CK][VP];                                       // Vn for this column block
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int Hv = a.Hv, T = a.T;
@@ -378,63 +407,52 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(DeltaArgs a, ChunkWs w
     const int slot = a.slot_ids ? a.slot_ids[b] : b;
     const int m = lane & 15, grp = lane >> 4;
     const int NC = (T + CK - 1) / CK;
-    const int tk = 16 * wave + (lane >> 2), c4 = 4 * (lane & 3);  // Vn / output element of this lane
+    const int tk = tid >> 3, c2 = 2 * (tid & 7);  // Vn / output elements of this thread
 
-    // This wave's state rows: tile 0 = rows 32 w + 4 grp + i, tile 1 = rows 32 w + 16 + 4 grp + i
-    // (i = 0..3), column n0 + m -- the C layout of the 16x16 MFMA, so the update accumulates in place.
-    // As the B operand of W S, k-slot j of lane (m, grp) is state row 32 w + 16 (j / 4) + 4 grp + j % 4:
-    // exactly the rows the lane holds, so W is read with the same k-slot order.
+    // This wave's 16 state rows 16 w + 4 grp + i (i < 4), column n0 + m: the C layout of the 16x16 MFMA,
+    // so the update accumulates in place.  As the B operand of W S (16x16x16: k-slot j of lane (m, grp)
+    // is row 4 grp + j of the wave's 16) the same four values serve directly.
     float* S = a.state + ((size_t)slot * Hv + h) * DK * DV;
-    f32x4 s0, s1;
+    f32x4 st;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        s0[i] = S[(size_t)(32 * wave + 4 * grp + i) * DV + n0 + m];
-        s1[i] = S[(size_t)(32 * wave + 16 + 4 * grp + i) * DV + n0 + m];
-    }
+    for (int i = 0; i < 4; ++i) st[i] = S[(size_t)(16 * wave + 4 * grp + i) * DV + n0 + m];
 
-    auto load_ops = [&](int c, StateOps<DK>& op) {
+    auto load_ops = [&](int c, StateOps& op) {
         const size_t hc = ((size_t)b * Hv + h) * ws.NC + c;
         const int t0 = c * CK, len = min(CK, T - t0);
         const size_t row0 = (size_t)b * T + t0;
-        const size_t wq = hc * CK * DK + 32 * wave + 4 * grp, kt = hc * DK * CK + 8 * grp;
+        const size_t wq = hc * CK * DK + 16 * wave + 4 * grp;
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
             const size_t e = wq + (size_t)(16 * rt + m) * DK;
-            const float4 w0 = *reinterpret_cast<const float4*>(ws.W + e);
-            const float4 w1 = *reinterpret_cast<const float4*>(ws.W + e + 16);
-            const float4 q0 = *reinterpret_cast<const float4*>(ws.Q + e);
-            const float4 q1 = *reinterpret_cast<const float4*>(ws.Q + e + 16);
-            op.w[rt][0] = w0.x, op.w[rt][1] = w0.y, op.w[rt][2] = w0.z, op.w[rt][3] = w0.w;
-            op.w[rt][4] = w1.x, op.w[rt][5] = w1.y, op.w[rt][6] = w1.z, op.w[rt][7] = w1.w;
-            op.q[rt][0] = q0.x, op.q[rt][1] = q0.y, op.q[rt][2] = q0.z, op.q[rt][3] = q0.w;
-            op.q[rt][4] = q1.x, op.q[rt][5] = q1.y, op.q[rt][6] = q1.z, op.q[rt][7] = q1.w;
+            op.w[rt] = *reinterpret_cast<const f32x4*>(ws.W + e);
+            op.q[rt] = *reinterpret_cast<const f32x4*>(ws.Q + e);
         }
+        const size_t kt = hc * DK * CK + (size_t)(16 * wave + m) * CK + 8 * grp;
 #pragma unroll
-        for (int rt2 = 0; rt2 < 2; ++rt2)
-#pragma unroll
-            for (int s = 0; s < 2; ++s) {
-                const size_t e = kt + (size_t)(32 * wave + 16 * rt2 + m) * CK + 32 * s;
-                op.kh[rt2][s] = *reinterpret_cast<const bf16x8*>(ws.Kh + e);
-                op.kl[rt2][s] = *reinterpret_cast<const bf16x8*>(ws.Kl + e);
-            }
+        for (int s = 0; s < 2; ++s) {
+            op.kh[s] = *reinterpret_cast<const bf16x8*>(ws.Kh + kt + 32 * s);
+            op.kl[s] = *reinterpret_cast<const bf16x8*>(ws.Kl + kt + 32 * s);
+        }
         op.glast = ws.G[hc * CK + CK - 1];
-        op.u = *reinterpret_cast<const float4*>(ws.U + hc * CK * DV + (size_t)tk * DV + n0 + c4);
-        op.o = tk < len ? *reinterpret_cast<const float4*>(a.o + ((row0 + tk) * Hv + h) * DV + n0 + c4)
-                        : make_float4(0.f, 0.f, 0.f, 0.f);
+        op.u = *reinterpret_cast<const float2*>(ws.U + hc * CK * DV + (size_t)tk * DV + n0 + c2);
+        // rows past the end of a partial chunk read a valid row (the value is not used): no branch
+        op.o = *reinterpret_cast<const float2*>(a.o + ((row0 + min(tk, len - 1)) * Hv + h) * DV + n0 + c2);
     };
 
-    auto step = [&](int c, const StateOps<DK>& cur) {
-        const int t0 = c * CK, len = min(CK, T - t0);
+    // FULL: the chunk has CK tokens (no per-token bounds test)
+    auto step = [&](int c, const StateOps& cur, auto full) {
+        constexpr bool FULL = decltype(full)::value;
+        const int t0 = c * CK, len = FULL ? CK : min(CK, T - t0);
         const size_t row0 = (size_t)b * T + t0;
 
-        // W S and Q' S over this wave's 32 state rows
-        float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
-        const Split8 Sb = split8(sv);
+        // W S and Q' S over this wave's 16 state rows
+        const Split4 Sb = split4(st);
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
             const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-            const f32x4 pw = mfma3(split8(cur.w[rt]), Sb, z);
-            const f32x4 pq = mfma3(split8(cur.q[rt]), Sb, z);
+            const f32x4 pw = mfma3k16(split4(cur.w[rt]), Sb, z);
+            const f32x4 pq = mfma3k16(split4(cur.q[rt]), Sb, z);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 red[wave][0][16 * rt + 4 * grp + i][m] = pw[i];
@@ -443,59 +461,67 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(DeltaArgs a, ChunkWs w
         }
         lds_barrier();
 
-        // Vn = U - W S and O += Q' S for token tk, columns c4..c4+3
+        // Vn = U - W S and O += Q' S for token tk, columns c2, c2 + 1
         {
-            float4 sw = make_float4(0.f, 0.f, 0.f, 0.f), sq = sw;
+            float2 sw = make_float2(0.f, 0.f), sq = sw;
 #pragma unroll
-            for (int w = 0; w < 4; ++w) {
-                const float4 x = *reinterpret_cast<const float4*>(&red[w][0][tk][c4]);
-                const float4 y = *reinterpret_cast<const float4*>(&red[w][1][tk][c4]);
-                sw.x += x.x, sw.y += x.y, sw.z += x.z, sw.w += x.w;
-                sq.x += y.x, sq.y += y.y, sq.z += y.z, sq.w += y.w;
+            for (int w = 0; w < NWV; ++w) {
+                const float2 x = *reinterpret_cast<const float2*>(&red[w][0][tk][c2]);
+                const float2 y = *reinterpret_cast<const float2*>(&red[w][1][tk][c2]);
+                sw.x += x.x, sw.y += x.y;
+                sq.x += y.x, sq.y += y.y;
             }
-            *reinterpret_cast<float4*>(&vn[tk][c4]) =
-                make_float4(cur.u.x - sw.x, cur.u.y - sw.y, cur.u.z - sw.z, cur.u.w - sw.w);
-            if (tk < len)
-                *reinterpret_cast<float4*>(a.o + ((row0 + tk) * Hv + h) * DV + n0 + c4) =
-                    make_float4(cur.o.x + sq.x, cur.o.y + sq.y, cur.o.z + sq.z, cur.o.w + sq.w);
+            vn[tk][c2] = cur.u.x - sw.x;
+            vn[tk][c2 + 1] = cur.u.y - sw.y;
+            if (FULL || tk < len)
+                *reinterpret_cast<float2*>(a.o + ((row0 + tk) * Hv + h) * DV + n0 + c2) =
+                    make_float2(cur.o.x + sq.x, cur.o.y + sq.y);
         }
         lds_barrier();
 
         // S <- e^{G_last} S + (K e^{G_last - G})^T Vn
         const float egl = __expf(cur.glast);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s0[i] *= egl, s1[i] *= egl;
+        for (int i = 0; i < 4; ++i) st[i] *= egl;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             float vb[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) vb[j] = vn[32 * s + 8 * grp + j][m];
-            const Split8 Vb = split8(vb);
-            s0 = mfma3(Split8{cur.kh[0][s], cur.kl[0][s]}, Vb, s0);
-            s1 = mfma3(Split8{cur.kh[1][s], cur.kl[1][s]}, Vb, s1);
+            st = mfma3(Split8{cur.kh[s], cur.kl[s]}, split8(vb), st);
         }
     };
 
-    // operands two chunks ahead: a 3-slot ring, unrolled so that every slot is a fixed set of registers
-    StateOps<DK> A, B, C;
+    // Operands two chunks ahead: a 3-slot ring, unrolled so that every slot is a fixed set of registers.
+    // The main loop runs over whole triples of full chunks with no conditional memory operation (loads
+    // past the last chunk re-read the last chunk), so the only waits are for the oldest slot's loads;
+    // the remaining (at most 3, the last possibly partial) chunks follow.
+    using Full = std::integral_constant<bool, true>;
+    using Part = std::integral_constant<bool, false>;
+    const int NCF = T / CK;  // full chunks
+    StateOps A, B, C;
     load_ops(0, A);
-    if (NC > 1) load_ops(1, B);
-    for (int c = 0; c < NC; c += 3) {
-        if (c + 2 < NC) load_ops(c + 2, C);
-        step(c, A);
-        if (c + 1 >= NC) break;
-        if (c + 3 < NC) load_ops(c + 3, A);
-        step(c + 1, B);
-        if (c + 2 >= NC) break;
-        if (c + 4 < NC) load_ops(c + 4, B);
-        step(c + 2, C);
+    load_ops(min(1, NC - 1), B);
+    int c = 0;
+    for (; c + 3 <= NCF; c += 3) {
+        load_ops(min(c + 2, NC - 1), C);
+        step(c, A, Full{});
+        load_ops(min(c + 3, NC - 1), A);
+        step(c + 1, B, Full{});
+        load_ops(min(c + 4, NC - 1), B);
+        step(c + 2, C, Full{});
+    }
+    if (c < NC) {
+        load_ops(min(c + 2, NC - 1), C);
+        step(c, A, Part{});
+        if (c + 1 < NC) {
+            step(c + 1, B, Part{});
+            if (c + 2 < NC) step(c + 2, C, Part{});
+        }
     }
 
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        S[(size_t)(32 * wave + 4 * grp + i) * DV + n0 + m] = s0[i];
-        S[(size_t)(32 * wave + 16 + 4 * grp + i) * DV + n0 + m] = s1[i];
-    }
+    for (int i = 0; i < 4; ++i) S[(size_t)(16 * wave + 4 * grp + i) * DV + n0 + m] = st[i];
 }
 
 }  // namespace
@@ -528,7 +554,7 @@ hipError_t launch_delta_chunked(const DeltaArgs& a, int dk, int dv, void* worksp
     hipLaunchKernelGGL((chunk_prep_kernel<128, 128>), dim3(ws.NC, a.Hv, a.B), dim3(256), 0, stream, a, ws);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((chunk_state_kernel<128, 128>), dim3(a.Hv * (128 / 16), a.B), dim3(256), 0, stream, a, ws);
+    hipLaunchKernelGGL((chunk_state_kernel<128, 128>), dim3(a.Hv * (128 / 16), a.B), dim3(512), 0, stream, a, ws);
     return hipGetLastError();
 }
 
