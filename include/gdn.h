@@ -26,6 +26,7 @@ extern "C" {
 #endif
 
 typedef struct gdn_layer gdn_layer;
+typedef struct gdn_stack gdn_stack;
 
 typedef enum gdn_status {
     GDN_OK = 0,
@@ -79,6 +80,17 @@ int gdn_layer_destroy(gdn_layer* layer);
  * for slots 0..B-1.  Continues every sequence from its slot's conv and recurrent state. */
 int gdn_layer_forward(gdn_layer* layer, const void* x, int B, int T, const int* slot_ids, void* out,
                       void* stream);
+
+/* Variable-length launch (no counterpart in the reference, which fixes one batch geometry per handle and
+ * maps row -> slot as m / T, 9B/kernels/layer_compute.cpp:231): n_seqs sequences of different lengths in
+ * one call, e.g. prefills and decode streams of a continuous batch.  x, out: bf16 [cu_seqlens[n_seqs], H];
+ * sequence i is rows [cu_seqlens[i], cu_seqlens[i+1]) (host int32 [n_seqs + 1], cu_seqlens[0] = 0, at most
+ * max_tokens rows) and continues slot slot_ids[i] (device int32 [n_seqs], or NULL for slots 0..n_seqs-1).
+ * The in_proj and out_proj run once over all rows; runs of consecutive equal-length sequences share one
+ * launch of the middle of the layer.  The result of each sequence equals its own gdn_layer_forward up to
+ * the rounding of the projection kernel chosen for the total row count. */
+int gdn_layer_forward_varlen(gdn_layer* layer, const void* x, int n_seqs, const int* cu_seqlens,
+                             const int* slot_ids, void* out, void* stream);
 
 /* 9B/gdn_layer.py:137-151 (reset_state): zero the states of `n` slots (device ids, NULL = the first n). */
 int gdn_state_reset(gdn_layer* layer, const int* slot_ids, int n, void* stream);
@@ -135,6 +147,30 @@ int gdn_gated_rmsnorm(gdn_layer* layer, const float* o, const float* z, int z_st
 
 /* out_proj: 9B/gdn_layer.py:272-276.  y bf16 [M, nv*dv] -> out bf16 [M, H]. */
 int gdn_out_proj(gdn_layer* layer, const void* y, int M, void* out, void* stream);
+
+/* ---- layer stack: mirrors Qwen35_08B_GDNStackL1 (wormhole_n150/qwen3.5_0.8B/gdn_l1.py:207-341) ---- */
+
+/* n_layers layers of one geometry (weights[i] = layer i, as in gdn_layer_create), run back to back: the
+ * output of layer i is the input of layer i + 1, each layer with its own `max_slots` state slots
+ * (gdn_l1.py:330-341: GDN mixers only).  inter_norm != 0 adds the decoder RMSNorm between layers,
+ * y = x rsqrt(mean(x^2) + eps) (1 + w) (HF Qwen3_5RMSNorm, modeling_qwen3_5.py:720-734), with w =
+ * norm_weights[i] (fp32 [H], host or device) after layer i, or w = 0 where norm_weights or the entry is
+ * NULL; no norm follows the last layer.  The layers share one workspace for `max_tokens` rows. */
+int gdn_stack_create(const gdn_dims* dims, const gdn_weights* weights, int n_layers, int inter_norm,
+                     const float* const* norm_weights, int max_slots, int max_tokens, gdn_stack** out);
+int gdn_stack_destroy(gdn_stack* stack);
+
+/* The handle of layer i, for the state calls (gdn_state_*) and per-op entries.  Owned by the stack. */
+int gdn_stack_layer(gdn_stack* stack, int i, gdn_layer** layer);
+
+/* gdn_l1.py:294-341 (forward_device / __call__(hidden_states, layers)): layers [first, first + count) on
+ * x bf16 [B*T, H] -> out bf16 [B*T, H], B*T <= max_tokens; slot_ids as in gdn_layer_forward. */
+int gdn_stack_forward(gdn_stack* stack, const void* x, int B, int T, const int* slot_ids, int first, int count,
+                      void* out, void* stream);
+
+/* The same over a variable-length launch (see gdn_layer_forward_varlen). */
+int gdn_stack_forward_varlen(gdn_stack* stack, const void* x, int n_seqs, const int* cu_seqlens,
+                             const int* slot_ids, int first, int count, void* out, void* stream);
 
 /* ---- standalone ops ------------------------------------------------------------------------------ */
 

@@ -1,6 +1,6 @@
 """MI355X-native Qwen3.5 Gated DeltaNet layer (hand-written HIP for gfx950 behind a C ABI).
 
-    from linear_attention_op_amd import Qwen35GatedDeltaNetHIP, GatedDeltaRuleHIP
+    from linear_attention_op_amd import Qwen35GatedDeltaNetHIP, Qwen35GDNStackHIP, GatedDeltaRuleHIP
 
 The compute lives in libgdn_hip.so (include/gdn.h); these classes mirror the reference's layer and
 recurrence-op objects.  Build the library with `python -m linear_attention_op_amd.build`.
@@ -9,6 +9,7 @@ recurrence-op objects.  Build the library with `python -m linear_attention_op_am
 from ._lib import GdnError, GdnValueError, LIB_PATH  # noqa: F401
 from .gated_delta import GatedDeltaRuleHIP  # noqa: F401
 from .gdn_layer import Qwen35GatedDeltaNetHIP, linear, weights_from_hf  # noqa: F401
+from .gdn_stack import Qwen35GDNStackHIP  # noqa: F401
 
-__all__ = ["Qwen35GatedDeltaNetHIP", "GatedDeltaRuleHIP", "linear", "weights_from_hf", "GdnError",
-           "GdnValueError"]
+__all__ = ["Qwen35GatedDeltaNetHIP", "Qwen35GDNStackHIP", "GatedDeltaRuleHIP", "linear", "weights_from_hf",
+           "GdnError", "GdnValueError"]

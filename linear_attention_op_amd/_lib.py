@@ -53,6 +53,13 @@ SIGNATURES = {
     "gdn_layer_create": (_I, [ctypes.POINTER(GdnDims), ctypes.POINTER(GdnWeights), _I, _I, ctypes.POINTER(_V)]),
     "gdn_layer_destroy": (_I, [_V]),
     "gdn_layer_forward": (_I, [_V, _V, _I, _I, _V, _V, _V]),
+    "gdn_layer_forward_varlen": (_I, [_V, _V, _I, ctypes.POINTER(_I), _V, _V, _V]),
+    "gdn_stack_create": (_I, [ctypes.POINTER(GdnDims), ctypes.POINTER(GdnWeights), _I, _I,
+                              ctypes.POINTER(ctypes.c_void_p), _I, _I, ctypes.POINTER(_V)]),
+    "gdn_stack_destroy": (_I, [_V]),
+    "gdn_stack_layer": (_I, [_V, _I, ctypes.POINTER(_V)]),
+    "gdn_stack_forward": (_I, [_V, _V, _I, _I, _V, _I, _I, _V, _V]),
+    "gdn_stack_forward_varlen": (_I, [_V, _V, _I, ctypes.POINTER(_I), _V, _I, _I, _V, _V]),
     "gdn_state_reset": (_I, [_V, _V, _I, _V]),
     "gdn_state_get": (_I, [_V, _V, _I, _V, _V, _V]),
     "gdn_state_set": (_I, [_V, _V, _I, _V, _V, _V]),

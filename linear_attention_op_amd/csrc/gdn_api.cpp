@@ -62,7 +62,11 @@ struct gdn_layer {
     float* rec = nullptr;     // [slots, nv, dk, dv]
     float* conv = nullptr;    // [slots, nv, 3, CH] conv history, time order
 
-    // workspace, sized for max_tokens rows
+    int* iota = nullptr;      // [max_slots] identity slot ids (slot offsets of varlen groups)
+
+    // workspace, sized for max_tokens rows; layers of a stack share one (run one at a time)
+    bool owns_ws = true;
+    std::vector<void*> ws_allocs;
     u16* x_ws = nullptr;      // [max_tokens, H] gathered input rows when a launch is split
     u16* x_frag = nullptr;    // [64, H] decode input in W_FRAG layout
     u16* out_ws = nullptr;    // [max_tokens, H]
@@ -82,10 +86,10 @@ struct gdn_layer {
     int prof_max = 0, prof_calls = 0;
 
     template <typename Tp>
-    hipError_t alloc(Tp** p, size_t count) {
+    hipError_t alloc(Tp** p, size_t count, bool workspace = false) {
         void* q = nullptr;
         hipError_t e = hipMalloc(&q, count * sizeof(Tp) > 0 ? count * sizeof(Tp) : 16);
-        if (e == hipSuccess) allocs.push_back(q);
+        if (e == hipSuccess) (workspace ? ws_allocs : allocs).push_back(q);
         *p = static_cast<Tp*>(q);
         return e;
     }
@@ -100,6 +104,7 @@ struct gdn_layer {
     ~gdn_layer() {
         prof_free();
         for (void* p : allocs) (void)hipFree(p);
+        for (void* p : ws_allocs) (void)hipFree(p);
     }
 };
 
@@ -134,52 +139,118 @@ hipError_t run_delta(gdn_layer* L, const gdn::DeltaArgs& r, hipStream_t st) {
     return gdn::launch_delta_seq(r, d.head_k_dim, d.head_v_dim, st);
 }
 
-int run_chunk(gdn_layer* L, const u16* x, int B, int T, const int* slot_ids, u16* out, hipStream_t st) {
+// A group of sequences of one launch with the same length: rows [row0, row0 + B T) of the launch,
+// sequence b of the group on state slot slots[b].
+struct Group {
+    int row0, B, T;
+    const int* slots;  // device [B]; never NULL here
+};
+
+// One launch over M rows made of row groups (9B/gdn_layer.py:244-280 for a single group): the in_proj over
+// all M rows, the middle of the layer per group (fused mixer for groups of <= kFusedMaxT tokens per
+// sequence, front end + chunked recurrence + gated RMSNorm otherwise), the out_proj over all M rows.
+int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, u16* out, hipStream_t st) {
     const gdn_dims& d = L->d;
-    const int M = B * T;
+    const int Kd = L->Kd, Vd = L->Vd, nv = d.num_v_heads;
     hipEvent_t ev[4] = {L->prof_event(0), L->prof_event(1), L->prof_event(2), L->prof_event(3)};
     if (ev[0]) HIP_OK(hipEventRecord(ev[0], st));
     // decode-sized launches stream the weights against fragment-tiled activations
     const bool frag = M <= 64;
-    const bool y_frag = frag && T <= kFusedMaxT;  // the fused mixer writes y straight into W_FRAG layout
+    // the fused mixer writes y straight into W_FRAG layout when it produces every row
+    const bool y_frag = frag && ng == 1 && grp[0].T <= kFusedMaxT;
     if (frag) HIP_OK(gdn::launch_frag_tile(x, M, d.hidden, L->x_frag, st));
     HIP_OK(gdn::launch_linear(frag ? L->x_frag : x, frag ? gdn::W_FRAG : gdn::W_ROW, L->w_in, gdn::W_FRAG, M, L->NP,
                               d.hidden, L->P, gdn::OUT_F32, st));
     if (ev[1]) HIP_OK(hipEventRecord(ev[1], st));
-    if (T <= kFusedMaxT) {
-        gdn::MixerArgs a{};
-        a.P = L->P, a.NP = L->NP, a.B = B, a.T = T, a.slot_ids = slot_ids;
-        a.nk = d.num_k_heads, a.nv = d.num_v_heads;
-        a.conv_w = L->conv_w, a.neg_A = L->neg_A, a.dt_bias = L->dt_bias, a.norm_w = L->norm_w;
-        a.eps = d.rms_norm_eps;
-        a.rec_state = L->rec, a.conv_state = L->conv;
-        a.y = L->y, a.y_frag = y_frag ? 1 : 0, a.o_tap = nullptr;
-        HIP_OK(gdn::launch_mixer(a, d.head_k_dim, d.head_v_dim, st));
-    } else {
-        gdn::FrontArgs f{};
-        f.P = L->P, f.NP = L->NP, f.B = B, f.T = T, f.slot_ids = slot_ids;
-        f.nk = d.num_k_heads, f.nv = d.num_v_heads, f.dk = d.head_k_dim, f.dv = d.head_v_dim;
-        f.conv_w = L->conv_w, f.neg_A = L->neg_A, f.dt_bias = L->dt_bias;
-        f.conv_state = L->conv;
-        f.qn = L->qn, f.kn = L->kn, f.v = L->v, f.g = L->g, f.beta = L->beta;
-        HIP_OK(gdn::launch_conv_front(f, st));
-        HIP_OK(gdn::launch_conv_commit(L->P, L->NP, B, T, slot_ids, d.num_k_heads, d.num_v_heads, d.head_k_dim,
-                                       d.head_v_dim, L->conv, st));
-        gdn::DeltaArgs r{};
-        r.q = L->qn, r.k = L->kn, r.v = L->v, r.g = L->g, r.beta = L->beta;
-        r.B = B, r.T = T, r.Hk = d.num_k_heads, r.Hv = d.num_v_heads, r.slot_ids = slot_ids;
-        r.state = L->rec, r.o = L->o, r.normalize = 0, r.scale = 1.f;
-        HIP_OK(run_delta(L, r, st));
-        HIP_OK(gdn::launch_gated_rmsnorm(L->o, M, d.num_v_heads, d.head_v_dim, L->P + L->CD, L->NP, L->norm_w,
-                                         d.rms_norm_eps, L->y, st));
+    for (int gi = 0; gi < ng; ++gi) {
+        const Group& g = grp[gi];
+        const size_t r0 = (size_t)g.row0;
+        const int Mg = g.B * g.T;
+        if (g.T <= kFusedMaxT) {
+            gdn::MixerArgs a{};
+            a.P = L->P + r0 * L->NP, a.NP = L->NP, a.B = g.B, a.T = g.T, a.slot_ids = g.slots;
+            a.nk = d.num_k_heads, a.nv = nv;
+            a.conv_w = L->conv_w, a.neg_A = L->neg_A, a.dt_bias = L->dt_bias, a.norm_w = L->norm_w;
+            a.eps = d.rms_norm_eps;
+            a.rec_state = L->rec, a.conv_state = L->conv;
+            a.y = y_frag ? L->y : L->y + r0 * Vd, a.y_frag = y_frag ? 1 : 0, a.o_tap = nullptr;
+            HIP_OK(gdn::launch_mixer(a, d.head_k_dim, d.head_v_dim, st));
+        } else {
+            float* P = L->P + r0 * L->NP;
+            gdn::FrontArgs f{};
+            f.P = P, f.NP = L->NP, f.B = g.B, f.T = g.T, f.slot_ids = g.slots;
+            f.nk = d.num_k_heads, f.nv = nv, f.dk = d.head_k_dim, f.dv = d.head_v_dim;
+            f.conv_w = L->conv_w, f.neg_A = L->neg_A, f.dt_bias = L->dt_bias;
+            f.conv_state = L->conv;
+            f.qn = L->qn + r0 * Kd, f.kn = L->kn + r0 * Kd, f.v = L->v + r0 * Vd;
+            f.g = L->g + r0 * nv, f.beta = L->beta + r0 * nv;
+            HIP_OK(gdn::launch_conv_front(f, st));
+            HIP_OK(gdn::launch_conv_commit(P, L->NP, g.B, g.T, g.slots, d.num_k_heads, nv, d.head_k_dim,
+                                           d.head_v_dim, L->conv, st));
+            gdn::DeltaArgs r{};
+            r.q = f.qn, r.k = f.kn, r.v = f.v, r.g = f.g, r.beta = f.beta;
+            r.B = g.B, r.T = g.T, r.Hk = d.num_k_heads, r.Hv = nv, r.slot_ids = g.slots;
+            r.state = L->rec, r.o = L->o + r0 * Vd, r.normalize = 0, r.scale = 1.f;
+            HIP_OK(run_delta(L, r, st));
+            HIP_OK(gdn::launch_gated_rmsnorm(r.o, Mg, nv, d.head_v_dim, P + L->CD, L->NP, L->norm_w,
+                                             d.rms_norm_eps, L->y + r0 * Vd, st));
+        }
     }
     if (ev[2]) HIP_OK(hipEventRecord(ev[2], st));
-    HIP_OK(gdn::launch_linear(L->y, y_frag ? gdn::W_FRAG : gdn::W_ROW, L->w_out, gdn::W_FRAG, M, d.hidden, L->Vd, out,
+    HIP_OK(gdn::launch_linear(L->y, y_frag ? gdn::W_FRAG : gdn::W_ROW, L->w_out, gdn::W_FRAG, M, d.hidden, Vd, out,
                               gdn::OUT_BF16, st));
     if (ev[3]) {
         HIP_OK(hipEventRecord(ev[3], st));
         ++L->prof_calls;
     }
+    return GDN_OK;
+}
+
+int run_chunk(gdn_layer* L, const u16* x, int B, int T, const int* slot_ids, u16* out, hipStream_t st) {
+    const Group g{0, B, T, slot_ids ? slot_ids : L->iota};
+    return run_rows(L, x, B * T, &g, 1, out, st);
+}
+
+// gdn_layer_forward without the argument checks: launches longer than the workspace are split by tokens.
+int layer_forward(gdn_layer* L, const u16* x, int B, int T, const int* slot_ids, u16* out, hipStream_t st) {
+    const int H = L->d.hidden;
+    const int tc_max = L->max_tokens / B;
+    if (T <= tc_max) return run_chunk(L, x, B, T, slot_ids, out, st);
+    for (int t0 = 0; t0 < T; t0 += tc_max) {
+        const int tc = T - t0 < tc_max ? T - t0 : tc_max;
+        const size_t rb = (size_t)H * sizeof(u16);
+        if (B == 1) {
+            int rc = run_chunk(L, x + (size_t)t0 * H, 1, tc, slot_ids, out + (size_t)t0 * H, st);
+            if (rc) return rc;
+            continue;
+        }
+        // gather rows [b, t0:t0+tc) of every sequence into one sequence-major block, and scatter back
+        HIP_OK(hipMemcpy2DAsync(L->x_ws, tc * rb, x + (size_t)t0 * H, (size_t)T * rb, tc * rb, B,
+                                hipMemcpyDeviceToDevice, st));
+        int rc = run_chunk(L, L->x_ws, B, tc, slot_ids, L->out_ws, st);
+        if (rc) return rc;
+        HIP_OK(hipMemcpy2DAsync(out + (size_t)t0 * H, (size_t)T * rb, L->out_ws, tc * rb, tc * rb, B,
+                                hipMemcpyDeviceToDevice, st));
+    }
+    return GDN_OK;
+}
+
+// Row groups of a varlen launch: runs of consecutive sequences with equal length.
+int varlen_groups(const gdn_layer* L, int n_seqs, const int* cu, const int* slot_ids, std::vector<Group>* out) {
+    out->clear();
+    if (n_seqs <= 0 || !cu) return fail(GDN_ERR_INVALID_ARG, "varlen: n_seqs=%d, cu_seqlens %p", n_seqs, (const void*)cu);
+    if (cu[0] != 0) return fail(GDN_ERR_SHAPE, "varlen: cu_seqlens[0]=%d must be 0", cu[0]);
+    if (!slot_ids && n_seqs > L->max_slots) return fail(GDN_ERR_SLOT, "%d sequences exceed max_slots=%d", n_seqs, L->max_slots);
+    for (int i = 0; i < n_seqs;) {
+        const int T = cu[i + 1] - cu[i];
+        if (T <= 0) return fail(GDN_ERR_SHAPE, "varlen: sequence %d has length %d", i, T);
+        int j = i + 1;
+        while (j < n_seqs && cu[j + 1] - cu[j] == T) ++j;
+        out->push_back(Group{cu[i], j - i, T, (slot_ids ? slot_ids : L->iota) + i});
+        i = j;
+    }
+    if (cu[n_seqs] > L->max_tokens)
+        return fail(GDN_ERR_SHAPE, "varlen: %d rows exceed max_tokens=%d", cu[n_seqs], L->max_tokens);
     return GDN_OK;
 }
 
@@ -191,7 +262,14 @@ const char* gdn_last_error(void) { return g_last_error.c_str(); }
 
 int gdn_version(void) { return 100; }
 
-int gdn_layer_create(const gdn_dims* dims, const gdn_weights* w, int max_slots, int max_tokens, gdn_layer** out) {
+}  // extern "C"
+
+namespace {
+
+// Layer creation; `share` (a layer of the same geometry) lends its launch workspace, as layers of a stack
+// run one at a time.
+int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int max_tokens, const gdn_layer* share,
+                 gdn_layer** out) {
     if (!out) return fail(GDN_ERR_INVALID_ARG, "out is NULL");
     *out = nullptr;
     int rc = check_dims(dims);
@@ -222,25 +300,33 @@ int gdn_layer_create(const gdn_dims* dims, const gdn_weights* w, int max_slots, 
     take(L->alloc(&L->norm_w, (size_t)dv));
     take(L->alloc(&L->rec, (size_t)max_slots * nv * dk * dv));
     take(L->alloc(&L->conv, (size_t)max_slots * nv * 3 * L->CH));
-    take(L->alloc(&L->x_ws, MT * H));
-    take(L->alloc(&L->x_frag, gdn::frag_elems(64, H)));
-    take(L->alloc(&L->out_ws, MT * H));
-    take(L->alloc(&L->P, MT * L->NP));
-    take(L->alloc(&L->qn, MT * L->Kd));
-    take(L->alloc(&L->kn, MT * L->Kd));
-    take(L->alloc(&L->v, MT * L->Vd));
-    take(L->alloc(&L->g, MT * nv));
-    take(L->alloc(&L->beta, MT * nv));
-    take(L->alloc(&L->o, MT * L->Vd));
-    take(L->alloc(&L->y, std::max(MT * L->Vd, gdn::frag_elems(64, L->Vd))));  // W_FRAG y pads rows to 16
-    if (max_tokens > kFusedMaxT && gdn::delta_chunked_supported(dk, dv)) {
-        // chunked-prefill workspace for the worst launch: B sequences of T > kFusedMaxT tokens with
-        // B * T <= max_tokens hold at most max_tokens / 64 + max_tokens / 65 + 1 chunks
-        const int chunks = max_tokens / 64 + max_tokens / (kFusedMaxT + 1) + 1;
-        L->chunk_ws_bytes = gdn::delta_chunked_workspace(1, 64 * chunks, nv, dk, dv);
-        char* p = nullptr;
-        take(L->alloc(&p, L->chunk_ws_bytes));
-        L->chunk_ws = p;
+    take(L->alloc(&L->iota, (size_t)max_slots));
+    if (share) {
+        L->owns_ws = false;
+        L->x_ws = share->x_ws, L->x_frag = share->x_frag, L->out_ws = share->out_ws, L->P = share->P;
+        L->qn = share->qn, L->kn = share->kn, L->v = share->v, L->g = share->g, L->beta = share->beta;
+        L->o = share->o, L->y = share->y, L->chunk_ws = share->chunk_ws, L->chunk_ws_bytes = share->chunk_ws_bytes;
+    } else {
+        take(L->alloc(&L->x_ws, MT * H, true));
+        take(L->alloc(&L->x_frag, gdn::frag_elems(64, H), true));
+        take(L->alloc(&L->out_ws, MT * H, true));
+        take(L->alloc(&L->P, MT * L->NP, true));
+        take(L->alloc(&L->qn, MT * L->Kd, true));
+        take(L->alloc(&L->kn, MT * L->Kd, true));
+        take(L->alloc(&L->v, MT * L->Vd, true));
+        take(L->alloc(&L->g, MT * nv, true));
+        take(L->alloc(&L->beta, MT * nv, true));
+        take(L->alloc(&L->o, MT * L->Vd, true));
+        take(L->alloc(&L->y, std::max(MT * L->Vd, gdn::frag_elems(64, L->Vd)), true));  // W_FRAG y pads rows to 16
+        if (max_tokens > kFusedMaxT && gdn::delta_chunked_supported(dk, dv)) {
+            // chunked-prefill workspace for the worst launch: sequences of T > kFusedMaxT tokens with
+            // at most max_tokens rows in all hold at most max_tokens / 64 + max_tokens / 65 + 1 chunks
+            const int chunks = max_tokens / 64 + max_tokens / (kFusedMaxT + 1) + 1;
+            L->chunk_ws_bytes = gdn::delta_chunked_workspace(1, 64 * chunks, nv, dk, dv);
+            char* p = nullptr;
+            take(L->alloc(&p, L->chunk_ws_bytes, true));
+            L->chunk_ws = p;
+        }
     }
     if (e != hipSuccess) {
         delete L;
@@ -272,6 +358,11 @@ int gdn_layer_create(const gdn_dims* dims, const gdn_weights* w, int max_slots, 
     }
     if (e == hipSuccess) e = hipMemcpy(L->dt_bias, w->dt_bias, nv * sizeof(float), hipMemcpyDefault);
     if (e == hipSuccess) e = hipMemcpy(L->norm_w, w->norm_weight, dv * sizeof(float), hipMemcpyDefault);
+    if (e == hipSuccess) {
+        std::vector<int> ids(max_slots);
+        for (int i = 0; i < max_slots; ++i) ids[i] = i;
+        e = hipMemcpy(L->iota, ids.data(), max_slots * sizeof(int), hipMemcpyHostToDevice);
+    }
     if (e == hipSuccess) e = gdn::launch_state_zero(L->rec, L->conv, nullptr, max_slots, nv, dk, dv,
                                                     L->CH, nullptr);
     if (e == hipSuccess) e = hipDeviceSynchronize();
@@ -281,6 +372,14 @@ int gdn_layer_create(const gdn_dims* dims, const gdn_weights* w, int max_slots, 
     }
     *out = L;
     return GDN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gdn_layer_create(const gdn_dims* dims, const gdn_weights* w, int max_slots, int max_tokens, gdn_layer** out) {
+    return create_layer(dims, w, max_slots, max_tokens, nullptr, out);
 }
 
 int gdn_layer_destroy(gdn_layer* L) {
@@ -295,27 +394,17 @@ int gdn_layer_forward(gdn_layer* L, const void* x, int B, int T, const int* slot
     if (B <= 0 || T <= 0) return fail(GDN_ERR_SHAPE, "gdn_layer_forward: B=%d T=%d must be > 0", B, T);
     if (B > L->max_tokens) return fail(GDN_ERR_SHAPE, "B=%d exceeds max_tokens=%d", B, L->max_tokens);
     if (!slot_ids && B > L->max_slots) return fail(GDN_ERR_SLOT, "B=%d exceeds max_slots=%d", B, L->max_slots);
-    const hipStream_t st = as_stream(stream);
-    const int H = L->d.hidden;
-    const int tc_max = L->max_tokens / B;
-    if (T <= tc_max) return run_chunk(L, (const u16*)x, B, T, slot_ids, (u16*)out, st);
-    for (int t0 = 0; t0 < T; t0 += tc_max) {
-        const int tc = T - t0 < tc_max ? T - t0 : tc_max;
-        const size_t rb = (size_t)H * sizeof(u16);
-        if (B == 1) {
-            int rc = run_chunk(L, (const u16*)x + (size_t)t0 * H, 1, tc, slot_ids, (u16*)out + (size_t)t0 * H, st);
-            if (rc) return rc;
-            continue;
-        }
-        // gather rows [b, t0:t0+tc) of every sequence into one sequence-major block, and scatter back
-        HIP_OK(hipMemcpy2DAsync(L->x_ws, tc * rb, (const u16*)x + (size_t)t0 * H, (size_t)T * rb, tc * rb, B,
-                                hipMemcpyDeviceToDevice, st));
-        int rc = run_chunk(L, L->x_ws, B, tc, slot_ids, L->out_ws, st);
-        if (rc) return rc;
-        HIP_OK(hipMemcpy2DAsync((u16*)out + (size_t)t0 * H, (size_t)T * rb, L->out_ws, tc * rb, tc * rb, B,
-                                hipMemcpyDeviceToDevice, st));
-    }
-    return GDN_OK;
+    return layer_forward(L, (const u16*)x, B, T, slot_ids, (u16*)out, as_stream(stream));
+}
+
+int gdn_layer_forward_varlen(gdn_layer* L, const void* x, int n_seqs, const int* cu_seqlens, const int* slot_ids,
+                             void* out, void* stream) {
+    if (!L || !x || !out) return fail(GDN_ERR_INVALID_ARG, "gdn_layer_forward_varlen: NULL argument");
+    std::vector<Group> groups;
+    int rc = varlen_groups(L, n_seqs, cu_seqlens, slot_ids, &groups);
+    if (rc) return rc;
+    return run_rows(L, (const u16*)x, cu_seqlens[n_seqs], groups.data(), (int)groups.size(), (u16*)out,
+                    as_stream(stream));
 }
 
 int gdn_state_reset(gdn_layer* L, const int* slot_ids, int n, void* stream) {
@@ -465,6 +554,123 @@ int gdn_linear_bf16(const void* x, const void* w, int M, int N, int K, void* y, 
     HIP_OK(gdn::launch_linear(x, gdn::W_ROW, w, gdn::W_ROW, M, N, K, y, out_fp32 ? gdn::OUT_F32 : gdn::OUT_BF16,
                               as_stream(stream)));
     return GDN_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------------------------------------
+// Layer stack: the reference's Qwen35_08B_GDNStackL1 (wormhole_n150/qwen3.5_0.8B/gdn_l1.py:207-341) --
+// layers of one geometry run back to back, each with its own weights and state slots, the output of
+// layer i the input of layer i + 1 -- optionally with the decoder RMSNorm between layers.  The layers
+// share one launch workspace; activations ping-pong between two buffers of the stack.
+// ------------------------------------------------------------------------------------------------
+struct gdn_stack {
+    std::vector<gdn_layer*> layers;
+    int inter_norm = 0;
+    float* norm_w = nullptr;  // [n_layers, H] decoder RMSNorm weights (y = x rstd (1 + w))
+    u16* act[2] = {nullptr, nullptr};
+    int H = 0, max_tokens = 0;
+    float eps = 1e-6f;
+    ~gdn_stack() {
+        for (size_t i = layers.size(); i-- > 0;) delete layers[i];  // borrowers before the workspace owner
+        if (norm_w) (void)hipFree(norm_w);
+        for (u16* a : act)
+            if (a) (void)hipFree(a);
+    }
+};
+
+namespace {
+
+// Layers [first, first + count) on rows made of `groups`; norms after every layer but the stack's last.
+int stack_run(gdn_stack* S, const u16* x, int M, const Group* groups, int ng, int first, int count, u16* out,
+              hipStream_t st) {
+    const u16* in = x;
+    for (int i = first; i < first + count; ++i) {
+        u16* dst = i + 1 == first + count ? out : S->act[(i - first) & 1];
+        int rc = run_rows(S->layers[i], in, M, groups, ng, dst, st);
+        if (rc) return rc;
+        if (S->inter_norm && i + 1 < (int)S->layers.size())
+            HIP_OK(gdn::launch_rmsnorm_rows(dst, M, S->H, S->norm_w + (size_t)i * S->H, S->eps, dst, st));
+        in = dst;
+    }
+    return GDN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gdn_stack_create(const gdn_dims* dims, const gdn_weights* weights, int n_layers, int inter_norm,
+                     const float* const* norm_weights, int max_slots, int max_tokens, gdn_stack** out) {
+    if (!out) return fail(GDN_ERR_INVALID_ARG, "out is NULL");
+    *out = nullptr;
+    if (!weights || n_layers <= 0) return fail(GDN_ERR_INVALID_ARG, "gdn_stack_create: %d layers", n_layers);
+    gdn_stack* S = new gdn_stack();
+    for (int i = 0; i < n_layers; ++i) {
+        gdn_layer* L = nullptr;
+        int rc = create_layer(dims, &weights[i], max_slots, max_tokens, i ? S->layers[0] : nullptr, &L);
+        if (rc) {
+            delete S;
+            return rc;
+        }
+        S->layers.push_back(L);
+    }
+    S->H = dims->hidden, S->max_tokens = max_tokens, S->inter_norm = inter_norm ? 1 : 0;
+    S->eps = dims->rms_norm_eps;
+    const size_t bytes = (size_t)max_tokens * S->H * sizeof(u16);
+    hipError_t e = hipMalloc(&S->act[0], bytes);
+    if (e == hipSuccess) e = hipMalloc(&S->act[1], bytes);
+    if (e == hipSuccess) e = hipMalloc(&S->norm_w, (size_t)n_layers * S->H * sizeof(float));
+    if (e == hipSuccess) e = hipMemset(S->norm_w, 0, (size_t)n_layers * S->H * sizeof(float));
+    for (int i = 0; e == hipSuccess && norm_weights && i < n_layers; ++i)
+        if (norm_weights[i])
+            e = hipMemcpy(S->norm_w + (size_t)i * S->H, norm_weights[i], S->H * sizeof(float), hipMemcpyDefault);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        delete S;
+        return fail(e == hipErrorOutOfMemory ? GDN_ERR_OUT_OF_MEMORY : GDN_ERR_HIP, "gdn_stack_create: %s",
+                    hipGetErrorString(e));
+    }
+    *out = S;
+    return GDN_OK;
+}
+
+int gdn_stack_destroy(gdn_stack* S) {
+    if (!S) return GDN_OK;
+    (void)hipDeviceSynchronize();
+    delete S;
+    return GDN_OK;
+}
+
+int gdn_stack_layer(gdn_stack* S, int i, gdn_layer** out) {
+    if (!S || !out) return fail(GDN_ERR_INVALID_ARG, "gdn_stack_layer: NULL argument");
+    if (i < 0 || i >= (int)S->layers.size()) return fail(GDN_ERR_INVALID_ARG, "layer %d of %zu", i, S->layers.size());
+    *out = S->layers[i];
+    return GDN_OK;
+}
+
+int gdn_stack_forward(gdn_stack* S, const void* x, int B, int T, const int* slot_ids, int first, int count,
+                      void* out, void* stream) {
+    if (!S || !x || !out) return fail(GDN_ERR_INVALID_ARG, "gdn_stack_forward: NULL argument");
+    const int n = (int)S->layers.size();
+    if (first < 0 || count <= 0 || first + count > n) return fail(GDN_ERR_INVALID_ARG, "layers [%d, %d) of %d", first, first + count, n);
+    if (B <= 0 || T <= 0 || (size_t)B * T > (size_t)S->max_tokens)
+        return fail(GDN_ERR_SHAPE, "gdn_stack_forward: B=%d T=%d (max_tokens %d)", B, T, S->max_tokens);
+    if (!slot_ids && B > S->layers[0]->max_slots) return fail(GDN_ERR_SLOT, "B=%d exceeds max_slots", B);
+    const Group g{0, B, T, slot_ids ? slot_ids : S->layers[0]->iota};
+    return stack_run(S, (const u16*)x, B * T, &g, 1, first, count, (u16*)out, as_stream(stream));
+}
+
+int gdn_stack_forward_varlen(gdn_stack* S, const void* x, int n_seqs, const int* cu_seqlens, const int* slot_ids,
+                             int first, int count, void* out, void* stream) {
+    if (!S || !x || !out) return fail(GDN_ERR_INVALID_ARG, "gdn_stack_forward_varlen: NULL argument");
+    const int n = (int)S->layers.size();
+    if (first < 0 || count <= 0 || first + count > n) return fail(GDN_ERR_INVALID_ARG, "layers [%d, %d) of %d", first, first + count, n);
+    std::vector<Group> groups;
+    int rc = varlen_groups(S->layers[0], n_seqs, cu_seqlens, slot_ids, &groups);
+    if (rc) return rc;
+    return stack_run(S, (const u16*)x, cu_seqlens[n_seqs], groups.data(), (int)groups.size(), first, count, (u16*)out,
+                     as_stream(stream));
 }
 
 }  // extern "C"

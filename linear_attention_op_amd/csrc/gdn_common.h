@@ -170,6 +170,9 @@ size_t delta_chunked_workspace(int B, int T, int Hv, int dk, int dv);
 bool delta_chunked_supported(int dk, int dv);
 
 // y = o * rsqrt(mean(o^2) + eps) * w * silu(z), per head of dv; y bf16.
+// Decoder RMSNorm of M rows of H bf16 values: y = x rsqrt(mean(x^2) + eps) (1 + w), w fp32 [H] or NULL
+// (= 0).  H % 8 == 0, H <= 8192.  In place (y == x) is allowed.
+hipError_t launch_rmsnorm_rows(const u16* x, int M, int H, const float* w, float eps, u16* y, hipStream_t stream);
 hipError_t launch_gated_rmsnorm(const float* o, int M, int nv, int dv, const float* z, int z_stride,
                                 const float* w, float eps, u16* y, hipStream_t stream);
 

@@ -339,6 +339,52 @@ hipError_t launch_gated_rmsnorm(const float* o, int M, int nv, int dv, const flo
 }
 
 // ------------------------------------------------------------------------------------------------
+// Decoder RMSNorm between stacked layers (HF Qwen3_5RMSNorm, modeling_qwen3_5.py:720-734):
+// y = x rsqrt(mean(x^2) + eps) (1 + w), fp32 math, bf16 in and out.  One workgroup per row; each
+// thread owns 8-element pieces of the row, read once and kept in registers between the two passes.
+// ------------------------------------------------------------------------------------------------
+constexpr int RN_PIECES = 4;  // pieces of 8 per thread: rows up to 256 * 8 * 4 = 8192 wide
+
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const u16* x, int H, const float* __restrict__ w,
+                                                           float eps, u16* y) {  // y may alias x
+    __shared__ float part[4];
+    const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const u16* xr = x + (size_t)m * H;
+    u16x8 v[RN_PIECES];
+    float ss = 0.f;
+#pragma unroll
+    for (int p = 0; p < RN_PIECES; ++p) {
+        const int c = 8 * (tid + 256 * p);
+        if (c < H) {
+            v[p] = *reinterpret_cast<const u16x8*>(xr + c);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ss += bf2f(v[p][j]) * bf2f(v[p][j]);
+        }
+    }
+    ss = warp_sum(ss);
+    if (lane == 0) part[wave] = ss;
+    __syncthreads();
+    const float rstd = rsqrtf((part[0] + part[1] + part[2] + part[3]) / (float)H + eps);
+#pragma unroll
+    for (int p = 0; p < RN_PIECES; ++p) {
+        const int c = 8 * (tid + 256 * p);
+        if (c < H) {
+            u16x8 o;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) o[j] = f2bf(bf2f(v[p][j]) * rstd * (1.f + (w ? w[c + j] : 0.f)));
+            *reinterpret_cast<u16x8*>(y + (size_t)m * H + c) = o;
+        }
+    }
+}
+
+hipError_t launch_rmsnorm_rows(const u16* x, int M, int H, const float* w, float eps, u16* y, hipStream_t stream) {
+    if (M <= 0) return hipSuccess;
+    if (H % 8 || H > 256 * 8 * RN_PIECES) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(M), dim3(256), 0, stream, x, H, w, eps, y);
+    return hipGetLastError();
+}
+
+// ------------------------------------------------------------------------------------------------
 // State import / export / zero.  Export gives the conv history in time order [n, conv_dim, 3]
 // (q/k channels from the copy of the first v-head of each k-head group).
 // ------------------------------------------------------------------------------------------------

@@ -45,55 +45,74 @@ def _slots(slot_ids, device):
     return s
 
 
+def prepare_weights(weights, dims, device):
+    """(dims, C structs) for an HF layer or a weight dict: (dims dict, GdnDims, GdnWeights, tensors to keep
+    alive until the create call returns)."""
+    if hasattr(weights, "in_proj_qkv"):
+        dims_hf, weights = weights_from_hf(weights)
+        dims = dims or dims_hf
+    if dims is None:
+        raise ValueError("dims are required with a weight dict")
+    missing = [k for k in _WEIGHT_KEYS if k not in weights]
+    if missing:
+        raise ValueError(f"missing weights: {missing}")
+    d = dict(dims)
+
+    def bf16(t):
+        return torch.as_tensor(t).to(device=device, dtype=torch.bfloat16).contiguous()
+
+    def f32(t):
+        return torch.as_tensor(t).to(device=device, dtype=torch.float32).contiguous()
+
+    w = {k: (bf16(weights[k]) if k in ("w_qkv", "w_z", "w_a", "w_b", "w_out") else f32(weights[k]))
+         for k in _WEIGHT_KEYS}
+    cdims = _lib.GdnDims(d["hidden"], d["num_k_heads"], d["num_v_heads"], d["head_k_dim"], d["head_v_dim"],
+                         d.get("conv_kernel", 4), d.get("rms_norm_eps", 1e-6))
+    cw = _lib.GdnWeights(w["w_qkv"].data_ptr(), w["w_z"].data_ptr(), w["w_a"].data_ptr(), w["w_b"].data_ptr(),
+                         w["conv_w"].data_ptr(), w["A_log"].data_ptr(), w["dt_bias"].data_ptr(),
+                         w["norm_w"].data_ptr(), w["w_out"].data_ptr())
+    return d, cdims, cw, w
+
+
+def cu_seqlens_arg(cu_seqlens, n_seqs):
+    """Host int32 array [n_seqs + 1] for the varlen entries."""
+    cu = [int(v) for v in (cu_seqlens.tolist() if hasattr(cu_seqlens, "tolist") else cu_seqlens)]
+    if len(cu) != n_seqs + 1:
+        raise ValueError(f"cu_seqlens has {len(cu)} entries for {n_seqs} sequences")
+    return (ctypes.c_int * len(cu))(*cu)
+
+
 class Qwen35GatedDeltaNetHIP:
     """One GDN layer.  `weights` is an HF Qwen3_5GatedDeltaNet or a dict with keys
     w_qkv [conv_dim, H], w_z [Vd, H], w_a, w_b [nv, H], conv_w [conv_dim, 4], A_log, dt_bias [nv],
     norm_w [dv], w_out [H, Vd] (projection weights are used as bf16, the rest as fp32)."""
 
-    def __init__(self, weights, dims=None, batch=1, max_slots=None, max_tokens=16384, device="cuda"):
-        if hasattr(weights, "in_proj_qkv"):
-            dims_hf, weights = weights_from_hf(weights)
-            dims = dims or dims_hf
-        assert dims is not None, "dims are required with a weight dict"
-        missing = [k for k in _WEIGHT_KEYS if k not in weights]
-        if missing:
-            raise ValueError(f"missing weights: {missing}")
+    def __init__(self, weights, dims=None, batch=1, max_slots=None, max_tokens=16384, device="cuda", _handle=None):
         self.device = torch.device(device)
-        self.dims = dict(dims)
         self.batch = batch
         self.max_slots = max_slots or batch
         self.max_tokens = max_tokens
+        if _handle is not None:  # a layer owned by a stack
+            self.dims = dict(dims)
+            self._h, self._owned = _handle, False
+        else:
+            self.dims, cdims, cw, _keep = prepare_weights(weights, dims, self.device)
+            self._h, self._owned = ctypes.c_void_p(), True
+            torch.cuda.synchronize(self.device)
+            _lib.check(_lib.lib().gdn_layer_create(ctypes.byref(cdims), ctypes.byref(cw), self.max_slots,
+                                                   self.max_tokens, ctypes.byref(self._h)))
         d = self.dims
         self.hidden = d["hidden"]
         self.nk, self.nv = d["num_k_heads"], d["num_v_heads"]
         self.dk, self.dv = d["head_k_dim"], d["head_v_dim"]
         self.conv_dim = 2 * self.nk * self.dk + self.nv * self.dv
-
-        dev = self.device
-
-        def bf16(t):
-            return torch.as_tensor(t).to(device=dev, dtype=torch.bfloat16).contiguous()
-
-        def f32(t):
-            return torch.as_tensor(t).to(device=dev, dtype=torch.float32).contiguous()
-
-        w = {k: (bf16(weights[k]) if k in ("w_qkv", "w_z", "w_a", "w_b", "w_out") else f32(weights[k]))
-             for k in _WEIGHT_KEYS}
-        cdims = _lib.GdnDims(d["hidden"], d["num_k_heads"], d["num_v_heads"], d["head_k_dim"], d["head_v_dim"],
-                             d.get("conv_kernel", 4), d.get("rms_norm_eps", 1e-6))
-        cw = _lib.GdnWeights(w["w_qkv"].data_ptr(), w["w_z"].data_ptr(), w["w_a"].data_ptr(), w["w_b"].data_ptr(),
-                             w["conv_w"].data_ptr(), w["A_log"].data_ptr(), w["dt_bias"].data_ptr(),
-                             w["norm_w"].data_ptr(), w["w_out"].data_ptr())
-        self._h = ctypes.c_void_p()
-        torch.cuda.synchronize(dev)
-        _lib.check(_lib.lib().gdn_layer_create(ctypes.byref(cdims), ctypes.byref(cw), self.max_slots,
-                                               self.max_tokens, ctypes.byref(self._h)))
         self.proj_width = _lib.lib().gdn_layer_proj_width(self._h)
 
     # ---- lifetime ---------------------------------------------------------------------------------
     def close(self):
         if getattr(self, "_h", None) and self._h.value:
-            _lib.lib().gdn_layer_destroy(self._h)
+            if self._owned:
+                _lib.lib().gdn_layer_destroy(self._h)
             self._h = ctypes.c_void_p()
 
     def __del__(self):
@@ -113,6 +132,17 @@ class Qwen35GatedDeltaNetHIP:
         out = torch.empty_like(x)
         s = _slots(slot_ids, self.device)
         _lib.check(_lib.lib().gdn_layer_forward(self._h, _ptr(x), B, T, _ptr(s), _ptr(out), _stream()))
+        return out
+
+    def forward_varlen(self, x, cu_seqlens, slot_ids=None):
+        """x [total, H]: sequences of different lengths (rows cu_seqlens[i]..cu_seqlens[i+1]) in one launch,
+        sequence i continuing slot slot_ids[i] (default i) -> [total, H] bf16."""
+        n = len(cu_seqlens) - 1
+        x = x.to(device=self.device, dtype=torch.bfloat16).reshape(-1, self.hidden).contiguous()
+        out = torch.empty_like(x)
+        s = _slots(slot_ids, self.device)
+        _lib.check(_lib.lib().gdn_layer_forward_varlen(self._h, _ptr(x), n, cu_seqlens_arg(cu_seqlens, n), _ptr(s),
+                                                       _ptr(out), _stream()))
         return out
 
     def reset_state(self, slot_ids=None):
