@@ -155,6 +155,63 @@ def measure_traffic(kernel="mixer_kernel", timeout=180):
     return {"bytes": out["FETCH_SIZE"]["bytes"] + out["WRITE_SIZE"]["bytes"], "passes": out}, None
 
 
+def stack_bench(d, n_layers=24, n_prefill=8, prefill_len=2048, n_decode=56, steps=3, warmup=1, seed=4):
+    """Continuous batching through a stack of 9B-shape layers with the decoder RMSNorm between layers:
+    every step carries the next prefill_len tokens of n_prefill prompts (chunked prefill, states carried)
+    and one token for each of n_decode streams, in one variable-length launch per layer.  The decode
+    streams start from 0.01 randn states (a GDN state has constant size, so a long context only changes
+    its values).  Weights: projections N(0, 0.02) in bf16 drawn on the GPU, the rest as synthetic.py."""
+    import torch
+
+    from linear_attention_op_amd import Qwen35GDNStackHIP
+    from linear_attention_op_amd import synthetic as syn
+
+    dev = torch.device("cuda", 0)
+    gg = torch.Generator(device=dev).manual_seed(seed)
+    _, gen = syn.make_weights(syn.SHAPES["tiny"], seed=seed)
+    H, nv, dv, C = d["hidden"], d["num_v_heads"], d["head_v_dim"], syn.conv_dim(d)
+    Vd = nv * dv
+
+    def n(*shape):
+        return (torch.randn(*shape, generator=gg, device=dev) * 0.02).to(torch.bfloat16)
+
+    layers = []
+    for _ in range(n_layers):
+        layers.append({"w_qkv": n(C, H), "w_z": n(Vd, H), "w_a": n(nv, H), "w_b": n(nv, H),
+                       "conv_w": n(C, 4).float(), "w_out": n(H, Vd),
+                       "norm_w": torch.rand(dv, generator=gen) + 0.5,
+                       "dt_bias": torch.rand(nv, generator=gen) * 2.0 - 1.0,
+                       "A_log": torch.log(torch.rand(nv, generator=gen) * 16.0).clamp_min(-20.0)})
+    n_seq = n_prefill + n_decode
+    rows = n_prefill * prefill_len + n_decode
+    stack = Qwen35GDNStackHIP(layers, dims=d, batch=n_seq, max_slots=n_seq, max_tokens=rows, inter_norm=True)
+    del layers
+    dec_slots = torch.arange(n_prefill, n_seq, dtype=torch.int32, device=dev)
+    for L in stack.layers:
+        L.set_state(rec=torch.randn(n_decode, nv, d["head_k_dim"], dv, generator=gg, device=dev) * 0.01,
+                    slot_ids=dec_slots)
+    cu = [0]
+    for i in range(n_seq):
+        cu.append(cu[-1] + (prefill_len if i < n_prefill else 1))
+    slots = torch.arange(n_seq, dtype=torch.int32, device=dev)
+    xs = [torch.randn(rows, H, generator=gg, device=dev).to(torch.bfloat16) for _ in range(2)]
+    for i in range(warmup):
+        stack.forward_varlen(xs[i % 2], cu, slots)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        stack.forward_varlen(xs[i % 2], cu, slots)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    stack.close()
+    flops = n_layers * rows * prefill_flops_per_token(d)
+    return {"workload": f"{n_layers} 9B-shape GDN layers with RMSNorm between layers, continuous batch of "
+                        f"{n_prefill} prefills x {prefill_len} tokens + {n_decode} decode streams per step",
+            "tokens_per_step": rows, "ms_per_step": dt * 1e3, "tok_per_s": rows / dt, "steps": steps,
+            "roofline": {"bound": "mfma", "achieved": flops / dt / 1e12, "peak": BF16_PEAK / 1e12,
+                         "unit": "TFLOP/s", "frac": flops / dt / BF16_PEAK, "flops": flops}}
+
+
 def main():
     if "--pmc-child" in sys.argv:
         pmc_child()
@@ -172,6 +229,8 @@ def main():
     ap.add_argument("--graph", type=int, default=0,
                     help="1: replay the decode step from HIP graphs; 0: launch eagerly (faster here: 104 vs 112 us)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--stack", action="store_true",
+                    help="also run the 24-layer continuous-batching stack (8 x 2048 prefill + 56 decode per step)")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 counter passes (required when bench.py itself runs under rocprofv3)")
     args = ap.parse_args()
@@ -312,6 +371,13 @@ def main():
         print(f"[bench] prefill T={T}: {ev * 1e3:.2f} ms, {T / ev:.0f} tok/s", file=sys.stderr, flush=True)
         lay.close()
 
+    stack = None
+    if args.stack:
+        print("[bench] 24-layer continuous-batching stack", file=sys.stderr, flush=True)
+        stack = stack_bench(d)
+        print(f"[bench] stack: {stack['ms_per_step']:.1f} ms/step, {stack['tok_per_s']:.0f} tok/s", file=sys.stderr,
+              flush=True)
+
     cpu = None
     if not args.no_cpu:
         print("[bench] timing the CPU oracle", file=sys.stderr, flush=True)
@@ -325,7 +391,7 @@ def main():
                                f"rotating over {L} layer copies" + (", HIP-graph replay" if args.graph else ""),
                    "hidden": d["hidden"], "num_k_heads": d["num_k_heads"], "num_v_heads": d["num_v_heads"],
                    "head_dim": 128, "batch": B, "state_dtype": "fp32", "weights": "bf16 N(0,0.02) seed 2"},
-        "roofline": roofline, "layer_roofline": layer_roof, "prefill": prefill, "cpu_baseline": cpu,
+        "roofline": roofline, "layer_roofline": layer_roof, "prefill": prefill, "stack": stack, "cpu_baseline": cpu,
     }
     print(json.dumps(line))
 
