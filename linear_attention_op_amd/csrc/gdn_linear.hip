@@ -13,9 +13,9 @@
 //    barriers in the loop), then the partials are summed through LDS and written once, coalesced.
 //    Activations may come in the same fragment layout (rows padded to 16 with zeros), which turns
 //    every x load into 1 KB of contiguous memory as well.
-//  * gemm_kernel / gemm256_kernel (M > 64, prefill): LDS-tiled GEMM on v_mfma_f32_32x32x16_bf16 with
-//    register-staged double buffering, 128x128 tiles (4 waves of 64x64) for small problems and 256x256
-//    tiles (8 waves of 128x64) once there are enough tiles to fill the chip;
+//  * gemm_kernel / gemm256_kernel (M > 64, prefill): LDS-tiled GEMM on v_mfma_f32_32x32x16_bf16, 128x128
+//    tiles (4 waves of 64x64, register-staged double buffering) for small problems and software-pipelined
+//    256x256 tiles (4 waves of 128x128) once there are enough tiles to fill the chip;
 //    tiles are rasterised per XCD in groups of 8 M-tiles so that workgroups running together on one
 //    XCD share A and B tiles in its L2.
 #include "gdn_common.h"
@@ -279,22 +279,28 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
 
 
 // ------------------------------------------------------------------------------------------------
-// Large GEMM: 256 x 256 x 64 block tile, 8 waves (2 x 4) of 128 x 64, 32x32x16 MFMA.  A and B tiles are
-// double-buffered in LDS (2 x 72 KB, one workgroup per CU) and staged through registers one k-step
-// ahead; two waves per SIMD hide each other's LDS and MFMA latencies.
+// Large GEMM: 256 x 256 x 64 block tile, 4 waves of 128 x 128 (4 x 4 tiles of 32x32x16 MFMA, 256 fp32
+// accumulators per lane in AGPRs), software-pipelined:
+//  * two register staging sets: the global loads of k-tile kt + 2 are issued while tile kt is computed
+//    and tile kt + 1 (loaded one step earlier) is stored to the other LDS buffer;
+//  * LDS rows padded to 72 bf16 (conflict-free 16-byte fragment reads), double-buffered (147 KB);
+//  * in each k-tile the fragment reads of the next k-16 sub-step, the global loads and the LDS stores are
+//    threaded one by one between the 64 MFMAs (scheduling groups), and the tile ends with an LDS-only
+//    barrier, so global loads stay in flight across it.
+// The main loop is branch-free (loads past the last k-tile re-read it); K % 128 == 0.
 // ------------------------------------------------------------------------------------------------
 constexpr int LBM = 256, LBN = 256, LBK = 64, LLD = LBK + 8;
 
+__device__ __forceinline__ int lds_off(int row, int ch) { return row * LLD + (ch << 3); }
+
 template <int OUT, int WL>
-__global__ __launch_bounds__(512, 2) void gemm256_kernel(const u16* __restrict__ x, const u16* __restrict__ w, int M,
+__global__ __launch_bounds__(256, 1) void gemm256_kernel(const u16* __restrict__ x, const u16* __restrict__ w, int M,
                                                          int N, int K, void* __restrict__ y) {
     __shared__ __attribute__((aligned(16))) u16 As[2][LBM * LLD];
     __shared__ __attribute__((aligned(16))) u16 Bs[2][LBN * LLD];
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63;
-    const int wave = tid >> 6;
-    const int wm = wave >> 2, wn = wave & 3;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
 
     const int TM = (M + LBM - 1) / LBM, TN = (N + LBN - 1) / LBN, total = TM * TN;
     const int id = blockIdx.x, per = total / 8;
@@ -304,93 +310,122 @@ __global__ __launch_bounds__(512, 2) void gemm256_kernel(const u16* __restrict__
     const int gm = min(TM - first_m, GROUP_M);
     const int tm = first_m + (t % gsz) % gm, tn = (t % gsz) / gm;
     const int m0 = tm * LBM, n0 = tn * LBN;
+    const int KQ = K >> 5, NT = (N + 15) >> 4;
 
-    // 2048 16-byte pieces per operand tile, 4 per thread
-    u16x8 ra[4], rb[4];
-    const u16* ag[4];
-    const u16* bg[4];
-    int soffa[4], soffb[4];
-    const int NT = (N + 15) >> 4;
+    // staging: 8 A and 8 B pieces of 16 bytes per thread and k-tile
+    const u16* ag[8];
+    const u16* bg[8];
+    int sa[8], sb[8];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int c = tid + 512 * j;
-        const int row = c >> 3, col = (c & 7) * 8;
-        ag[j] = x + (size_t)min(m0 + row, M - 1) * K + col;
-        soffa[j] = row * LLD + col;
-        if (WL == W_FRAG) {
+    for (int j = 0; j < 8; ++j) {
+        const int c = tid + 256 * j;
+        const int row = c >> 3, ch = c & 7;
+        ag[j] = x + (size_t)min(m0 + row, M - 1) * K + ch * 8;
+        sa[j] = lds_off(row, ch);
+        if (WL == W_FRAG) {  // piece c of the 32 fragment blocks (16 n-tiles x 2 k-steps) of the tile
             const int blk = c >> 6, l = c & 63;
             const int ntl = blk >> 1, kql = blk & 1;
-            bg[j] = w + ((size_t)min((n0 >> 4) + ntl, NT - 1) * (K >> 5) + kql) * 512 + l * 8;
-            soffb[j] = (16 * ntl + (l & 15)) * LLD + 32 * kql + 8 * (l >> 4);
+            bg[j] = w + ((size_t)min((n0 >> 4) + ntl, NT - 1) * KQ + kql) * 512 + l * 8;
+            sb[j] = lds_off(16 * ntl + (l & 15), 4 * kql + (l >> 4));
         } else {
-            bg[j] = w + (size_t)min(n0 + row, N - 1) * K + col;
-            soffb[j] = row * LLD + col;
+            bg[j] = w + (size_t)min(n0 + row, N - 1) * K + ch * 8;
+            sb[j] = lds_off(row, ch);
         }
     }
-    constexpr size_t BSTEP = WL == W_FRAG ? 1024 : LBK;
+    constexpr int BSTEP = WL == W_FRAG ? 1024 : LBK;  // elements per k-tile along a B piece's stream
+    const int nk = K / LBK;
 
-    f32x16 acc[4][2];
+    u16x8 ra0[8], rb0[8], ra1[8], rb1[8];
+    auto gload = [&](u16x8* ra, u16x8* rb, int kt) {
+        const int k = min(kt, nk - 1);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            ra[j] = *reinterpret_cast<const u16x8*>(ag[j] + (size_t)k * LBK);
+            rb[j] = *reinterpret_cast<const u16x8*>(bg[j] + (size_t)k * BSTEP);
+        }
+    };
+    auto lstore = [&](const u16x8* ra, const u16x8* rb, int buf) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            *reinterpret_cast<u16x8*>(&As[buf][sa[j]]) = ra[j];
+            *reinterpret_cast<u16x8*>(&Bs[buf][sb[j]]) = rb[j];
+        }
+    };
+
+    f32x16 acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j)
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
-    const int nk = K / LBK;
+    const int fr = lane & 31, fh = lane >> 5;
+    int aoff[4], boff[4];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        ra[j] = *reinterpret_cast<const u16x8*>(ag[j]);
-        rb[j] = *reinterpret_cast<const u16x8*>(bg[j]);
+    for (int i = 0; i < 4; ++i) {
+        aoff[i] = wm * 128 + i * 32 + fr;
+        boff[i] = wn * 128 + i * 32 + fr;
     }
+    auto rdfrag = [&](int buf, int s, bf16x8* a, bf16x8* b) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        *reinterpret_cast<u16x8*>(&As[0][soffa[j]]) = ra[j];
-        *reinterpret_cast<u16x8*>(&Bs[0][soffb[j]]) = rb[j];
-    }
-    __syncthreads();
+        for (int i = 0; i < 4; ++i) {
+            a[i] = *reinterpret_cast<const bf16x8*>(&As[buf][lds_off(aoff[i], 2 * s + fh)]);
+            b[i] = *reinterpret_cast<const bf16x8*>(&Bs[buf][lds_off(boff[i], 2 * s + fh)]);
+        }
+    };
+    auto mma = [&](const bf16x8* a, const bf16x8* b) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+    };
+    // one k-tile on LDS buffer `buf`, loading tile kt_ld into (ra_ld, rb_ld) and storing (ra_st, rb_st)
+    // into the other buffer
+    auto tile = [&](int buf, u16x8* ra_ld, u16x8* rb_ld, const u16x8* ra_st, const u16x8* rb_st, int kt_ld) {
+        bf16x8 a0[4], b0[4], a1[4], b1[4];
+        rdfrag(buf, 0, a0, b0);
+        rdfrag(buf, 1, a1, b1);
+        gload(ra_ld, rb_ld, kt_ld);
+        mma(a0, b0);
+        rdfrag(buf, 2, a0, b0);
+        mma(a1, b1);
+        rdfrag(buf, 3, a1, b1);
+        lstore(ra_st, rb_st, buf ^ 1);
+        mma(a0, b0);
+        mma(a1, b1);
+        // 8 fragment reads up front; then per k-16 sub-step 16 MFMAs, each of the first 8 followed by a
+        // fragment read (sub-steps 0-2), the last 8 by two global loads (0-1) or an LDS store (2); in
+        // sub-step 3 the first 8 by an LDS store
+        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+        for (int ss = 0; ss < 4; ++ss)
+            for (int m = 0; m < 16; ++m) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                if (ss < 3 && m < 8)
+                    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                else if (ss < 2)
+                    __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
+                else if ((ss == 2 && m >= 8) || (ss == 3 && m < 8))
+                    __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
+            }
+        lds_barrier();
+    };
 
-    const int fr = lane & 31;
-    const int fk = (lane >> 5) * 8;
-    for (int kt = 0; kt < nk; ++kt) {
-        const int cur = kt & 1;
-        if (kt + 1 < nk) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                ra[j] = *reinterpret_cast<const u16x8*>(ag[j] + (size_t)(kt + 1) * LBK);
-                rb[j] = *reinterpret_cast<const u16x8*>(bg[j] + (size_t)(kt + 1) * BSTEP);
-            }
-        }
-        const u16* Ab = &As[cur][(wm * 128 + fr) * LLD + fk];
-        const u16* Bb = &Bs[cur][(wn * 64 + fr) * LLD + fk];
-#pragma unroll
-        for (int kk = 0; kk < LBK; kk += 16) {
-            bf16x8 a[4], b[2];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) a[i] = *reinterpret_cast<const bf16x8*>(Ab + i * 32 * LLD + kk);
-#pragma unroll
-            for (int j = 0; j < 2; ++j) b[j] = *reinterpret_cast<const bf16x8*>(Bb + j * 32 * LLD + kk);
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-                for (int j = 0; j < 2; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
-        }
-        if (kt + 1 < nk) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                *reinterpret_cast<u16x8*>(&As[cur ^ 1][soffa[j]]) = ra[j];
-                *reinterpret_cast<u16x8*>(&Bs[cur ^ 1][soffb[j]]) = rb[j];
-            }
-        }
-        __syncthreads();
+    gload(ra0, rb0, 0);
+    gload(ra1, rb1, 1);
+    lstore(ra0, rb0, 0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt += 2) {
+        tile(0, ra0, rb0, ra1, rb1, kt + 2);
+        tile(1, ra1, rb1, ra0, rb0, kt + 3);
     }
 
     // C layout of 32x32 MFMA: lane l, element e -> row 8*(e/4) + 4*(l/32) + e%4, column l % 32.
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int col = n0 + wn * 64 + j * 32 + (lane & 31);
+        for (int j = 0; j < 4; ++j) {
+            const int col = n0 + wn * 128 + j * 32 + (lane & 31);
             if (col >= N) continue;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
@@ -451,10 +486,10 @@ hipError_t linear_wl(const void* x, int xlayout, const void* w, int M, int N, in
     if ((size_t)M * N >= (size_t)256 * 256 * 256) {  // >= one round of 256 x 256 tiles over the CUs
         const dim3 grid(((M + LBM - 1) / LBM) * ((N + LBN - 1) / LBN));
         if (out_kind == OUT_F32)
-            hipLaunchKernelGGL((gemm256_kernel<OUT_F32, WL>), grid, dim3(512), 0, stream, (const u16*)x,
+            hipLaunchKernelGGL((gemm256_kernel<OUT_F32, WL>), grid, dim3(256), 0, stream, (const u16*)x,
                                (const u16*)w, M, N, K, y);
         else
-            hipLaunchKernelGGL((gemm256_kernel<OUT_BF16, WL>), grid, dim3(512), 0, stream, (const u16*)x,
+            hipLaunchKernelGGL((gemm256_kernel<OUT_BF16, WL>), grid, dim3(256), 0, stream, (const u16*)x,
                                (const u16*)w, M, N, K, y);
         return hipGetLastError();
     }
