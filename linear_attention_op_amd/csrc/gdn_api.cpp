@@ -42,6 +42,8 @@ int fail(int code, const char* fmt, ...) {
 
 // Prefills longer than this many tokens per sequence use the token-parallel front end + chunked rule.
 constexpr int kFusedMaxT = 64;
+// k ranges of the a | b rows in the decode in_proj (the mixer adds the partial sums)
+constexpr int kAbSplits = 8;
 
 bool supported_head_dim(int d) { return d == 32 || d == 64 || d == 128; }
 
@@ -78,6 +80,7 @@ struct gdn_layer {
     float* beta = nullptr;    // [max_tokens, nv]
     float* o = nullptr;       // [max_tokens, Vd]
     u16* y = nullptr;         // [max_tokens, Vd]
+    float* ab = nullptr;      // [kAbSplits, 64, 2 nv] partial a | b of the decode in_proj
     void* chunk_ws = nullptr;
     size_t chunk_ws_bytes = 0;
 
@@ -158,9 +161,21 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, u16* o
     const bool frag = M <= 64;
     // the fused mixer writes y straight into W_FRAG layout when it produces every row
     const bool y_frag = frag && ng == 1 && grp[0].T <= kFusedMaxT;
-    if (frag) HIP_OK(gdn::launch_frag_tile(x, M, d.hidden, L->x_frag, st));
-    HIP_OK(gdn::launch_linear(frag ? L->x_frag : x, frag ? gdn::W_FRAG : gdn::W_ROW, L->w_in, gdn::W_FRAG, M, L->NP,
-                              d.hidden, L->P, gdn::OUT_F32, st));
+    // decode: q | k | v | z over workgroups balanced on the CUs, a | b as partial sums for the mixer
+    const bool split_ab = frag && L->CD + Vd == L->NP - 2 * nv;
+    bool ab_split = false;
+    if (frag) {
+        HIP_OK(gdn::launch_frag_tile(x, M, d.hidden, L->x_frag, st));
+        bool mixer_only = true;
+        for (int gi = 0; gi < ng; ++gi) mixer_only = mixer_only && grp[gi].T <= kFusedMaxT;
+        ab_split = split_ab && mixer_only;
+    }
+    if (ab_split)
+        HIP_OK(gdn::launch_in_proj_decode(L->x_frag, L->w_in, M, L->CD + Vd, 2 * nv, d.hidden, L->P, L->NP, L->ab,
+                                          kAbSplits, st));
+    else
+        HIP_OK(gdn::launch_linear(frag ? L->x_frag : x, frag ? gdn::W_FRAG : gdn::W_ROW, L->w_in, gdn::W_FRAG, M,
+                                  L->NP, d.hidden, L->P, gdn::OUT_F32, st));
     if (ev[1]) HIP_OK(hipEventRecord(ev[1], st));
     for (int gi = 0; gi < ng; ++gi) {
         const Group& g = grp[gi];
@@ -174,6 +189,8 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, u16* o
             a.eps = d.rms_norm_eps;
             a.rec_state = L->rec, a.conv_state = L->conv;
             a.y = y_frag ? L->y : L->y + r0 * Vd, a.y_frag = y_frag ? 1 : 0, a.o_tap = nullptr;
+            a.ab = ab_split ? L->ab + r0 * 2 * nv : nullptr, a.ab_splits = kAbSplits;
+            a.ab_stride = (size_t)M * 2 * nv;
             HIP_OK(gdn::launch_mixer(a, d.head_k_dim, d.head_v_dim, st));
         } else {
             float* P = L->P + r0 * L->NP;
@@ -306,6 +323,7 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
         L->x_ws = share->x_ws, L->x_frag = share->x_frag, L->out_ws = share->out_ws, L->P = share->P;
         L->qn = share->qn, L->kn = share->kn, L->v = share->v, L->g = share->g, L->beta = share->beta;
         L->o = share->o, L->y = share->y, L->chunk_ws = share->chunk_ws, L->chunk_ws_bytes = share->chunk_ws_bytes;
+        L->ab = share->ab;
     } else {
         take(L->alloc(&L->x_ws, MT * H, true));
         take(L->alloc(&L->x_frag, gdn::frag_elems(64, H), true));
@@ -318,6 +336,7 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
         take(L->alloc(&L->beta, MT * nv, true));
         take(L->alloc(&L->o, MT * L->Vd, true));
         take(L->alloc(&L->y, std::max(MT * L->Vd, gdn::frag_elems(64, L->Vd)), true));  // W_FRAG y pads rows to 16
+        take(L->alloc(&L->ab, (size_t)kAbSplits * 64 * 2 * nv, true));
         if (max_tokens > kFusedMaxT && gdn::delta_chunked_supported(dk, dv)) {
             // chunked-prefill workspace for the worst launch: sequences of T > kFusedMaxT tokens with
             // at most max_tokens rows in all hold at most max_tokens / 64 + max_tokens / 65 + 1 chunks

@@ -99,6 +99,11 @@ enum WLayout { W_ROW = 0, W_FRAG = 1 };
 // x in `xlayout` (W_FRAG activations only for M <= 64).
 hipError_t launch_linear(const void* x, int xlayout, const void* w, int wlayout, int M, int N, int K, void* y,
                          int out_kind, hipStream_t stream);
+// Decode in_proj on W_FRAG weights and activations (M <= 64): rows [0, N1) of w into P (fp32, row stride
+// ldp) with the workgroups balanced over the CUs; the next N2 rows as ab_splits partial sums over k
+// ranges into Pab [ab_splits][M][N2] (the consumer adds the slices).  N1 % 16 == 0.
+hipError_t launch_in_proj_decode(const void* x_frag, const void* w_frag, int M, int N1, int N2, int K, float* P,
+                                 int ldp, float* Pab, int ab_splits, hipStream_t stream);
 // Elements of an [N, K] matrix in W_FRAG layout (rows padded to a multiple of 16).
 size_t frag_elems(int N, int K);
 // Convert a row-major device matrix [N, K] into W_FRAG layout (frag_elems(N, K) elements).
@@ -124,6 +129,11 @@ struct MixerArgs {
     u16* y;                 // [M, nv * dv] bf16 gated RMSNorm output
     int y_frag;             // 1: y in W_FRAG layout (rows padded to 16; M <= 64), 0: row-major
     float* o_tap;           // optional [M, nv * dv] recurrence output (nullptr: not written)
+    // optional: a | b as ab_splits partial sums, slice s row m at ab[s * ab_stride + m * 2 nv] (then
+    // the a | b columns of P are not read)
+    const float* ab;
+    int ab_splits;
+    size_t ab_stride;
 };
 hipError_t launch_mixer(const MixerArgs& a, int dk, int dv, hipStream_t stream);
 

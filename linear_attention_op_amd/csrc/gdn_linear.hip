@@ -57,19 +57,20 @@ __device__ __forceinline__ bf16x8 ldw(const u16* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(p));
 }
 
+// One workgroup of the GEMV: rows [n0, n0 + 16 NTS) of w (of N) against the M rows of x over the k-steps
+// [kqb, kqb + kqn) of 32, written to y[m * ldy + n] (the partial sum of that K range).
 template <int NTS, int MT, int NW, int PD, int OUT, int WL, int XL>
-__global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x, const u16* __restrict__ w, int M,
-                                                      int N, int K, void* __restrict__ y) {
+__device__ __forceinline__ void gemv_block(const u16* __restrict__ x, const u16* __restrict__ w, int M, int N, int K,
+                                           void* __restrict__ y, int ldy, int n0, int kqb, int kqn) {
     constexpr int BN = NTS * 16, BM = MT * 16;
     __shared__ float red[NW][BM][BN + 1];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int KQ = K >> 5;
-    const int kq_per = (KQ + NW - 1) / NW;
-    const int kq0 = min(KQ, wave * kq_per);
-    const int nsteps = min(KQ, kq0 + kq_per) - kq0;
-    const int n0 = blockIdx.x * BN;
+    const int kq_per = (kqn + NW - 1) / NW;
+    const int kq0 = kqb + min(kqn, wave * kq_per);
+    const int nsteps = kqb + min(kqn, (wave + 1) * kq_per) - kq0;
     const int NT = (N + 15) >> 4;
 
     // fragment base pointers and per-k-step strides
@@ -148,7 +149,35 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x
         float s = 0.f;
 #pragma unroll
         for (int wv = 0; wv < NW; ++wv) s += red[wv][m][nl];
-        store_out<OUT>(y, (size_t)m * N + n, s);
+        store_out<OUT>(y, (size_t)m * ldy + n, s);
+    }
+}
+
+template <int NTS, int MT, int NW, int PD, int OUT, int WL, int XL>
+__global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x, const u16* __restrict__ w, int M,
+                                                      int N, int K, void* __restrict__ y) {
+    gemv_block<NTS, MT, NW, PD, OUT, WL, XL>(x, w, M, N, K, y, N, blockIdx.x * NTS * 16, 0, K >> 5);
+}
+
+// Decode in_proj (fragment-layout weights and activations, fp32 out), balanced over the CUs: workgroups
+// [0, G) own NTS row tiles each of the first N1 rows (G = N1 / (16 NTS), chosen ~ one per CU) and write
+// them to P (row stride ldp); the remaining N2 rows (the a | b projection, 64 rows at 9B) are split into
+// KS k-ranges over workgroups [G, G + ceil(N2 / 16) KS), each writing its partial sums to slice ks of
+// Pab [KS][M][N2], which the mixer adds up.  One launch, no tail of half-used CUs.
+template <int NTS, int MT, int NW, int PD>
+__global__ __launch_bounds__(NW * 64) void in_proj_decode_kernel(const u16* __restrict__ x, const u16* __restrict__ w,
+                                                                int M, int N1, int N2, int K, int G, int KS,
+                                                                float* __restrict__ P, int ldp, float* __restrict__ Pab) {
+    const int bid = blockIdx.x;
+    if (bid < G) {
+        gemv_block<NTS, MT, NW, PD, OUT_F32, W_FRAG, W_FRAG>(x, w, M, N1, K, P, ldp, bid * NTS * 16, 0, K >> 5);
+    } else {
+        const int e = bid - G, nt = e % ((N2 + 15) >> 4), ks = e / ((N2 + 15) >> 4);
+        const int KQ = K >> 5, per = (KQ + KS - 1) / KS;
+        const int kqb = min(KQ, ks * per), kqn = min(KQ, kqb + per) - kqb;
+        const u16* w2 = w + (size_t)(N1 >> 4) * KQ * 512;  // first fragment row of the split rows
+        gemv_block<1, MT, NW, PD, OUT_F32, W_FRAG, W_FRAG>(x, w2, M, N2, K, Pab + (size_t)ks * M * N2, N2, nt * 16,
+                                                          kqb, kqn);
     }
 }
 
@@ -512,6 +541,40 @@ hipError_t launch_frag_tile(const void* w, int N, int K, void* wf, hipStream_t s
     hipLaunchKernelGGL(frag_tile_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, stream, (const u16*)w,
                        N, K, (u16*)wf);
     return hipGetLastError();
+}
+
+namespace {
+
+template <int MT>
+hipError_t in_proj_decode_mt(const void* x, const void* w, int M, int N1, int N2, int K, float* P, int ldp,
+                             float* Pab, int ab_splits, hipStream_t stream) {
+    constexpr int PD = 4, NW = 4;
+    const int NT1 = N1 >> 4, NT2 = (N2 + 15) >> 4;
+    // tiles per workgroup: the smallest that keeps the main workgroups within one per CU
+    const int nts = NT1 <= 256 ? 1 : (NT1 <= 512 ? 2 : (NT1 <= 768 ? 3 : 4));
+    if (NT1 % nts) return hipErrorInvalidValue;
+    const int G = NT1 / nts;
+    const dim3 grid(G + NT2 * ab_splits), block(NW * 64);
+    const u16 *xs = (const u16*)x, *ws = (const u16*)w;
+    switch (nts) {
+        case 1: hipLaunchKernelGGL((in_proj_decode_kernel<1, MT, NW, PD>), grid, block, 0, stream, xs, ws, M, N1, N2, K, G, ab_splits, P, ldp, Pab); break;
+        case 2: hipLaunchKernelGGL((in_proj_decode_kernel<2, MT, NW, PD>), grid, block, 0, stream, xs, ws, M, N1, N2, K, G, ab_splits, P, ldp, Pab); break;
+        case 3: hipLaunchKernelGGL((in_proj_decode_kernel<3, MT, NW, PD>), grid, block, 0, stream, xs, ws, M, N1, N2, K, G, ab_splits, P, ldp, Pab); break;
+        default: hipLaunchKernelGGL((in_proj_decode_kernel<4, MT, NW, PD>), grid, block, 0, stream, xs, ws, M, N1, N2, K, G, ab_splits, P, ldp, Pab); break;
+    }
+    return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_in_proj_decode(const void* x_frag, const void* w_frag, int M, int N1, int N2, int K, float* P,
+                                 int ldp, float* Pab, int ab_splits, hipStream_t stream) {
+    if (M <= 0) return hipSuccess;
+    if (M > 64 || N1 % 16 || ab_splits <= 0 || K % 32) return hipErrorInvalidValue;
+    if (M <= 16) return in_proj_decode_mt<1>(x_frag, w_frag, M, N1, N2, K, P, ldp, Pab, ab_splits, stream);
+    if (M <= 32) return in_proj_decode_mt<2>(x_frag, w_frag, M, N1, N2, K, P, ldp, Pab, ab_splits, stream);
+    if (M <= 48) return in_proj_decode_mt<3>(x_frag, w_frag, M, N1, N2, K, P, ldp, Pab, ab_splits, stream);
+    return in_proj_decode_mt<4>(x_frag, w_frag, M, N1, N2, K, P, ldp, Pab, ab_splits, stream);
 }
 
 hipError_t launch_linear(const void* x, int xlayout, const void* w, int wlayout, int M, int N, int K, void* y,

@@ -64,7 +64,23 @@ __global__ __launch_bounds__(256) void mixer_kernel(MixerArgs a) {
             xin[c] = Prow[pcol[c]];
         }
     }
-    float av = Prow[CD + Vd + h], bv = Prow[CD + Vd + nv + h];
+    // gating inputs a, b of row m: from P, or summed over the partial slices of the split in_proj
+    // (lane q of every wave loads slice q; the slices are summed with a wave reduction)
+    auto load_ab = [&](size_t m, float& av_, float& bv_) {
+        if (a.ab) {
+            float sa = 0.f, sb = 0.f;
+            if (lane < a.ab_splits) {
+                const float* r = a.ab + lane * a.ab_stride + m * 2 * nv;
+                sa = r[h], sb = r[nv + h];
+            }
+            av_ = warp_sum(sa), bv_ = warp_sum(sb);
+        } else {
+            const float* r = a.P + m * a.NP + CD + Vd;
+            av_ = r[h], bv_ = r[nv + h];
+        }
+    };
+    float av, bv;
+    load_ab((size_t)b * T, av, bv);
     float4 zv = make_float4(0.f, 0.f, 0.f, 0.f), nw = zv;
     if (tid < Tile::CG) {
         zv = *reinterpret_cast<const float4*>(Prow + CD + h * DV + 4 * tid);
@@ -106,7 +122,7 @@ __global__ __launch_bounds__(256) void mixer_kernel(MixerArgs a) {
 #pragma unroll
             for (int c = 0; c < CPT; ++c)
                 if (tid + 256 * c < CH) xin[c] = Pn[pcol[c]];
-            av_n = Pn[CD + Vd + h], bv_n = Pn[CD + Vd + nv + h];
+            load_ab(m + 1, av_n, bv_n);
             if (tid < Tile::CG) zv_n = *reinterpret_cast<const float4*>(Pn + CD + h * DV + 4 * tid);
         }
         __syncthreads();
