@@ -108,6 +108,14 @@ class Qwen35GatedDeltaNetHIP:
         self.conv_dim = 2 * self.nk * self.dk + self.nv * self.dv
         self.proj_width = _lib.lib().gdn_layer_proj_width(self._h)
 
+    @classmethod
+    def from_checkpoint(cls, path, layer_idx, prefix=None, **kwargs):
+        """Layer `layer_idx` of a local safetensors checkpoint (file or directory; see checkpoint.py)."""
+        from .checkpoint import load_gdn_weights
+
+        dims, w = load_gdn_weights(path, layer_idx, prefix)
+        return cls(w, dims=dims, **kwargs)
+
     # ---- lifetime ---------------------------------------------------------------------------------
     def close(self):
         if getattr(self, "_h", None) and self._h.value:

@@ -54,6 +54,16 @@ class Qwen35GDNStackHIP:
             self.layers.append(Qwen35GatedDeltaNetHIP(None, dims=self.dims, batch=batch, max_slots=self.max_slots,
                                                       max_tokens=self.max_tokens, device=device, _handle=h))
 
+    @classmethod
+    def from_checkpoint(cls, path, layers=None, prefix=None, **kwargs):
+        """The GDN layers `layers` (default: every linear-attention layer, in order) of a local safetensors
+        checkpoint, stacked."""
+        from .checkpoint import linear_attention_layers, load_gdn_weights
+
+        idx = linear_attention_layers(path, prefix) if layers is None else list(layers)
+        loaded = [load_gdn_weights(path, i, prefix) for i in idx]
+        return cls([w for _, w in loaded], dims=loaded[0][0], **kwargs)
+
     def close(self):
         if getattr(self, "_h", None) and self._h.value:
             for L in self.layers:

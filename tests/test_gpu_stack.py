@@ -169,3 +169,31 @@ def test_varlen_equals_separate_launches(shape, lens):
     print(f"  out {r:.2e} state {rs:.2e}", flush=True)
     assert r < 2e-3 and rs < 1e-4
     assert rel(a.get_conv_state(slots), b.get_conv_state(slots)) < 1e-5
+
+
+def test_layer_and_stack_from_checkpoint(tmp_path):
+    """A layer and a stack built from a local safetensors checkpoint run exactly like the ones built from
+    the same weights in memory."""
+    from safetensors.torch import save_file
+
+    print("from_checkpoint", flush=True)
+    d = syn.SHAPES["0.8b"]
+    ws, gen = make_layers(d, 2, seed=61)
+    names = {"w_qkv": "in_proj_qkv.weight", "w_z": "in_proj_z.weight", "w_a": "in_proj_a.weight",
+             "w_b": "in_proj_b.weight", "conv_w": "conv1d.weight", "A_log": "A_log", "dt_bias": "dt_bias",
+             "norm_w": "norm.weight", "w_out": "out_proj.weight"}
+    t = {}
+    for i, w in enumerate(ws):
+        for k, n in names.items():
+            v = w[k].bfloat16() if k in ("w_qkv", "w_z", "w_a", "w_b", "w_out") else w[k].float()
+            t[f"model.layers.{i}.linear_attn.{n}"] = (v[:, None, :] if k == "conv_w" else v).contiguous()
+    save_file(t, str(tmp_path / "model.safetensors"))
+    B = 2
+    x, _ = syn.make_inputs(d, B, 3, gen)
+    a = Qwen35GatedDeltaNetHIP.from_checkpoint(str(tmp_path), 1, batch=B, max_tokens=64)
+    b = Qwen35GatedDeltaNetHIP(ws[1], dims=d, batch=B, max_tokens=64)
+    assert torch.equal(a(x.cuda()), b(x.cuda()))
+    sa = Qwen35GDNStackHIP.from_checkpoint(str(tmp_path), batch=B)
+    sb = Qwen35GDNStackHIP(ws, dims=d, batch=B)
+    assert sa.n_layers == 2
+    assert torch.equal(sa(x[:, 0].cuda()), sb(x[:, 0].cuda()))
