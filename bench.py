@@ -27,15 +27,48 @@ HBM_PEAK = 8.0e12        # B/s, MI355X HBM3E
 BF16_PEAK = 2.5e15       # FLOP/s, MI355X dense bf16 MFMA
 
 
-def decode_bytes(d, B):
+def decode_bytes(d, B, fp8=False):
     """Algorithmic HBM bytes of one decode layer step: weights once plus per-sequence state and I/O.
-    W = bf16 projections (qkv, z, a, b, out) + bf16 conv taps; s = fp32 state read + write, fp32 conv
-    history (3 reads + 1 write per channel), bf16 x in and out."""
+    W = bf16 projections (qkv, z, a, b, out) + bf16 conv taps (fp8: qkv, z and out as 1-byte codes plus an
+    fp32 scale per row, a and b bf16); s = fp32 state read + write, fp32 conv history (3 reads + 1 write per
+    channel), bf16 x in and out."""
     H, nk, nv, dk, dv = d["hidden"], d["num_k_heads"], d["num_v_heads"], d["head_k_dim"], d["head_v_dim"]
     C, Vd = 2 * nk * dk + nv * dv, nv * dv
-    W = 2 * (C * H + Vd * H + 2 * nv * H + H * Vd) + 2 * C * 4
+    if fp8:
+        W = (C * H + Vd * H + H * Vd) + 4 * (C + Vd + H) + 2 * 2 * nv * H + 2 * C * 4
+    else:
+        W = 2 * (C * H + Vd * H + 2 * nv * H + H * Vd) + 2 * C * 4
     s = nv * dk * dv * 4 * 2 + C * 4 * 4 + 2 * H * 2
     return W, s
+
+
+def eager_decode(layers, xs, steps, warmup):
+    """Wall ms per eager decode step over `layers` in rotation, and the per-stage HIP-event averages."""
+    import torch
+
+    L = len(layers)
+    for i in range(warmup):
+        layers[i % L](xs[i % len(xs)])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        layers[i % L](xs[i % len(xs)])
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    for lay in layers:
+        lay.profile(steps)
+    for i in range(steps):
+        layers[i % L](xs[i % len(xs)])
+    torch.cuda.synchronize()
+    stage = {"in_proj": 0.0, "mixer": 0.0, "out_proj": 0.0, "total": 0.0}
+    calls = 0
+    for lay in layers:
+        ms, n = lay.profile_read()
+        calls += n
+        for k in stage:
+            stage[k] += ms[k]
+        lay.profile(0)
+    return wall, {k: v / max(calls, 1) for k, v in stage.items()}
 
 
 def mixer_bytes_per_seq(d):
@@ -229,6 +262,7 @@ def main():
     ap.add_argument("--graph", type=int, default=0,
                     help="1: replay the decode step from HIP graphs; 0: launch eagerly (faster here: 104 vs 112 us)")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-fp8", action="store_true", help="skip the FP8-weight decode measurement")
     ap.add_argument("--stack", action="store_true",
                     help="also run the 24-layer continuous-batching stack (8 x 2048 prefill + 56 decode per step)")
     ap.add_argument("--no-traffic", action="store_true",
@@ -256,15 +290,18 @@ def main():
     print(f"[bench] building {L} 9B-shape layers, batch {B}", file=sys.stderr, flush=True)
 
     w0, gen = syn.make_weights(d, seed=2)
+
+    def copy_weights(i):
+        if i == 0:
+            return w0
+        # further copies: same distribution, drawn on the GPU (values do not affect timing)
+        gg = torch.Generator(device=dev).manual_seed(100 + i)
+        return {k: (torch.randn(v.shape, generator=gg, device=dev) * v.float().std()).to(v.dtype)
+                if k.startswith("w_") or k == "conv_w" else v for k, v in w0.items()}
+
     layers = []
     for i in range(L):
-        if i == 0:
-            w = w0
-        else:  # further copies: same distribution, drawn on the GPU (values do not affect timing)
-            gg = torch.Generator(device=dev).manual_seed(100 + i)
-            w = {k: (torch.randn(v.shape, generator=gg, device=dev) * v.float().std()).to(v.dtype)
-                 if k.startswith("w_") or k == "conv_w" else v for k, v in w0.items()}
-        lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B, max_tokens=max(B, 64))
+        lay = Qwen35GatedDeltaNetHIP(copy_weights(i), dims=d, batch=B, max_tokens=max(B, 64))
         s0 = torch.randn(B, d["num_v_heads"], 128, 128, device=dev) * 0.01
         lay.set_state(rec=s0)
         layers.append(lay)
@@ -346,6 +383,32 @@ def main():
         lay.close()
     del layers[1:]
 
+    # the same decode step on E4M3 weights (q|k|v|z and out_proj one byte per weight, per-row scales)
+    fp8 = None
+    if not args.no_fp8:
+        print(f"[bench] FP8-weight decode, {L} copies", file=sys.stderr, flush=True)
+        lays8 = []
+        for i in range(L):
+            lay = Qwen35GatedDeltaNetHIP(copy_weights(i), dims=d, batch=B, max_tokens=max(B, 64), weight_dtype="fp8")
+            lay.set_state(rec=torch.randn(B, d["num_v_heads"], 128, 128, device=dev) * 0.01)
+            lays8.append(lay)
+        wall8, st8 = eager_decode(lays8, xs, args.steps, args.warmup)
+        W8, s8 = decode_bytes(d, B, fp8=True)
+        b8 = W8 + B * s8
+        fp8 = {"ms_per_step": wall8, "tok_per_s": B / (wall8 / 1e3), "bytes_per_step": b8,
+               "frac": b8 / (wall8 / 1e3) / HBM_PEAK, "event_step_us": st8["total"] * 1e3,
+               "stage_us": {k: v * 1e3 for k, v in st8.items()},
+               "weights": "E4M3, one fp32 scale per row (a|b rows bf16)"}
+        # in_proj weight stream (q|k|v|z codes + scales + bf16 a|b rows) over the in_proj stage time
+        H, nv = d["hidden"], d["num_v_heads"]
+        n1 = 2 * d["num_k_heads"] * 128 + 2 * nv * 128
+        fp8["in_proj_GBps"] = (n1 * H + 4 * n1 + 2 * 2 * nv * H) / (st8["in_proj"] / 1e3) / 1e9
+        print(f"[bench] fp8 decode B={B}: {wall8 * 1e3:.1f} us/step wall, stages (us) "
+              f"{ {k: round(v * 1e3, 1) for k, v in st8.items()} }", file=sys.stderr, flush=True)
+        for lay in lays8:
+            lay.close()
+        del lays8
+
     prefill = None
     if not args.no_prefill:
         T = args.prefill_len
@@ -391,7 +454,8 @@ def main():
                                f"rotating over {L} layer copies" + (", HIP-graph replay" if args.graph else ""),
                    "hidden": d["hidden"], "num_k_heads": d["num_k_heads"], "num_v_heads": d["num_v_heads"],
                    "head_dim": 128, "batch": B, "state_dtype": "fp32", "weights": "bf16 N(0,0.02) seed 2"},
-        "roofline": roofline, "layer_roofline": layer_roof, "prefill": prefill, "stack": stack, "cpu_baseline": cpu,
+        "roofline": roofline, "layer_roofline": layer_roof, "prefill": prefill, "stack": stack, "fp8_decode": fp8,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(line))
 

@@ -64,6 +64,15 @@ typedef struct gdn_weights {
     const void* out_proj;      /* bf16 [H, nv*dv] */
 } gdn_weights;
 
+/* Weight storage of a layer: the reference's weight_dtype argument (9B/gdn_layer.py:55, 115-120: w_in and
+ * w_out in ttnn.bfloat16 or ttnn.bfloat8_b, w_ab always bfloat16; 0.8B/gdn_l1.py:79-80). */
+typedef enum gdn_weight_format {
+    GDN_WEIGHTS_BF16 = 0,      /* the bf16 weights as given */
+    GDN_WEIGHTS_FP8_E4M3 = 1,  /* in_proj q|k|v|z rows and out_proj as OCP E4M3 codes with one fp32 scale per
+                                * output row (absmax / 448, see gdn_quantize_fp8); the a|b rows stay bf16.
+                                * Activations and accumulation are unchanged (bf16 x bf16 MFMA, fp32). */
+} gdn_weight_format;
+
 /* ---- layer handle: mirrors Qwen35GatedDeltaNetTT (9B/gdn_layer.py:54-292) ------------------------ */
 
 /* 9B/gdn_layer.py:55-78 (__init__), 90-127 (_prepare_weights), 137-151 (reset_state).
@@ -72,6 +81,14 @@ typedef struct gdn_weights {
  * `max_tokens` rows (longer launches are split, 9B/gdn_layer.py:282-292). */
 int gdn_layer_create(const gdn_dims* dims, const gdn_weights* weights, int max_slots, int max_tokens,
                      gdn_layer** out);
+
+/* 9B/gdn_layer.py:55 with weight_dtype: gdn_layer_create with the weights stored in `weight_format`
+ * (a gdn_weight_format), quantized on the device from the bf16 weights given. */
+int gdn_layer_create_ex(const gdn_dims* dims, const gdn_weights* weights, int max_slots, int max_tokens,
+                        int weight_format, gdn_layer** out);
+
+/* The gdn_weight_format of a layer. */
+int gdn_layer_weight_format(const gdn_layer* layer);
 
 int gdn_layer_destroy(gdn_layer* layer);
 
@@ -158,6 +175,10 @@ int gdn_out_proj(gdn_layer* layer, const void* y, int M, void* out, void* stream
  * NULL; no norm follows the last layer.  The layers share one workspace for `max_tokens` rows. */
 int gdn_stack_create(const gdn_dims* dims, const gdn_weights* weights, int n_layers, int inter_norm,
                      const float* const* norm_weights, int max_slots, int max_tokens, gdn_stack** out);
+/* The same with every layer's weights in `weight_format` (gdn_l1.py:79-80, the stack's weight dtype). */
+int gdn_stack_create_ex(const gdn_dims* dims, const gdn_weights* weights, int n_layers, int inter_norm,
+                        const float* const* norm_weights, int max_slots, int max_tokens, int weight_format,
+                        gdn_stack** out);
 int gdn_stack_destroy(gdn_stack* stack);
 
 /* The handle of layer i, for the state calls (gdn_state_*) and per-op entries.  Owned by the stack. */
@@ -186,6 +207,13 @@ int gdn_delta_rule_fla(const float* q, const float* k, const float* v, const flo
 /* Projection y[M, N] = x[M, K] . w[N, K]^T, bf16 inputs, fp32 accumulation (the ttnn.linear call sites
  * 9B/gdn_layer.py:255, 259, 272).  out_fp32 != 0: y is fp32, else bf16.  K % 128 == 0. */
 int gdn_linear_bf16(const void* x, const void* w, int M, int N, int K, void* y, int out_fp32, void* stream);
+
+/* The E4M3 weight quantizer of GDN_WEIGHTS_FP8_E4M3 (the reference's host-side conversion to bfloat8_b,
+ * ttnn.from_torch(..., dtype=weight_dtype) at 9B/gdn_layer.py:115-120, re-specified for OCP E4M3):
+ * w bf16 [N, K] (device) -> q uint8 [N, K] E4M3 codes, scale fp32 [N], with scale[n] = max_k |w[n, k]| / 448
+ * (1 for an all-zero row) and q[n, k] = round-to-nearest-even(w[n, k] / scale[n]), saturating at +-448.
+ * Row n of the dequantized matrix is decode(q[n, :]) * scale[n]. */
+int gdn_quantize_fp8(const void* w, int N, int K, void* q, float* scale, void* stream);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* gdn_last_error(void);

@@ -19,6 +19,20 @@ GDN_ERR_SLOT = -4
 GDN_ERR_HIP = -5
 GDN_ERR_OUT_OF_MEMORY = -6
 
+# gdn_weight_format; Python names follow the reference's weight_dtype argument
+GDN_WEIGHTS_BF16 = 0
+GDN_WEIGHTS_FP8_E4M3 = 1
+WEIGHT_FORMATS = {"bf16": GDN_WEIGHTS_BF16, "bfloat16": GDN_WEIGHTS_BF16, "fp8": GDN_WEIGHTS_FP8_E4M3,
+                  "fp8_e4m3": GDN_WEIGHTS_FP8_E4M3}
+
+
+def weight_format(weight_dtype):
+    """gdn_weight_format of a weight_dtype name ("bf16" or "fp8")."""
+    try:
+        return WEIGHT_FORMATS[str(weight_dtype).lower()]
+    except KeyError:
+        raise ValueError(f"weight_dtype {weight_dtype!r}: expected one of {sorted(WEIGHT_FORMATS)}") from None
+
 
 class GdnError(RuntimeError):
     """A gdn_* call returned a negative status."""
@@ -51,11 +65,16 @@ _F = ctypes.c_float
 # name -> (restype, argtypes)
 SIGNATURES = {
     "gdn_layer_create": (_I, [ctypes.POINTER(GdnDims), ctypes.POINTER(GdnWeights), _I, _I, ctypes.POINTER(_V)]),
+    "gdn_layer_create_ex": (_I, [ctypes.POINTER(GdnDims), ctypes.POINTER(GdnWeights), _I, _I, _I,
+                                 ctypes.POINTER(_V)]),
+    "gdn_layer_weight_format": (_I, [_V]),
     "gdn_layer_destroy": (_I, [_V]),
     "gdn_layer_forward": (_I, [_V, _V, _I, _I, _V, _V, _V]),
     "gdn_layer_forward_varlen": (_I, [_V, _V, _I, ctypes.POINTER(_I), _V, _V, _V]),
     "gdn_stack_create": (_I, [ctypes.POINTER(GdnDims), ctypes.POINTER(GdnWeights), _I, _I,
                               ctypes.POINTER(ctypes.c_void_p), _I, _I, ctypes.POINTER(_V)]),
+    "gdn_stack_create_ex": (_I, [ctypes.POINTER(GdnDims), ctypes.POINTER(GdnWeights), _I, _I,
+                                 ctypes.POINTER(ctypes.c_void_p), _I, _I, _I, ctypes.POINTER(_V)]),
     "gdn_stack_destroy": (_I, [_V]),
     "gdn_stack_layer": (_I, [_V, _I, ctypes.POINTER(_V)]),
     "gdn_stack_forward": (_I, [_V, _V, _I, _I, _V, _I, _I, _V, _V]),
@@ -74,6 +93,7 @@ SIGNATURES = {
     "gdn_out_proj": (_I, [_V, _V, _I, _V, _V]),
     "gdn_delta_rule_fla": (_I, [_V, _V, _V, _V, _V, _I, _I, _I, _I, _I, _I, _V, _I, _F, _V, _V]),
     "gdn_linear_bf16": (_I, [_V, _V, _I, _I, _I, _V, _I, _V]),
+    "gdn_quantize_fp8": (_I, [_V, _I, _I, _V, _V, _V]),
     "gdn_last_error": (ctypes.c_char_p, []),
     "gdn_version": (_I, []),
 }

@@ -18,6 +18,7 @@
 #include "gdn_common.h"
 
 using gdn::u16;
+using gdn::u8;
 
 namespace {
 
@@ -55,8 +56,14 @@ struct gdn_layer {
     int max_slots = 0, max_tokens = 0;
     std::vector<void*> allocs;
 
-    u16* w_in = nullptr;      // [NP, H]  rows q | k | v | z | a | b, W_FRAG layout
-    u16* w_out = nullptr;     // [H, Vd] W_FRAG layout
+    int wfmt = GDN_WEIGHTS_BF16;
+    u16* w_in = nullptr;      // bf16: [NP, H]  rows q | k | v | z | a | b, W_FRAG layout
+    u16* w_out = nullptr;     // bf16: [H, Vd] W_FRAG layout
+    u16* w_ab = nullptr;      // [2 nv, H] a | b rows, W_FRAG (bf16: inside w_in)
+    u8* w_in8 = nullptr;      // fp8: [CD + Vd, H] rows q | k | v | z, W_F8 layout
+    float* s_in = nullptr;    // fp8: per-row scales of w_in8
+    u8* w_out8 = nullptr;     // fp8: [H, Vd] W_F8 layout
+    float* s_out = nullptr;   // fp8: per-row scales of w_out8
     float4* conv_w = nullptr; // [CD] taps
     float* neg_A = nullptr;   // [nv]
     float* dt_bias = nullptr; // [nv]
@@ -142,6 +149,25 @@ hipError_t run_delta(gdn_layer* L, const gdn::DeltaArgs& r, hipStream_t st) {
     return gdn::launch_delta_seq(r, d.head_k_dim, d.head_v_dim, st);
 }
 
+bool fp8(const gdn_layer* L) { return L->wfmt == GDN_WEIGHTS_FP8_E4M3; }
+
+// in_proj of M rows (x row-major, or W_FRAG for M <= 64) into P [M, NP] (9B/gdn_layer.py:255-259).  FP8
+// layers run the q | k | v | z rows on E4M3 weights and the a | b rows on bf16 ones.
+hipError_t in_proj_rows(const gdn_layer* L, const void* x, int xl, int M, float* P, hipStream_t st) {
+    const int H = L->d.hidden, N1 = L->CD + L->Vd, nab = 2 * L->d.num_v_heads;
+    if (!fp8(L)) return gdn::launch_linear(x, xl, L->w_in, gdn::W_FRAG, nullptr, M, L->NP, H, P, L->NP, gdn::OUT_F32, st);
+    hipError_t e = gdn::launch_linear(x, xl, L->w_in8, gdn::W_F8, L->s_in, M, N1, H, P, L->NP, gdn::OUT_F32, st);
+    if (e != hipSuccess) return e;
+    return gdn::launch_linear(x, xl, L->w_ab, gdn::W_FRAG, nullptr, M, nab, H, P + N1, L->NP, gdn::OUT_F32, st);
+}
+
+// out_proj of M rows of y (row-major, or W_FRAG for M <= 64) into out bf16 [M, H] (9B/gdn_layer.py:272-276).
+hipError_t out_proj_rows(const gdn_layer* L, const void* y, int yl, int M, void* out, hipStream_t st) {
+    const int H = L->d.hidden;
+    if (fp8(L)) return gdn::launch_linear(y, yl, L->w_out8, gdn::W_F8, L->s_out, M, H, L->Vd, out, H, gdn::OUT_BF16, st);
+    return gdn::launch_linear(y, yl, L->w_out, gdn::W_FRAG, nullptr, M, H, L->Vd, out, H, gdn::OUT_BF16, st);
+}
+
 // A group of sequences of one launch with the same length: rows [row0, row0 + B T) of the launch,
 // sequence b of the group on state slot slots[b].
 struct Group {
@@ -171,11 +197,11 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, u16* o
         ab_split = split_ab && mixer_only;
     }
     if (ab_split)
-        HIP_OK(gdn::launch_in_proj_decode(L->x_frag, L->w_in, M, L->CD + Vd, 2 * nv, d.hidden, L->P, L->NP, L->ab,
-                                          kAbSplits, st));
+        HIP_OK(gdn::launch_in_proj_decode(L->x_frag, fp8(L) ? (const void*)L->w_in8 : L->w_in,
+                                          fp8(L) ? gdn::W_F8 : gdn::W_FRAG, L->s_in, L->w_ab, M, L->CD + Vd, 2 * nv,
+                                          d.hidden, L->P, L->NP, L->ab, kAbSplits, st));
     else
-        HIP_OK(gdn::launch_linear(frag ? L->x_frag : x, frag ? gdn::W_FRAG : gdn::W_ROW, L->w_in, gdn::W_FRAG, M,
-                                  L->NP, d.hidden, L->P, gdn::OUT_F32, st));
+        HIP_OK(in_proj_rows(L, frag ? L->x_frag : x, frag ? gdn::W_FRAG : gdn::W_ROW, M, L->P, st));
     if (ev[1]) HIP_OK(hipEventRecord(ev[1], st));
     for (int gi = 0; gi < ng; ++gi) {
         const Group& g = grp[gi];
@@ -214,8 +240,7 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, u16* o
         }
     }
     if (ev[2]) HIP_OK(hipEventRecord(ev[2], st));
-    HIP_OK(gdn::launch_linear(L->y, y_frag ? gdn::W_FRAG : gdn::W_ROW, L->w_out, gdn::W_FRAG, M, d.hidden, Vd, out,
-                              gdn::OUT_BF16, st));
+    HIP_OK(out_proj_rows(L, L->y, y_frag ? gdn::W_FRAG : gdn::W_ROW, M, out, st));
     if (ev[3]) {
         HIP_OK(hipEventRecord(ev[3], st));
         ++L->prof_calls;
@@ -285,12 +310,14 @@ namespace {
 
 // Layer creation; `share` (a layer of the same geometry) lends its launch workspace, as layers of a stack
 // run one at a time.
-int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int max_tokens, const gdn_layer* share,
-                 gdn_layer** out) {
+int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int max_tokens, int wfmt,
+                 const gdn_layer* share, gdn_layer** out) {
     if (!out) return fail(GDN_ERR_INVALID_ARG, "out is NULL");
     *out = nullptr;
     int rc = check_dims(dims);
     if (rc) return rc;
+    if (wfmt != GDN_WEIGHTS_BF16 && wfmt != GDN_WEIGHTS_FP8_E4M3)
+        return fail(GDN_ERR_INVALID_ARG, "unknown weight format %d", wfmt);
     if (!w || !w->in_proj_qkv || !w->in_proj_z || !w->in_proj_a || !w->in_proj_b || !w->conv1d || !w->A_log ||
         !w->dt_bias || !w->norm_weight || !w->out_proj)
         return fail(GDN_ERR_INVALID_ARG, "a weight pointer is NULL");
@@ -303,14 +330,25 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
     L->Kd = nk * dk, L->Vd = nv * dv, L->CD = 2 * L->Kd + L->Vd, L->NP = L->CD + L->Vd + 2 * nv;
     L->CH = 2 * dk + dv;
     L->max_slots = max_slots, L->max_tokens = max_tokens;
+    L->wfmt = wfmt;
     const size_t MT = (size_t)max_tokens;
+    const int N1 = L->CD + L->Vd;  // q | k | v | z rows (a multiple of 16)
 
     hipError_t e = hipSuccess;
     auto take = [&](hipError_t r) {
         if (e == hipSuccess) e = r;
     };
-    take(L->alloc(&L->w_in, gdn::frag_elems(L->NP, H)));
-    take(L->alloc(&L->w_out, gdn::frag_elems(H, L->Vd)));
+    if (wfmt == GDN_WEIGHTS_FP8_E4M3) {
+        take(L->alloc(&L->w_in8, gdn::frag_elems(N1, H)));
+        take(L->alloc(&L->s_in, (size_t)N1));
+        take(L->alloc(&L->w_ab, gdn::frag_elems(2 * nv, H)));
+        take(L->alloc(&L->w_out8, gdn::frag_elems(H, L->Vd)));
+        take(L->alloc(&L->s_out, (size_t)H));
+    } else {
+        take(L->alloc(&L->w_in, gdn::frag_elems(L->NP, H)));
+        take(L->alloc(&L->w_out, gdn::frag_elems(H, L->Vd)));
+        if (e == hipSuccess) L->w_ab = L->w_in + gdn::frag_elems(N1, H);
+    }
     take(L->alloc(&L->conv_w, (size_t)L->CD));
     take(L->alloc(&L->neg_A, (size_t)nv));
     take(L->alloc(&L->dt_bias, (size_t)nv));
@@ -354,7 +392,9 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
     }
 
     // fused in_proj rows: q | k | v (in_proj_qkv), z, a, b -- one weight stream per token.  The HF
-    // row-major weights are staged in a temporary device buffer and re-laid out into fragment blocks.
+    // row-major weights are staged in a temporary device buffer and re-laid out into fragment blocks
+    // (FP8: the q | k | v | z rows and out_proj quantized to E4M3 with per-row scales, as the reference
+    // converts w_in and w_out to its weight_dtype and keeps w_ab bf16, 9B/gdn_layer.py:115-120).
     const size_t row = (size_t)H * sizeof(u16);
     u16* stage = nullptr;
     e = hipMalloc(&stage, std::max((size_t)L->NP * H, (size_t)H * L->Vd) * sizeof(u16));
@@ -363,9 +403,23 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
     if (e == hipSuccess) e = hipMemcpy(stage + (size_t)(L->CD + L->Vd) * H, w->in_proj_a, nv * row, hipMemcpyDefault);
     if (e == hipSuccess)
         e = hipMemcpy(stage + (size_t)(L->CD + L->Vd + nv) * H, w->in_proj_b, nv * row, hipMemcpyDefault);
-    if (e == hipSuccess) e = gdn::launch_frag_tile(stage, L->NP, H, L->w_in, nullptr);
+    if (e == hipSuccess) {
+        if (wfmt == GDN_WEIGHTS_FP8_E4M3) {
+            e = gdn::launch_quantize_e4m3(stage, N1, H, L->w_in8, L->s_in, 1, nullptr);
+            if (e == hipSuccess) e = gdn::launch_frag_tile(stage + (size_t)N1 * H, 2 * nv, H, L->w_ab, nullptr);
+        } else {
+            e = gdn::launch_frag_tile(stage, L->NP, H, L->w_in, nullptr);
+        }
+    }
+    // the stage is reused: finish reading it first
+    if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e == hipSuccess) e = hipMemcpy(stage, w->out_proj, (size_t)H * L->Vd * sizeof(u16), hipMemcpyDefault);
-    if (e == hipSuccess) e = gdn::launch_frag_tile(stage, H, L->Vd, L->w_out, nullptr);
+    if (e == hipSuccess) {
+        if (wfmt == GDN_WEIGHTS_FP8_E4M3)
+            e = gdn::launch_quantize_e4m3(stage, H, L->Vd, L->w_out8, L->s_out, 1, nullptr);
+        else
+            e = gdn::launch_frag_tile(stage, H, L->Vd, L->w_out, nullptr);
+    }
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (stage) (void)hipFree(stage);
     if (e == hipSuccess) e = hipMemcpy(L->conv_w, w->conv1d, (size_t)L->CD * 4 * sizeof(float), hipMemcpyDefault);
@@ -398,8 +452,15 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
 extern "C" {
 
 int gdn_layer_create(const gdn_dims* dims, const gdn_weights* w, int max_slots, int max_tokens, gdn_layer** out) {
-    return create_layer(dims, w, max_slots, max_tokens, nullptr, out);
+    return create_layer(dims, w, max_slots, max_tokens, GDN_WEIGHTS_BF16, nullptr, out);
 }
+
+int gdn_layer_create_ex(const gdn_dims* dims, const gdn_weights* w, int max_slots, int max_tokens,
+                        int weight_format, gdn_layer** out) {
+    return create_layer(dims, w, max_slots, max_tokens, weight_format, nullptr, out);
+}
+
+int gdn_layer_weight_format(const gdn_layer* L) { return L ? L->wfmt : fail(GDN_ERR_INVALID_ARG, "layer is NULL"); }
 
 int gdn_layer_destroy(gdn_layer* L) {
     if (!L) return GDN_OK;
@@ -494,8 +555,7 @@ int gdn_layer_proj_width(const gdn_layer* L) { return L ? L->NP : fail(GDN_ERR_I
 int gdn_in_proj(gdn_layer* L, const void* x, int M, float* P, void* stream) {
     if (!L || !x || !P) return fail(GDN_ERR_INVALID_ARG, "gdn_in_proj: NULL argument");
     if (M <= 0) return fail(GDN_ERR_SHAPE, "M=%d", M);
-    HIP_OK(gdn::launch_linear(x, gdn::W_ROW, L->w_in, gdn::W_FRAG, M, L->NP, L->d.hidden, P, gdn::OUT_F32,
-                              as_stream(stream)));
+    HIP_OK(in_proj_rows(L, x, gdn::W_ROW, M, P, as_stream(stream)));
     return GDN_OK;
 }
 
@@ -544,8 +604,7 @@ int gdn_gated_rmsnorm(gdn_layer* L, const float* o, const float* z, int z_stride
 int gdn_out_proj(gdn_layer* L, const void* y, int M, void* out, void* stream) {
     if (!L || !y || !out) return fail(GDN_ERR_INVALID_ARG, "gdn_out_proj: NULL argument");
     if (M <= 0) return fail(GDN_ERR_SHAPE, "M=%d", M);
-    HIP_OK(gdn::launch_linear(y, gdn::W_ROW, L->w_out, gdn::W_FRAG, M, L->d.hidden, L->Vd, out, gdn::OUT_BF16,
-                              as_stream(stream)));
+    HIP_OK(out_proj_rows(L, y, gdn::W_ROW, M, out, as_stream(stream)));
     return GDN_OK;
 }
 
@@ -570,8 +629,15 @@ int gdn_linear_bf16(const void* x, const void* w, int M, int N, int K, void* y, 
     if (!x || !w || !y) return fail(GDN_ERR_INVALID_ARG, "gdn_linear_bf16: NULL argument");
     if (M <= 0 || N <= 0 || K <= 0) return fail(GDN_ERR_SHAPE, "M=%d N=%d K=%d", M, N, K);
     if (K % 128) return fail(GDN_ERR_UNSUPPORTED, "K=%d is not a multiple of 128", K);
-    HIP_OK(gdn::launch_linear(x, gdn::W_ROW, w, gdn::W_ROW, M, N, K, y, out_fp32 ? gdn::OUT_F32 : gdn::OUT_BF16,
-                              as_stream(stream)));
+    HIP_OK(gdn::launch_linear(x, gdn::W_ROW, w, gdn::W_ROW, nullptr, M, N, K, y, N,
+                              out_fp32 ? gdn::OUT_F32 : gdn::OUT_BF16, as_stream(stream)));
+    return GDN_OK;
+}
+
+int gdn_quantize_fp8(const void* w, int N, int K, void* q, float* scale, void* stream) {
+    if (!w || !q || !scale) return fail(GDN_ERR_INVALID_ARG, "gdn_quantize_fp8: NULL argument");
+    if (N <= 0 || K <= 0) return fail(GDN_ERR_SHAPE, "N=%d K=%d", N, K);
+    HIP_OK(gdn::launch_quantize_e4m3(w, N, K, (u8*)q, scale, 0, as_stream(stream)));
     return GDN_OK;
 }
 
@@ -621,13 +687,21 @@ extern "C" {
 
 int gdn_stack_create(const gdn_dims* dims, const gdn_weights* weights, int n_layers, int inter_norm,
                      const float* const* norm_weights, int max_slots, int max_tokens, gdn_stack** out) {
+    return gdn_stack_create_ex(dims, weights, n_layers, inter_norm, norm_weights, max_slots, max_tokens,
+                               GDN_WEIGHTS_BF16, out);
+}
+
+int gdn_stack_create_ex(const gdn_dims* dims, const gdn_weights* weights, int n_layers, int inter_norm,
+                        const float* const* norm_weights, int max_slots, int max_tokens, int weight_format,
+                        gdn_stack** out) {
     if (!out) return fail(GDN_ERR_INVALID_ARG, "out is NULL");
     *out = nullptr;
     if (!weights || n_layers <= 0) return fail(GDN_ERR_INVALID_ARG, "gdn_stack_create: %d layers", n_layers);
     gdn_stack* S = new gdn_stack();
     for (int i = 0; i < n_layers; ++i) {
         gdn_layer* L = nullptr;
-        int rc = create_layer(dims, &weights[i], max_slots, max_tokens, i ? S->layers[0] : nullptr, &L);
+        int rc = create_layer(dims, &weights[i], max_slots, max_tokens, weight_format, i ? S->layers[0] : nullptr,
+                              &L);
         if (rc) {
             delete S;
             return rc;

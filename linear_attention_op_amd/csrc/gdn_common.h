@@ -14,6 +14,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint16_t u16;
 typedef uint16_t u16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint8_t u8;
 
 constexpr int WAVE = 64;
 
@@ -75,6 +77,31 @@ __device__ __forceinline__ f32x4 mfma3(const Split8& a, const Split8& b, f32x4 c
     return mfma16(a.h, b.h, c);
 }
 
+// ---- FP8 (OCP E4M3: 1 sign, 4 exponent bits biased by 7, 3 mantissa bits; largest finite 448) --------
+// Encoding of one value, round to nearest even, saturating to +-448 (the weight quantizer).
+__host__ __device__ __forceinline__ uint32_t e4m3_code(float v) {
+    union { float f; uint32_t u; } b{v};
+    const uint32_t sign = (b.u >> 24) & 0x80u;
+    const float a = fminf(fabsf(v), 448.0f);
+    if (a < 0.015625f) return sign | (uint32_t)rintf(a * 512.0f);  // subnormal steps of 2^-9 (8 = 2^-6)
+    b.f = a;
+    const uint32_t u = b.u + 0x7ffffu + ((b.u >> 20) & 1u);         // keep 3 mantissa bits, ties to even
+    return sign | (((u >> 23) - 120u) << 3) | ((u >> 20) & 7u);
+}
+
+// 16 E4M3 values (bytes in k order) -> 2 x 8 bf16, exact (every E4M3 value is a bf16 value).
+__device__ __forceinline__ void e4m3x16_to_bf16(const u32x4 q, bf16x8& lo, bf16x8& hi) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    bf16x2 p[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        p[2 * i] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[i], 1.0f, false);     // bytes 0, 1
+        p[2 * i + 1] = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(q[i], 1.0f, true);  // bytes 2, 3
+    }
+    lo = bf16x8{p[0][0], p[0][1], p[1][0], p[1][1], p[2][0], p[2][1], p[3][0], p[3][1]};
+    hi = bf16x8{p[4][0], p[4][1], p[5][0], p[5][1], p[6][0], p[6][1], p[7][0], p[7][1]};
+}
+
 // Workgroup barrier for LDS traffic only: unlike __syncthreads() it does not wait for outstanding
 // global loads, so loads issued for the next step stay in flight across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
@@ -92,20 +119,35 @@ __device__ __forceinline__ float softplusf_(float x) { return x > 20.0f ? x : lo
 namespace gdn {
 
 enum OutKind { OUT_F32 = 0, OUT_BF16 = 1 };
-// Weight layouts: W_ROW = row-major [N, K]; W_FRAG = MFMA-fragment blocks (see gdn_linear.hip).
-enum WLayout { W_ROW = 0, W_FRAG = 1 };
+// Weight layouts: W_ROW = row-major bf16 [N, K]; W_FRAG = bf16 MFMA-fragment blocks; W_F8 = E4M3 fragment
+// blocks with one fp32 scale per row (see gdn_linear.hip).
+enum WLayout { W_ROW = 0, W_FRAG = 1, W_F8 = 2 };
 
-// y[M, N] = x[M, K] . w[N, K]^T ; bf16 inputs, fp32 accumulation; K % 128 == 0.  w in layout `wlayout`;
-// x in `xlayout` (W_FRAG activations only for M <= 64).
-hipError_t launch_linear(const void* x, int xlayout, const void* w, int wlayout, int M, int N, int K, void* y,
-                         int out_kind, hipStream_t stream);
-// Decode in_proj on W_FRAG weights and activations (M <= 64): rows [0, N1) of w into P (fp32, row stride
-// ldp) with the workgroups balanced over the CUs; the next N2 rows as ab_splits partial sums over k
-// ranges into Pab [ab_splits][M][N2] (the consumer adds the slices).  N1 % 16 == 0.
-hipError_t launch_in_proj_decode(const void* x_frag, const void* w_frag, int M, int N1, int N2, int K, float* P,
-                                 int ldp, float* Pab, int ab_splits, hipStream_t stream);
-// Elements of an [N, K] matrix in W_FRAG layout (rows padded to a multiple of 16).
+// y[M, N] (row stride ldy) = x[M, K] . w[N, K]^T ; bf16 activations, fp32 accumulation; K % 128 == 0.
+// w in layout `wlayout` (W_F8: w = E4M3 codes, row n scaled by w_scale[n]); x in `xlayout` (W_FRAG
+// activations only for M <= 64).
+hipError_t launch_linear(const void* x, int xlayout, const void* w, int wlayout, const float* w_scale, int M, int N,
+                         int K, void* y, int ldy, int out_kind, hipStream_t stream);
+// Decode in_proj on fragment-layout activations (M <= 64): rows [0, N1) of w (W_FRAG, or W_F8 with
+// w_scale) into P (fp32, row stride ldp) with the workgroups balanced over the CUs; the N2 rows of w2
+// (W_FRAG) as ab_splits partial sums over k ranges into Pab [ab_splits][M][N2] (the consumer adds the
+// slices).  N1 % 16 == 0.
+hipError_t launch_in_proj_decode(const void* x_frag, const void* w, int wlayout, const float* w_scale,
+                                 const void* w2, int M, int N1, int N2, int K, float* P, int ldp, float* Pab,
+                                 int ab_splits, hipStream_t stream);
+// Elements of an [N, K] matrix in W_FRAG layout (rows padded to a multiple of 16); also the bytes of the
+// same matrix in W_F8 layout.
 size_t frag_elems(int N, int K);
+// Quantize a row-major bf16 [N, K] matrix to E4M3 with per-row scale absmax / 448 (1 for a zero row):
+// codes in W_F8 layout (to_frag != 0; rows padded to 16 with zeros, K % 64 == 0) or row-major [N, K].
+hipError_t launch_quantize_e4m3(const void* w, int N, int K, u8* q, float* scale, int to_frag, hipStream_t stream);
+// Byte offset of (row n, column k) of an [N, K] matrix in W_F8 layout: blocks of 16 rows x 64 columns
+// (1 KB), lane l = 16 g + r of block holding the 16 bytes W[16 nt + r][64 kp + 32 h + 8 g + j] at
+// 16 l + 8 h + j -- two consecutive MFMA A operands per 16-byte load.
+__host__ __device__ __forceinline__ size_t f8_offset(int n, int k, int K) {
+    return ((size_t)(n >> 4) * (K >> 6) + (k >> 6)) * 1024 + ((((k >> 3) & 3) << 4) + (n & 15)) * 16 +
+           ((k >> 5) & 1) * 8 + (k & 7);
+}
 // Convert a row-major device matrix [N, K] into W_FRAG layout (frag_elems(N, K) elements).
 hipError_t launch_frag_tile(const void* w, int N, int K, void* wf, hipStream_t stream);
 // Element offset of (row n, column k) of an [N, K] matrix in W_FRAG layout.

@@ -6,6 +6,11 @@
 // [ceil(N/16)][K/32] blocks of 512 bf16, block (nt, kq) holding for lane l = 16 g + r the 8 values
 // W[16 nt + r][32 kq + 8 g + j] at offset 8 l + j -- exactly the A operand of v_mfma_f32_16x16x32_bf16,
 // so one fragment load is 1 KB of contiguous memory and a wave streams its rows sequentially.
+// W_F8 is the same idea for E4M3 weights (the counterpart of the reference's bfloat8_b weight_dtype,
+// 9B/gdn_layer.py:55,115-120): blocks of 16 rows x 64 columns, lane l = 16 g + r holding the 16 codes
+// W[16 nt + r][64 kp + 32 h + 8 g + j] (h = 0, 1), i.e. the A operands of two consecutive k-steps, plus one
+// fp32 scale per row applied to the finished dot product.  Codes are widened to bf16 in registers
+// (v_cvt_scalef32_pk_bf16_fp8, exact), so the MFMA work is unchanged and the weight stream halves.
 //
 // Kernels (bf16 MFMA, fp32 accumulation):
 //  * gemv_kernel (M <= 64, decode): HBM-bound weight streaming.  A workgroup owns 16 NTS rows of w; its
@@ -49,12 +54,69 @@ __global__ void frag_tile_kernel(const u16* __restrict__ w, int N, int K, u16* _
 }
 
 // ------------------------------------------------------------------------------------------------
+// E4M3 weight quantizer: one workgroup per (padded) row.  scale = absmax / 448 (1 for a zero row);
+// codes = e4m3_code(w / scale), written in W_F8 layout or row-major.  Rows past N: zero codes, scale 1.
+// ------------------------------------------------------------------------------------------------
+template <bool FRAG>
+__global__ __launch_bounds__(256) void quantize_e4m3_kernel(const u16* __restrict__ w, int N, int K,
+                                                            u8* __restrict__ q, float* __restrict__ scale) {
+    __shared__ float part[4];
+    const int n = blockIdx.x;
+    const bool real = n < N;
+    float m = 0.f;
+    if (real)
+        for (int k = threadIdx.x; k < K; k += 256) m = fmaxf(m, fabsf(bf2f(w[(size_t)n * K + k])));
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, WAVE));
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(part[0], part[1]), fmaxf(part[2], part[3]));
+    const float sc = m > 0.f ? m / 448.0f : 1.0f;
+    if (threadIdx.x == 0 && real) scale[n] = sc;
+    for (int k = threadIdx.x; k < K; k += 256) {
+        const u8 c = real ? (u8)e4m3_code(bf2f(w[(size_t)n * K + k]) / sc) : (u8)0;
+        q[FRAG ? f8_offset(n, k, K) : (size_t)n * K + k] = c;
+    }
+}
+
+// ------------------------------------------------------------------------------------------------
 // GEMV: M <= 16 MT
 // ------------------------------------------------------------------------------------------------
 // Weight fragments are read once per call: non-temporal loads, so they do not evict the activations
 // every workgroup re-reads.
 __device__ __forceinline__ bf16x8 ldw(const u16* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const bf16x8*>(p));
+}
+__device__ __forceinline__ u32x4 ldw8(const u8* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+
+// Sum of the NW waves' partial tiles through LDS and one coalesced write of rows [n0, n0 + 16 NTS):
+// C element i of lane (r, g) in acc[t][mt] is w row n0 + 16 t + 4 g + i, x row 16 mt + r.  A non-NULL
+// `scale` multiplies row n of w's results by scale[n].
+template <int NTS, int MT, int NW, int OUT>
+__device__ __forceinline__ void gemv_finish(const f32x4 (&acc)[NTS][MT], float (*red)[MT * 16][NTS * 16 + 1],
+                                            int M, int N, void* __restrict__ y, int ldy, int n0,
+                                            const float* __restrict__ scale) {
+    constexpr int BN = NTS * 16, BM = MT * 16;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+#pragma unroll
+    for (int t = 0; t < NTS; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) red[wave][16 * mt + r][16 * t + 4 * g + i] = acc[t][mt][i];
+    __syncthreads();
+    for (int e = threadIdx.x; e < BM * BN; e += NW * 64) {
+        const int m = e / BN, nl = e % BN, n = n0 + nl;
+        if (m >= M || n >= N) continue;
+        float s = 0.f;
+#pragma unroll
+        for (int wv = 0; wv < NW; ++wv) s += red[wv][m][nl];
+        if (scale) s *= scale[n];
+        store_out<OUT>(y, (size_t)m * ldy + n, s);
+    }
 }
 
 // One workgroup of the GEMV: rows [n0, n0 + 16 NTS) of w (of N) against the M rows of x over the k-steps
@@ -135,28 +197,106 @@ __device__ __forceinline__ void gemv_block(const u16* __restrict__ x, const u16*
         }
     }
 
-    // C element i of lane (r, g) in acc[t][mt]: w row n0 + 16 t + 4 g + i, x row 16 mt + r
+    gemv_finish<NTS, MT, NW, OUT>(acc, red, M, N, y, ldy, n0, nullptr);
+}
+
+// The same on W_F8 weights: a k-step of the ring is a k-pair (64 columns), one 16-byte load per row
+// tile and two x fragments per row block; rows scaled by scale[n] at the end.  K % 64 == 0; the k range
+// is [kpb, kpb + kpn) in k-pairs.
+template <int NTS, int MT, int NW, int PD, int OUT, int XL>
+__device__ __forceinline__ void gemv_block_f8(const u16* __restrict__ x, const u8* __restrict__ w,
+                                              const float* __restrict__ scale, int M, int N, int K,
+                                              void* __restrict__ y, int ldy, int n0, int kpb, int kpn) {
+    constexpr int BN = NTS * 16, BM = MT * 16;
+    __shared__ float red[NW][BM][BN + 1];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int KQ = K >> 5, KP = K >> 6;
+    const int kp_per = (kpn + NW - 1) / NW;
+    const int kp0 = kpb + min(kpn, wave * kp_per);
+    const int nsteps = kpb + min(kpn, (wave + 1) * kp_per) - kp0;
+    const int NT = (N + 15) >> 4;
+
+    const u8* wp[NTS];
 #pragma unroll
-    for (int t = 0; t < NTS; ++t)
+    for (int t = 0; t < NTS; ++t) wp[t] = w + ((size_t)min((n0 >> 4) + t, NT - 1) * KP + kp0) * 1024 + lane * 16;
+    // x: the two k-steps of a pair are 512 elements apart in fragment layout, 32 row-major
+    const u16* xp[MT];
+    bool xv[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        if (XL == W_FRAG) {
+            xv[mt] = true;
+            xp[mt] = x + ((size_t)mt * KQ + 2 * kp0) * 512 + lane * 8;
+        } else {
+            xv[mt] = 16 * mt + r < M;
+            xp[mt] = x + (size_t)min(16 * mt + r, M - 1) * K + 64 * kp0 + 8 * g;
+        }
+    }
+    constexpr size_t XSTEP = XL == W_FRAG ? 1024 : 64, XHALF = XL == W_FRAG ? 512 : 32;
+
+    u32x4 wb[PD][NTS];
+    bf16x8 xb[PD][MT][2];
+    const bf16x8 zero8 = {};
+    auto xload = [&](int j, int s) {
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) red[wave][16 * mt + r][16 * t + 4 * g + i] = acc[t][mt][i];
-    __syncthreads();
-    for (int e = threadIdx.x; e < BM * BN; e += NW * 64) {
-        const int m = e / BN, nl = e % BN, n = n0 + nl;
-        if (m >= M || n >= N) continue;
-        float s = 0.f;
+            for (int h = 0; h < 2; ++h)
+                xb[j][mt][h] =
+                    xv[mt] ? *reinterpret_cast<const bf16x8*>(xp[mt] + (size_t)s * XSTEP + h * XHALF) : zero8;
+    };
 #pragma unroll
-        for (int wv = 0; wv < NW; ++wv) s += red[wv][m][nl];
-        store_out<OUT>(y, (size_t)m * ldy + n, s);
+    for (int j = 0; j < PD; ++j) {
+        if (j < nsteps) {
+#pragma unroll
+            for (int t = 0; t < NTS; ++t) wb[j][t] = ldw8(wp[t] + j * 1024);
+            xload(j, j);
+        }
     }
+    f32x4 acc[NTS][MT];
+#pragma unroll
+    for (int t = 0; t < NTS; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int s0 = 0; s0 < nsteps; s0 += PD) {
+#pragma unroll
+        for (int j = 0; j < PD; ++j) {
+            const int s = s0 + j;
+            if (s < nsteps) {
+#pragma unroll
+                for (int t = 0; t < NTS; ++t) {
+                    bf16x8 a0, a1;
+                    e4m3x16_to_bf16(wb[j][t], a0, a1);
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        acc[t][mt] = mfma16(a0, xb[j][mt][0], acc[t][mt]);
+                        acc[t][mt] = mfma16(a1, xb[j][mt][1], acc[t][mt]);
+                    }
+                }
+                if (s + PD < nsteps) {
+#pragma unroll
+                    for (int t = 0; t < NTS; ++t) wb[j][t] = ldw8(wp[t] + (size_t)(s + PD) * 1024);
+                    xload(j, s + PD);
+                }
+            }
+        }
+    }
+    gemv_finish<NTS, MT, NW, OUT>(acc, red, M, N, y, ldy, n0, scale);
 }
 
 template <int NTS, int MT, int NW, int PD, int OUT, int WL, int XL>
-__global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x, const u16* __restrict__ w, int M,
-                                                      int N, int K, void* __restrict__ y) {
-    gemv_block<NTS, MT, NW, PD, OUT, WL, XL>(x, w, M, N, K, y, N, blockIdx.x * NTS * 16, 0, K >> 5);
+__global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x, const void* __restrict__ w,
+                                                      const float* __restrict__ scale, int M, int N, int K,
+                                                      void* __restrict__ y, int ldy) {
+    if constexpr (WL == W_F8)
+        gemv_block_f8<NTS, MT, NW, PD, OUT, XL>(x, (const u8*)w, scale, M, N, K, y, ldy, blockIdx.x * NTS * 16, 0,
+                                                K >> 6);
+    else
+        gemv_block<NTS, MT, NW, PD, OUT, WL, XL>(x, (const u16*)w, M, N, K, y, ldy, blockIdx.x * NTS * 16, 0,
+                                                 K >> 5);
 }
 
 // Decode in_proj (fragment-layout weights and activations, fp32 out), balanced over the CUs: workgroups
@@ -164,18 +304,24 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x
 // them to P (row stride ldp); the remaining N2 rows (the a | b projection, 64 rows at 9B) are split into
 // KS k-ranges over workgroups [G, G + ceil(N2 / 16) KS), each writing its partial sums to slice ks of
 // Pab [KS][M][N2], which the mixer adds up.  One launch, no tail of half-used CUs.
-template <int NTS, int MT, int NW, int PD>
-__global__ __launch_bounds__(NW * 64) void in_proj_decode_kernel(const u16* __restrict__ x, const u16* __restrict__ w,
-                                                                int M, int N1, int N2, int K, int G, int KS,
-                                                                float* __restrict__ P, int ldp, float* __restrict__ Pab) {
+template <int NTS, int MT, int NW, int PD, int WL>
+__global__ __launch_bounds__(NW * 64) void in_proj_decode_kernel(const u16* __restrict__ x, const void* __restrict__ w,
+                                                                const float* __restrict__ scale,
+                                                                const u16* __restrict__ w2, int M, int N1, int N2,
+                                                                int K, int G, int KS, float* __restrict__ P, int ldp,
+                                                                float* __restrict__ Pab) {
     const int bid = blockIdx.x;
     if (bid < G) {
-        gemv_block<NTS, MT, NW, PD, OUT_F32, W_FRAG, W_FRAG>(x, w, M, N1, K, P, ldp, bid * NTS * 16, 0, K >> 5);
+        if constexpr (WL == W_F8)
+            gemv_block_f8<NTS, MT, NW, PD, OUT_F32, W_FRAG>(x, (const u8*)w, scale, M, N1, K, P, ldp, bid * NTS * 16,
+                                                           0, K >> 6);
+        else
+            gemv_block<NTS, MT, NW, PD, OUT_F32, W_FRAG, W_FRAG>(x, (const u16*)w, M, N1, K, P, ldp, bid * NTS * 16,
+                                                                0, K >> 5);
     } else {
         const int e = bid - G, nt = e % ((N2 + 15) >> 4), ks = e / ((N2 + 15) >> 4);
         const int KQ = K >> 5, per = (KQ + KS - 1) / KS;
         const int kqb = min(KQ, ks * per), kqn = min(KQ, kqb + per) - kqb;
-        const u16* w2 = w + (size_t)(N1 >> 4) * KQ * 512;  // first fragment row of the split rows
         gemv_block<1, MT, NW, PD, OUT_F32, W_FRAG, W_FRAG>(x, w2, M, N2, K, Pab + (size_t)ks * M * N2, N2, nt * 16,
                                                           kqb, kqn);
     }
@@ -186,9 +332,25 @@ __global__ __launch_bounds__(NW * 64) void in_proj_decode_kernel(const u16* __re
 // ------------------------------------------------------------------------------------------------
 constexpr int TBM = 128, TBN = 128, TBK = 64, TPAD = 8, TLD = TBK + TPAD, GROUP_M = 8;
 
+// Epilogue of both GEMMs: C of a 32x32x16 MFMA (lane l, element e -> row 8 (e / 4) + 4 (l / 32) + e % 4,
+// column l % 32) at (row0, col), times scale[col] when given.
+template <int OUT>
+__device__ __forceinline__ void store_tile32(const f32x16& c, int row0, int col, int M, int N, void* y, int ldy,
+                                             const float* __restrict__ scale) {
+    if (col >= N) return;
+    const float sc = scale ? scale[col] : 1.0f;
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int row = row0 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
+        if (row < M) store_out<OUT>(y, (size_t)row * ldy + col, scale ? c[e] * sc : c[e]);
+    }
+}
+
 template <int OUT, int WL>
-__global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, const u16* __restrict__ w, int M, int N,
-                                                   int K, void* __restrict__ y) {
+__global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, const void* __restrict__ wv,
+                                                   const float* __restrict__ scale, int M, int N, int K,
+                                                   void* __restrict__ y, int ldy) {
     __shared__ __attribute__((aligned(16))) u16 As[2][TBM * TLD];
     __shared__ __attribute__((aligned(16))) u16 Bs[2][TBN * TLD];
 
@@ -209,10 +371,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
     const int tm = first_m + (t % gsz) % gm, tn = (t % gsz) / gm;
     const int m0 = tm * TBM, n0 = tn * TBN;
 
-    // global -> register staging: 1024 16-byte pieces per operand tile, 4 per thread
+    // global -> register staging: 1024 16-byte pieces per operand tile, 4 per thread (W_F8: 512 B pieces,
+    // 2 per thread, each widened to two 16-byte bf16 pieces on the way to LDS)
+    constexpr int NB = WL == W_F8 ? 2 : 4;
+    const u16* w = (const u16*)wv;
+    const u8* w8 = (const u8*)wv;
     u16x8 ra[4], rb[4];
+    u32x4 rq[2];
     const u16* ag[4];
     const u16* bg[4];
+    const u8* bq[2];
     int soffa[4], soffb[4];
     const int NT = (N + 15) >> 4;
 #pragma unroll
@@ -221,7 +389,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
         const int row = c >> 3, col = (c & 7) * 8;
         ag[j] = x + (size_t)min(m0 + row, M - 1) * K + col;
         soffa[j] = row * TLD + col;
-        if (WL == W_FRAG) {
+        if (WL == W_F8) {
+            // piece c (< 512) of the 8 W_F8 blocks (8 n-tiles x 1 k-pair): lane l of n-tile c / 64; its two
+            // 8-code halves are columns 8 g and 32 + 8 g of row 16 ntl + r
+            if (j < NB) {
+                const int ntl = c >> 6, l = c & 63;
+                bq[j] = w8 + (size_t)min((n0 >> 4) + ntl, NT - 1) * (K >> 6) * 1024 + l * 16;
+                soffb[2 * j] = (16 * ntl + (l & 15)) * TLD + 8 * (l >> 4);
+                soffb[2 * j + 1] = soffb[2 * j] + 32;
+            }
+        } else if (WL == W_FRAG) {
             // piece c of the 16 fragment blocks (8 n-tiles x 2 k-steps) covering this 128 x 64 tile
             const int blk = c >> 6, l = c & 63;
             const int ntl = blk >> 1, kql = blk & 1;
@@ -232,8 +409,31 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
             soffb[j] = row * TLD + col;
         }
     }
-    // k advance per 64-wide step: row-major 64 elements, fragment layout 2 blocks
-    constexpr size_t BSTEP = WL == W_FRAG ? 1024 : TBK;
+    // k advance per 64-wide step: row-major 64 elements, fragment layout 2 blocks, W_F8 one block (bytes)
+    constexpr size_t BSTEP = WL == W_ROW ? TBK : 1024;
+    auto bload = [&](int kt) {
+        if constexpr (WL == W_F8) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) rq[j] = *reinterpret_cast<const u32x4*>(bq[j] + (size_t)kt * BSTEP);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) rb[j] = *reinterpret_cast<const u16x8*>(bg[j] + (size_t)kt * BSTEP);
+        }
+    };
+    auto bstore = [&](int buf) {
+        if constexpr (WL == W_F8) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                bf16x8 lo, hi;
+                e4m3x16_to_bf16(rq[j], lo, hi);
+                *reinterpret_cast<bf16x8*>(&Bs[buf][soffb[2 * j]]) = lo;
+                *reinterpret_cast<bf16x8*>(&Bs[buf][soffb[2 * j + 1]]) = hi;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) *reinterpret_cast<u16x8*>(&Bs[buf][soffb[j]]) = rb[j];
+        }
+    };
 
     f32x16 acc[2][2];
 #pragma unroll
@@ -245,15 +445,11 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
 
     const int nk = K / TBK;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        ra[j] = *reinterpret_cast<const u16x8*>(ag[j]);
-        rb[j] = *reinterpret_cast<const u16x8*>(bg[j]);
-    }
+    for (int j = 0; j < 4; ++j) ra[j] = *reinterpret_cast<const u16x8*>(ag[j]);
+    bload(0);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        *reinterpret_cast<u16x8*>(&As[0][soffa[j]]) = ra[j];
-        *reinterpret_cast<u16x8*>(&Bs[0][soffb[j]]) = rb[j];
-    }
+    for (int j = 0; j < 4; ++j) *reinterpret_cast<u16x8*>(&As[0][soffa[j]]) = ra[j];
+    bstore(0);
     __syncthreads();
 
     const int fr = lane & 31;
@@ -262,10 +458,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
         const int cur = kt & 1;
         if (kt + 1 < nk) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                ra[j] = *reinterpret_cast<const u16x8*>(ag[j] + (size_t)(kt + 1) * TBK);
-                rb[j] = *reinterpret_cast<const u16x8*>(bg[j] + (size_t)(kt + 1) * BSTEP);
-            }
+            for (int j = 0; j < 4; ++j) ra[j] = *reinterpret_cast<const u16x8*>(ag[j] + (size_t)(kt + 1) * TBK);
+            bload(kt + 1);
         }
 #pragma unroll
         for (int kk = 0; kk < TBK; kk += 16) {
@@ -283,27 +477,18 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
         }
         if (kt + 1 < nk) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                *reinterpret_cast<u16x8*>(&As[cur ^ 1][soffa[j]]) = ra[j];
-                *reinterpret_cast<u16x8*>(&Bs[cur ^ 1][soffb[j]]) = rb[j];
-            }
+            for (int j = 0; j < 4; ++j) *reinterpret_cast<u16x8*>(&As[cur ^ 1][soffa[j]]) = ra[j];
+            bstore(cur ^ 1);
         }
         __syncthreads();
     }
 
-    // C layout of 32x32 MFMA: lane l, element e -> row 8*(e/4) + 4*(l/32) + e%4, column l % 32.
 #pragma unroll
     for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const int col = n0 + wn * 64 + j * 32 + (lane & 31);
-            if (col >= N) continue;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int row = m0 + wm * 64 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                if (row < M) store_out<OUT>(y, (size_t)row * N + col, acc[i][j][e]);
-            }
-        }
+        for (int j = 0; j < 2; ++j)
+            store_tile32<OUT>(acc[i][j], m0 + wm * 64 + i * 32, n0 + wn * 64 + j * 32 + (lane & 31), M, N, y, ldy,
+                              WL == W_F8 ? scale : nullptr);
 }
 
 
@@ -323,8 +508,9 @@ constexpr int LBM = 256, LBN = 256, LBK = 64, LLD = LBK + 8;
 __device__ __forceinline__ int lds_off(int row, int ch) { return row * LLD + (ch << 3); }
 
 template <int OUT, int WL>
-__global__ __launch_bounds__(256, 1) void gemm256_kernel(const u16* __restrict__ x, const u16* __restrict__ w, int M,
-                                                         int N, int K, void* __restrict__ y) {
+__global__ __launch_bounds__(256, 1) void gemm256_kernel(const u16* __restrict__ x, const void* __restrict__ wv,
+                                                         const float* __restrict__ scale, int M, int N, int K,
+                                                         void* __restrict__ y, int ldy) {
     __shared__ __attribute__((aligned(16))) u16 As[2][LBM * LLD];
     __shared__ __attribute__((aligned(16))) u16 Bs[2][LBN * LLD];
 
@@ -341,9 +527,14 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(const u16* __restrict__
     const int m0 = tm * LBM, n0 = tn * LBN;
     const int KQ = K >> 5, NT = (N + 15) >> 4;
 
-    // staging: 8 A and 8 B pieces of 16 bytes per thread and k-tile
+    // staging: 8 A and 8 B pieces of 16 bytes per thread and k-tile (W_F8: 4 B pieces of 16 codes, each
+    // widened to two bf16 pieces on the way to LDS)
+    constexpr int NB = WL == W_F8 ? 4 : 8;
+    const u16* w = (const u16*)wv;
+    const u8* w8 = (const u8*)wv;
     const u16* ag[8];
     const u16* bg[8];
+    const u8* bq[4];
     int sa[8], sb[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -351,7 +542,14 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(const u16* __restrict__
         const int row = c >> 3, ch = c & 7;
         ag[j] = x + (size_t)min(m0 + row, M - 1) * K + ch * 8;
         sa[j] = lds_off(row, ch);
-        if (WL == W_FRAG) {  // piece c of the 32 fragment blocks (16 n-tiles x 2 k-steps) of the tile
+        if (WL == W_F8) {  // piece c (< 1024) of the 16 W_F8 blocks (16 n-tiles x 1 k-pair) of the tile
+            if (j < NB) {
+                const int ntl = c >> 6, l = c & 63;
+                bq[j] = w8 + (size_t)min((n0 >> 4) + ntl, NT - 1) * (K >> 6) * 1024 + l * 16;
+                sb[2 * j] = lds_off(16 * ntl + (l & 15), l >> 4);
+                sb[2 * j + 1] = lds_off(16 * ntl + (l & 15), 4 + (l >> 4));
+            }
+        } else if (WL == W_FRAG) {  // piece c of the 32 fragment blocks (16 n-tiles x 2 k-steps) of the tile
             const int blk = c >> 6, l = c & 63;
             const int ntl = blk >> 1, kql = blk & 1;
             bg[j] = w + ((size_t)min((n0 >> 4) + ntl, NT - 1) * KQ + kql) * 512 + l * 8;
@@ -361,23 +559,37 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(const u16* __restrict__
             sb[j] = lds_off(row, ch);
         }
     }
-    constexpr int BSTEP = WL == W_FRAG ? 1024 : LBK;  // elements per k-tile along a B piece's stream
+    // elements (W_F8: bytes) per k-tile along a B piece's stream
+    constexpr int BSTEP = WL == W_ROW ? LBK : 1024;
     const int nk = K / LBK;
 
+    // B staging: 8 bf16 pieces, or 4 code pieces in the first half of the same registers
     u16x8 ra0[8], rb0[8], ra1[8], rb1[8];
     auto gload = [&](u16x8* ra, u16x8* rb, int kt) {
         const int k = min(kt, nk - 1);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            ra[j] = *reinterpret_cast<const u16x8*>(ag[j] + (size_t)k * LBK);
-            rb[j] = *reinterpret_cast<const u16x8*>(bg[j] + (size_t)k * BSTEP);
+        for (int j = 0; j < 8; ++j) ra[j] = *reinterpret_cast<const u16x8*>(ag[j] + (size_t)k * LBK);
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            if constexpr (WL == W_F8)
+                rb[j] = __builtin_bit_cast(u16x8, *reinterpret_cast<const u32x4*>(bq[j] + (size_t)k * BSTEP));
+            else
+                rb[j] = *reinterpret_cast<const u16x8*>(bg[j] + (size_t)k * BSTEP);
         }
     };
     auto lstore = [&](const u16x8* ra, const u16x8* rb, int buf) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            *reinterpret_cast<u16x8*>(&As[buf][sa[j]]) = ra[j];
-            *reinterpret_cast<u16x8*>(&Bs[buf][sb[j]]) = rb[j];
+        for (int j = 0; j < 8; ++j) *reinterpret_cast<u16x8*>(&As[buf][sa[j]]) = ra[j];
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            if constexpr (WL == W_F8) {
+                bf16x8 lo, hi;
+                e4m3x16_to_bf16(__builtin_bit_cast(u32x4, rb[j]), lo, hi);
+                *reinterpret_cast<bf16x8*>(&Bs[buf][sb[2 * j]]) = lo;
+                *reinterpret_cast<bf16x8*>(&Bs[buf][sb[2 * j + 1]]) = hi;
+            } else {
+                *reinterpret_cast<u16x8*>(&Bs[buf][sb[j]]) = rb[j];
+            }
         }
     };
 
@@ -449,32 +661,35 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(const u16* __restrict__
         tile(1, ra1, rb1, ra0, rb0, kt + 3);
     }
 
-    // C layout of 32x32 MFMA: lane l, element e -> row 8*(e/4) + 4*(l/32) + e%4, column l % 32.
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int col = n0 + wn * 128 + j * 32 + (lane & 31);
-            if (col >= N) continue;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int row = m0 + wm * 128 + i * 32 + 8 * (e >> 2) + 4 * (lane >> 5) + (e & 3);
-                if (row < M) store_out<OUT>(y, (size_t)row * N + col, acc[i][j][e]);
-            }
-        }
+        for (int j = 0; j < 4; ++j)
+            store_tile32<OUT>(acc[i][j], m0 + wm * 128 + i * 32, n0 + wn * 128 + j * 32 + (lane & 31), M, N, y, ldy,
+                              WL == W_F8 ? scale : nullptr);
 }
 
+// Launch arguments shared by the projection dispatchers below.
+struct LinArgs {
+    const void* x;
+    const void* w;
+    const float* scale;
+    int M, N, K;
+    void* y;
+    int ldy, out_kind;
+};
+
 template <int NTS, int MT, int NW, int WL, int XL>
-hipError_t gemv(const void* x, const void* w, int M, int N, int K, void* y, int out_kind, hipStream_t stream) {
+hipError_t gemv(const LinArgs& a, hipStream_t stream) {
     constexpr int PD = 4;
-    const dim3 grid((N + NTS * 16 - 1) / (NTS * 16));
+    const dim3 grid((a.N + NTS * 16 - 1) / (NTS * 16));
     const dim3 block(NW * 64);
-    if (out_kind == OUT_F32)
-        hipLaunchKernelGGL((gemv_kernel<NTS, MT, NW, PD, OUT_F32, WL, XL>), grid, block, 0, stream, (const u16*)x,
-                           (const u16*)w, M, N, K, y);
+    if (a.out_kind == OUT_F32)
+        hipLaunchKernelGGL((gemv_kernel<NTS, MT, NW, PD, OUT_F32, WL, XL>), grid, block, 0, stream, (const u16*)a.x,
+                           a.w, a.scale, a.M, a.N, a.K, a.y, a.ldy);
     else
-        hipLaunchKernelGGL((gemv_kernel<NTS, MT, NW, PD, OUT_BF16, WL, XL>), grid, block, 0, stream, (const u16*)x,
-                           (const u16*)w, M, N, K, y);
+        hipLaunchKernelGGL((gemv_kernel<NTS, MT, NW, PD, OUT_BF16, WL, XL>), grid, block, 0, stream, (const u16*)a.x,
+                           a.w, a.scale, a.M, a.N, a.K, a.y, a.ldy);
     return hipGetLastError();
 }
 
@@ -482,59 +697,72 @@ hipError_t gemv(const void* x, const void* w, int M, int N, int K, void* y, int 
 // enough waves per workgroup to keep >= 8 k-steps of 32 per wave.  Measured on the 9B shape at M = 64:
 // in_proj (N 12352, K 4096) NTS 4 / NW 4, out_proj (N 4096, K 4096) NTS 1 / NW 8.
 template <int MT, int WL, int XL>
-hipError_t gemv_mt(const void* x, const void* w, int M, int N, int K, void* y, int out_kind, hipStream_t stream) {
-    const int NT = (N + 15) / 16, KQ = K / 32;
+hipError_t gemv_mt(const LinArgs& a, hipStream_t stream) {
+    const int NT = (a.N + 15) / 16, KQ = a.K / 32;
     if (NT >= 4 * 160) {
-        if (KQ >= 64) return gemv<4, MT, 4, WL, XL>(x, w, M, N, K, y, out_kind, stream);
-        return gemv<4, MT, 2, WL, XL>(x, w, M, N, K, y, out_kind, stream);
+        if (KQ >= 64) return gemv<4, MT, 4, WL, XL>(a, stream);
+        return gemv<4, MT, 2, WL, XL>(a, stream);
     }
     if (NT >= 2 * 160) {
-        if (KQ >= 64) return gemv<2, MT, 8, WL, XL>(x, w, M, N, K, y, out_kind, stream);
-        return gemv<2, MT, 4, WL, XL>(x, w, M, N, K, y, out_kind, stream);
+        if (KQ >= 64) return gemv<2, MT, 8, WL, XL>(a, stream);
+        return gemv<2, MT, 4, WL, XL>(a, stream);
     }
-    if (KQ >= 64) return gemv<1, MT, 8, WL, XL>(x, w, M, N, K, y, out_kind, stream);
-    return gemv<1, MT, 4, WL, XL>(x, w, M, N, K, y, out_kind, stream);
+    if (KQ >= 64) return gemv<1, MT, 8, WL, XL>(a, stream);
+    return gemv<1, MT, 4, WL, XL>(a, stream);
 }
 
 template <int WL, int XL>
-hipError_t gemv_m(const void* x, const void* w, int M, int N, int K, void* y, int out_kind, hipStream_t stream) {
-    if (M <= 16) return gemv_mt<1, WL, XL>(x, w, M, N, K, y, out_kind, stream);
-    if (M <= 32) return gemv_mt<2, WL, XL>(x, w, M, N, K, y, out_kind, stream);
-    if (M <= 48) return gemv_mt<3, WL, XL>(x, w, M, N, K, y, out_kind, stream);
-    return gemv_mt<4, WL, XL>(x, w, M, N, K, y, out_kind, stream);
+hipError_t gemv_m(const LinArgs& a, hipStream_t stream) {
+    if (a.M <= 16) return gemv_mt<1, WL, XL>(a, stream);
+    if (a.M <= 32) return gemv_mt<2, WL, XL>(a, stream);
+    if (a.M <= 48) return gemv_mt<3, WL, XL>(a, stream);
+    return gemv_mt<4, WL, XL>(a, stream);
 }
 
 template <int WL>
-hipError_t linear_wl(const void* x, int xlayout, const void* w, int M, int N, int K, void* y, int out_kind,
-                     hipStream_t stream) {
-    if (M <= 64) {
-        if (xlayout == W_FRAG) return gemv_m<WL, W_FRAG>(x, w, M, N, K, y, out_kind, stream);
-        return gemv_m<WL, W_ROW>(x, w, M, N, K, y, out_kind, stream);
+hipError_t linear_wl(const LinArgs& a, int xlayout, hipStream_t stream) {
+    if (a.M <= 64) {
+        if (xlayout == W_FRAG) return gemv_m<WL, W_FRAG>(a, stream);
+        return gemv_m<WL, W_ROW>(a, stream);
     }
     if (xlayout != W_ROW) return hipErrorInvalidValue;  // the GEMM reads row-major activations
-    if ((size_t)M * N >= (size_t)256 * 256 * 256) {  // >= one round of 256 x 256 tiles over the CUs
-        const dim3 grid(((M + LBM - 1) / LBM) * ((N + LBN - 1) / LBN));
-        if (out_kind == OUT_F32)
-            hipLaunchKernelGGL((gemm256_kernel<OUT_F32, WL>), grid, dim3(256), 0, stream, (const u16*)x,
-                               (const u16*)w, M, N, K, y);
+    const u16* x = (const u16*)a.x;
+    if ((size_t)a.M * a.N >= (size_t)256 * 256 * 256) {  // >= one round of 256 x 256 tiles over the CUs
+        const dim3 grid(((a.M + LBM - 1) / LBM) * ((a.N + LBN - 1) / LBN));
+        if (a.out_kind == OUT_F32)
+            hipLaunchKernelGGL((gemm256_kernel<OUT_F32, WL>), grid, dim3(256), 0, stream, x, a.w, a.scale, a.M, a.N,
+                               a.K, a.y, a.ldy);
         else
-            hipLaunchKernelGGL((gemm256_kernel<OUT_BF16, WL>), grid, dim3(256), 0, stream, (const u16*)x,
-                               (const u16*)w, M, N, K, y);
+            hipLaunchKernelGGL((gemm256_kernel<OUT_BF16, WL>), grid, dim3(256), 0, stream, x, a.w, a.scale, a.M,
+                               a.N, a.K, a.y, a.ldy);
         return hipGetLastError();
     }
-    const dim3 grid(((M + TBM - 1) / TBM) * ((N + TBN - 1) / TBN));
-    if (out_kind == OUT_F32)
-        hipLaunchKernelGGL((gemm_kernel<OUT_F32, WL>), grid, dim3(256), 0, stream, (const u16*)x, (const u16*)w, M,
-                           N, K, y);
+    const dim3 grid(((a.M + TBM - 1) / TBM) * ((a.N + TBN - 1) / TBN));
+    if (a.out_kind == OUT_F32)
+        hipLaunchKernelGGL((gemm_kernel<OUT_F32, WL>), grid, dim3(256), 0, stream, x, a.w, a.scale, a.M, a.N, a.K,
+                           a.y, a.ldy);
     else
-        hipLaunchKernelGGL((gemm_kernel<OUT_BF16, WL>), grid, dim3(256), 0, stream, (const u16*)x, (const u16*)w,
-                           M, N, K, y);
+        hipLaunchKernelGGL((gemm_kernel<OUT_BF16, WL>), grid, dim3(256), 0, stream, x, a.w, a.scale, a.M, a.N, a.K,
+                           a.y, a.ldy);
     return hipGetLastError();
 }
 
 }  // namespace
 
 size_t frag_elems(int N, int K) { return (size_t)((N + 15) / 16) * 16 * K; }
+
+hipError_t launch_quantize_e4m3(const void* w, int N, int K, u8* q, float* scale, int to_frag, hipStream_t stream) {
+    if (N <= 0 || K <= 0) return hipSuccess;
+    if (to_frag) {
+        if (K % 64) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(quantize_e4m3_kernel<true>, dim3((N + 15) / 16 * 16), dim3(256), 0, stream, (const u16*)w,
+                           N, K, q, scale);
+    } else {
+        hipLaunchKernelGGL(quantize_e4m3_kernel<false>, dim3(N), dim3(256), 0, stream, (const u16*)w, N, K, q,
+                           scale);
+    }
+    return hipGetLastError();
+}
 
 hipError_t launch_frag_tile(const void* w, int N, int K, void* wf, hipStream_t stream) {
     const size_t pieces = frag_elems(N, K) / 8;
@@ -545,43 +773,74 @@ hipError_t launch_frag_tile(const void* w, int N, int K, void* wf, hipStream_t s
 
 namespace {
 
-template <int MT>
-hipError_t in_proj_decode_mt(const void* x, const void* w, int M, int N1, int N2, int K, float* P, int ldp,
-                             float* Pab, int ab_splits, hipStream_t stream) {
+struct DecodeArgs {
+    const u16* x;
+    const void* w;
+    const float* scale;
+    const u16* w2;
+    int M, N1, N2, K, G, KS;
+    float* P;
+    int ldp;
+    float* Pab;
+};
+
+template <int NTS, int MT, int WL>
+void in_proj_decode_launch(const DecodeArgs& a, hipStream_t stream) {
     constexpr int PD = 4, NW = 4;
-    const int NT1 = N1 >> 4, NT2 = (N2 + 15) >> 4;
+    const dim3 grid(a.G + ((a.N2 + 15) >> 4) * a.KS), block(NW * 64);
+    hipLaunchKernelGGL((in_proj_decode_kernel<NTS, MT, NW, PD, WL>), grid, block, 0, stream, a.x, a.w, a.scale, a.w2,
+                       a.M, a.N1, a.N2, a.K, a.G, a.KS, a.P, a.ldp, a.Pab);
+}
+
+template <int MT, int WL>
+hipError_t in_proj_decode_mt(DecodeArgs a, hipStream_t stream) {
+    const int NT1 = a.N1 >> 4;
     // tiles per workgroup: the smallest that keeps the main workgroups within one per CU
     const int nts = NT1 <= 256 ? 1 : (NT1 <= 512 ? 2 : (NT1 <= 768 ? 3 : 4));
     if (NT1 % nts) return hipErrorInvalidValue;
-    const int G = NT1 / nts;
-    const dim3 grid(G + NT2 * ab_splits), block(NW * 64);
-    const u16 *xs = (const u16*)x, *ws = (const u16*)w;
+    a.G = NT1 / nts;
     switch (nts) {
-        case 1: hipLaunchKernelGGL((in_proj_decode_kernel<1, MT, NW, PD>), grid, block, 0, stream, xs, ws, M, N1, N2, K, G, ab_splits, P, ldp, Pab); break;
-        case 2: hipLaunchKernelGGL((in_proj_decode_kernel<2, MT, NW, PD>), grid, block, 0, stream, xs, ws, M, N1, N2, K, G, ab_splits, P, ldp, Pab); break;
-        case 3: hipLaunchKernelGGL((in_proj_decode_kernel<3, MT, NW, PD>), grid, block, 0, stream, xs, ws, M, N1, N2, K, G, ab_splits, P, ldp, Pab); break;
-        default: hipLaunchKernelGGL((in_proj_decode_kernel<4, MT, NW, PD>), grid, block, 0, stream, xs, ws, M, N1, N2, K, G, ab_splits, P, ldp, Pab); break;
+        case 1: in_proj_decode_launch<1, MT, WL>(a, stream); break;
+        case 2: in_proj_decode_launch<2, MT, WL>(a, stream); break;
+        case 3: in_proj_decode_launch<3, MT, WL>(a, stream); break;
+        default: in_proj_decode_launch<4, MT, WL>(a, stream); break;
     }
     return hipGetLastError();
 }
 
-}  // namespace
-
-hipError_t launch_in_proj_decode(const void* x_frag, const void* w_frag, int M, int N1, int N2, int K, float* P,
-                                 int ldp, float* Pab, int ab_splits, hipStream_t stream) {
-    if (M <= 0) return hipSuccess;
-    if (M > 64 || N1 % 16 || ab_splits <= 0 || K % 32) return hipErrorInvalidValue;
-    if (M <= 16) return in_proj_decode_mt<1>(x_frag, w_frag, M, N1, N2, K, P, ldp, Pab, ab_splits, stream);
-    if (M <= 32) return in_proj_decode_mt<2>(x_frag, w_frag, M, N1, N2, K, P, ldp, Pab, ab_splits, stream);
-    if (M <= 48) return in_proj_decode_mt<3>(x_frag, w_frag, M, N1, N2, K, P, ldp, Pab, ab_splits, stream);
-    return in_proj_decode_mt<4>(x_frag, w_frag, M, N1, N2, K, P, ldp, Pab, ab_splits, stream);
+template <int WL>
+hipError_t in_proj_decode_wl(const DecodeArgs& a, hipStream_t stream) {
+    if (a.M <= 16) return in_proj_decode_mt<1, WL>(a, stream);
+    if (a.M <= 32) return in_proj_decode_mt<2, WL>(a, stream);
+    if (a.M <= 48) return in_proj_decode_mt<3, WL>(a, stream);
+    return in_proj_decode_mt<4, WL>(a, stream);
 }
 
-hipError_t launch_linear(const void* x, int xlayout, const void* w, int wlayout, int M, int N, int K, void* y,
-                         int out_kind, hipStream_t stream) {
+}  // namespace
+
+hipError_t launch_in_proj_decode(const void* x_frag, const void* w, int wlayout, const float* w_scale,
+                                 const void* w2, int M, int N1, int N2, int K, float* P, int ldp, float* Pab,
+                                 int ab_splits, hipStream_t stream) {
+    if (M <= 0) return hipSuccess;
+    if (M > 64 || N1 % 16 || ab_splits <= 0 || K % 32) return hipErrorInvalidValue;
+    if (wlayout != W_FRAG && wlayout != W_F8) return hipErrorInvalidValue;
+    if (wlayout == W_F8 && (K % 64 || !w_scale)) return hipErrorInvalidValue;
+    const DecodeArgs a{(const u16*)x_frag, w, w_scale, (const u16*)w2, M, N1, N2, K, 0, ab_splits, P, ldp, Pab};
+    if (wlayout == W_F8) return in_proj_decode_wl<W_F8>(a, stream);
+    return in_proj_decode_wl<W_FRAG>(a, stream);
+}
+
+hipError_t launch_linear(const void* x, int xlayout, const void* w, int wlayout, const float* w_scale, int M, int N,
+                         int K, void* y, int ldy, int out_kind, hipStream_t stream) {
     if (M <= 0 || N <= 0) return hipSuccess;
-    if (wlayout == W_FRAG) return linear_wl<W_FRAG>(x, xlayout, w, M, N, K, y, out_kind, stream);
-    return linear_wl<W_ROW>(x, xlayout, w, M, N, K, y, out_kind, stream);
+    if (ldy < N) return hipErrorInvalidValue;
+    const LinArgs a{x, w, w_scale, M, N, K, y, ldy, out_kind};
+    if (wlayout == W_F8) {
+        if (K % 64 || !w_scale) return hipErrorInvalidValue;
+        return linear_wl<W_F8>(a, xlayout, stream);
+    }
+    if (wlayout == W_FRAG) return linear_wl<W_FRAG>(a, xlayout, stream);
+    return linear_wl<W_ROW>(a, xlayout, stream);
 }
 
 }  // namespace gdn

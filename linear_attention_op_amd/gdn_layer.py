@@ -85,9 +85,12 @@ def cu_seqlens_arg(cu_seqlens, n_seqs):
 class Qwen35GatedDeltaNetHIP:
     """One GDN layer.  `weights` is an HF Qwen3_5GatedDeltaNet or a dict with keys
     w_qkv [conv_dim, H], w_z [Vd, H], w_a, w_b [nv, H], conv_w [conv_dim, 4], A_log, dt_bias [nv],
-    norm_w [dv], w_out [H, Vd] (projection weights are used as bf16, the rest as fp32)."""
+    norm_w [dv], w_out [H, Vd] (projection weights are used as bf16, the rest as fp32).
+    `weight_dtype` ("bf16" or "fp8") mirrors the reference's weight_dtype (9B/gdn_layer.py:55): "fp8" keeps the
+    q|k|v|z and out projections as E4M3 with per-row scales (see quantize_fp8); a|b stay bf16."""
 
-    def __init__(self, weights, dims=None, batch=1, max_slots=None, max_tokens=16384, device="cuda", _handle=None):
+    def __init__(self, weights, dims=None, batch=1, max_slots=None, max_tokens=16384, device="cuda", _handle=None,
+                 weight_dtype="bf16"):
         self.device = torch.device(device)
         self.batch = batch
         self.max_slots = max_slots or batch
@@ -99,14 +102,17 @@ class Qwen35GatedDeltaNetHIP:
             self.dims, cdims, cw, _keep = prepare_weights(weights, dims, self.device)
             self._h, self._owned = ctypes.c_void_p(), True
             torch.cuda.synchronize(self.device)
-            _lib.check(_lib.lib().gdn_layer_create(ctypes.byref(cdims), ctypes.byref(cw), self.max_slots,
-                                                   self.max_tokens, ctypes.byref(self._h)))
+            _lib.check(_lib.lib().gdn_layer_create_ex(ctypes.byref(cdims), ctypes.byref(cw), self.max_slots,
+                                                      self.max_tokens, _lib.weight_format(weight_dtype),
+                                                      ctypes.byref(self._h)))
         d = self.dims
         self.hidden = d["hidden"]
         self.nk, self.nv = d["num_k_heads"], d["num_v_heads"]
         self.dk, self.dv = d["head_k_dim"], d["head_v_dim"]
         self.conv_dim = 2 * self.nk * self.dk + self.nv * self.dv
         self.proj_width = _lib.lib().gdn_layer_proj_width(self._h)
+        fmt = _lib.lib().gdn_layer_weight_format(self._h)
+        self.weight_dtype = "fp8" if fmt == _lib.GDN_WEIGHTS_FP8_E4M3 else "bf16"
 
     @classmethod
     def from_checkpoint(cls, path, layer_idx, prefix=None, **kwargs):
@@ -259,3 +265,13 @@ def linear(x, w, out_dtype=torch.float32):
     _lib.check(_lib.lib().gdn_linear_bf16(_ptr(x), _ptr(w), x.shape[0], w.shape[0], x.shape[1], _ptr(y),
                                           int(out_dtype == torch.float32), _stream()))
     return y
+
+
+def quantize_fp8(w):
+    """The library's E4M3 weight quantizer (gdn_quantize_fp8) on a CUDA matrix w [N, K]: -> (codes uint8 [N, K],
+    scales fp32 [N]); row n dequantizes to e4m3_value(codes[n]) * scales[n], scales[n] = max|w[n]| / 448."""
+    w = w.to(torch.bfloat16).contiguous()
+    q = torch.empty(w.shape, device=w.device, dtype=torch.uint8)
+    s = torch.empty(w.shape[0], device=w.device, dtype=torch.float32)
+    _lib.check(_lib.lib().gdn_quantize_fp8(_ptr(w), w.shape[0], w.shape[1], _ptr(q), _ptr(s), _stream()))
+    return q, s

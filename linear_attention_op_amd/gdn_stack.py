@@ -19,10 +19,11 @@ from .gdn_layer import Qwen35GatedDeltaNetHIP, _ptr, _slots, _stream, cu_seqlens
 
 class Qwen35GDNStackHIP:
     """`layers`: HF Qwen3_5GatedDeltaNet modules or weight dicts (see Qwen35GatedDeltaNetHIP), one per layer.
-    `norm_weights`: optional per-layer [H] weights of the RMSNorm after each layer (default 0, i.e. (1 + w) = 1)."""
+    `norm_weights`: optional per-layer [H] weights of the RMSNorm after each layer (default 0, i.e. (1 + w) = 1).
+    `weight_dtype`: "bf16" or "fp8" for every layer (wormhole_n150/qwen3.5_0.8B/gdn_l1.py:79-80)."""
 
     def __init__(self, layers, dims=None, batch=1, max_slots=None, max_tokens=None, inter_norm=False,
-                 norm_weights=None, device="cuda"):
+                 norm_weights=None, device="cuda", weight_dtype="bf16"):
         self.device = torch.device(device)
         self.batch = batch
         self.max_slots = max_slots or batch
@@ -45,8 +46,9 @@ class Qwen35GDNStackHIP:
                     nw[i] = t.data_ptr()
         self._h = ctypes.c_void_p()
         torch.cuda.synchronize(self.device)
-        _lib.check(_lib.lib().gdn_stack_create(ctypes.byref(prepared[0][1]), cw, self.n_layers, int(inter_norm),
-                                               nw, self.max_slots, self.max_tokens, ctypes.byref(self._h)))
+        _lib.check(_lib.lib().gdn_stack_create_ex(ctypes.byref(prepared[0][1]), cw, self.n_layers, int(inter_norm),
+                                                  nw, self.max_slots, self.max_tokens,
+                                                  _lib.weight_format(weight_dtype), ctypes.byref(self._h)))
         self.layers = []
         for i in range(self.n_layers):
             h = ctypes.c_void_p()

@@ -60,6 +60,11 @@ def _declare(L):
     L.orc_gated_rmsnorm.argtypes = [_P, _P, _I, _I, _P, ctypes.c_float, _P]
     L.orc_layer_forward.argtypes = [ctypes.POINTER(Dims)] + [_P] * 10 + [_I, _I] + [_P] * 5
     L.orc_conv_front.argtypes = [ctypes.POINTER(Dims), _P, _I, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P]
+    L.orc_e4m3_value.argtypes = [_I]
+    L.orc_e4m3_value.restype = ctypes.c_double
+    L.orc_e4m3_encode.argtypes = [ctypes.c_float]
+    L.orc_e4m3_encode.restype = _I
+    L.orc_quantize_e4m3.argtypes = [_P, _I, _I, ctypes.c_void_p, _P]
 
 
 def _f(a):
@@ -214,3 +219,29 @@ def conv_front(dm, P, B, T, weights, conv_state):
     lib().orc_conv_front(ctypes.byref(dm), pp, B, T, pcw, pal, pdt, _ptr(conv_state), _ptr(qn), _ptr(kn), _ptr(v),
                          _ptr(g), _ptr(beta))
     return qn, kn, v, g, beta
+
+
+# ---- low-precision weights (E4M3, one scale per row) -------------------------------------------------
+def e4m3_table():
+    """float32 [256]: the value of every E4M3 code (NaN for 0x7f and 0xff)."""
+    return np.array([lib().orc_e4m3_value(c) for c in range(256)], np.float32)
+
+
+def e4m3_encode(v):
+    """E4M3 code of one float (nearest, ties to even, saturating at +-448)."""
+    return lib().orc_e4m3_encode(float(v))
+
+
+def quantize_e4m3(w):
+    """w [N, K] -> (codes uint8 [N, K], scale float32 [N]) with scale = max|w[n]| / 448."""
+    w, pw = _f(w)
+    N, K = w.shape
+    q = np.empty((N, K), np.uint8)
+    s = np.empty(N, np.float32)
+    lib().orc_quantize_e4m3(pw, N, K, q.ctypes.data_as(ctypes.c_void_p), _ptr(s))
+    return q, s
+
+
+def dequantize_e4m3(q, scale):
+    """codes [N, K], scale [N] -> float32 [N, K] = value(code) * scale (the weights the FP8 path multiplies by)."""
+    return e4m3_table()[np.asarray(q)] * np.asarray(scale, np.float32)[:, None]

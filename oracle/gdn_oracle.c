@@ -556,3 +556,42 @@ EXPORT void orc_conv_front(const orc_dims* dm, const float* P, int B, int T, con
     for (size_t i = 0; i < (size_t)M * nv; ++i) g_out[i] = (float)g[i], beta_out[i] = (float)beta[i];
     free(pd), free(hist), free(cv), free(qn), free(kn), free(vv), free(g), free(beta);
 }
+
+/* ---- low-precision weights: E4M3 with one scale per output row -----------------------------------
+ * The reference stores w_in and w_out in its weight_dtype (9B/gdn_layer.py:55, 115-120: ttnn.bfloat16 or
+ * ttnn.bfloat8_b; w_ab stays bfloat16; 0.8B/gdn_l1.py:79-80).  bfloat8_b is a shared-exponent tile format
+ * with no MI355X counterpart; the HIP path stores those matrices as OCP 8-bit floating point E4M3
+ * (OCP 8-bit Floating Point Specification v1.0, 2023: 1 sign bit, 4 exponent bits with bias 7, 3
+ * mantissa bits; no infinities; S.1111.111 is NaN; largest finite 448; subnormals m 2^-9) with
+ * scale[n] = max_k |w[n, k]| / 448 (1 for an all-zero row) and code = nearest E4M3 value of w / scale,
+ * ties to the even mantissa, saturating at +-448.  Dequantized weight = value(code) * scale.
+ * Restated here from the specification: decode by the closed form, encode by exhaustive nearest search
+ * over the 127 non-negative finite values (an independent route from the HIP path's bit arithmetic). */
+EXPORT double orc_e4m3_value(int code) {
+    const int s = (code >> 7) & 1, e = (code >> 3) & 15, m = code & 7;
+    if (e == 15 && m == 7) return NAN;
+    const double mag = e == 0 ? ldexp((double)m, -9) : ldexp(1.0 + m / 8.0, e - 7);
+    return s ? -mag : mag;
+}
+
+EXPORT int orc_e4m3_encode(float v) {
+    const double a = fmin(fabs((double)v), 448.0);
+    int best = 0;
+    double dbest = INFINITY;
+    for (int c = 0; c <= 0x7e; ++c) {  /* codes 0..126 are the non-negative finite values, ascending */
+        const double d = fabs(orc_e4m3_value(c) - a);
+        if (d < dbest || (d == dbest && (c & 1) == 0)) best = c, dbest = d;
+    }
+    return (signbit(v) ? 0x80 : 0) | best;
+}
+
+EXPORT void orc_quantize_e4m3(const float* w, int N, int K, uint8_t* q, float* scale) {
+#pragma omp parallel for schedule(static)
+    for (int n = 0; n < N; ++n) {
+        float m = 0.f;
+        for (int k = 0; k < K; ++k) m = fmaxf(m, fabsf(w[(size_t)n * K + k]));
+        const float s = m > 0.f ? m / 448.0f : 1.0f;
+        scale[n] = s;
+        for (int k = 0; k < K; ++k) q[(size_t)n * K + k] = (uint8_t)orc_e4m3_encode(w[(size_t)n * K + k] / s);
+    }
+}

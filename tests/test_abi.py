@@ -72,3 +72,22 @@ def test_errors_raise_value_error_in_python():
         _lib.check(_lib.GDN_ERR_SHAPE)
     with pytest.raises(_lib.GdnError):
         _lib.check(_lib.GDN_ERR_HIP)
+
+
+def test_weight_format_checks():
+    L = _lib.lib()
+    h = ctypes.c_void_p()
+    w = _lib.GdnWeights(*([1] * 9))  # never dereferenced: the format is checked before the weights
+    assert L.gdn_layer_create_ex(ctypes.byref(_dims()), ctypes.byref(w), 1, 1, 7, ctypes.byref(h)) == \
+        _lib.GDN_ERR_INVALID_ARG
+    assert h.value is None and b"weight format" in L.gdn_last_error()
+    assert L.gdn_stack_create_ex(ctypes.byref(_dims()), ctypes.byref(w), 2, 0, None, 1, 1, -1, ctypes.byref(h)) == \
+        _lib.GDN_ERR_INVALID_ARG
+    assert L.gdn_layer_weight_format(None) == _lib.GDN_ERR_INVALID_ARG
+    p = ctypes.c_void_p(16)
+    assert L.gdn_quantize_fp8(None, 4, 64, p, p, None) == _lib.GDN_ERR_INVALID_ARG
+    assert L.gdn_quantize_fp8(p, 0, 64, p, p, None) == _lib.GDN_ERR_SHAPE
+    assert _lib.weight_format("fp8") == _lib.GDN_WEIGHTS_FP8_E4M3 == _lib.weight_format("FP8_E4M3")
+    assert _lib.weight_format("bf16") == _lib.GDN_WEIGHTS_BF16
+    with pytest.raises(ValueError):
+        _lib.weight_format("bfp4")
