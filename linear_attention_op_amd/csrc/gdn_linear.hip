@@ -91,29 +91,58 @@ __device__ __forceinline__ u32x4 ldw8(const u8* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
-// Sum of the NW waves' partial tiles through LDS and one coalesced write of rows [n0, n0 + 16 NTS):
-// C element i of lane (r, g) in acc[t][mt] is w row n0 + 16 t + 4 g + i, x row 16 mt + r.  A non-NULL
-// `scale` multiplies row n of w's results by scale[n].
+// LDS floats of the cross-wave sum below: the upper half of the waves adds into the lower half first, so
+// NW / 2 partial tiles are stored at once.
+template <int NTS, int MT, int NW>
+constexpr int gemv_red_floats() {
+    return (NW > 1 ? NW / 2 : 1) * MT * 16 * (NTS * 16 + 1);
+}
+
+// Sum of the NW waves' partial tiles through LDS (`red`: gemv_red_floats() floats) and one coalesced
+// write of rows [n0, n0 + 16 NTS): C element i of lane (r, g) in acc[t][mt] is w row n0 + 16 t + 4 g + i,
+// x row 16 mt + r.  A non-NULL `scale` multiplies row n of w's results by scale[n].
 template <int NTS, int MT, int NW, int OUT>
-__device__ __forceinline__ void gemv_finish(const f32x4 (&acc)[NTS][MT], float (*red)[MT * 16][NTS * 16 + 1],
-                                            int M, int N, void* __restrict__ y, int ldy, int n0,
-                                            const float* __restrict__ scale) {
-    constexpr int BN = NTS * 16, BM = MT * 16;
+__device__ __forceinline__ void gemv_finish(f32x4 (&acc)[NTS][MT], float* red_lds, int M, int N,
+                                            void* __restrict__ y, int ldy, int n0, const float* __restrict__ scale) {
+    constexpr int BN = NTS * 16, BM = MT * 16, LD = BN + 1, HALF = NW > 1 ? NW / 2 : 1;
+    float(*red)[BM][LD] = reinterpret_cast<float(*)[BM][LD]>(red_lds);
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
+    if (NW > 1) {
+        if (wave >= HALF) {
 #pragma unroll
-    for (int t = 0; t < NTS; ++t)
+            for (int t = 0; t < NTS; ++t)
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
+                for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) red[wave][16 * mt + r][16 * t + 4 * g + i] = acc[t][mt][i];
+                    for (int i = 0; i < 4; ++i) red[wave - HALF][16 * mt + r][16 * t + 4 * g + i] = acc[t][mt][i];
+        }
+        __syncthreads();
+        if (wave < HALF) {
+#pragma unroll
+            for (int t = 0; t < NTS; ++t)
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) acc[t][mt][i] += red[wave][16 * mt + r][16 * t + 4 * g + i];
+        }
+        __syncthreads();
+    }
+    if (wave < HALF) {
+#pragma unroll
+        for (int t = 0; t < NTS; ++t)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) red[wave][16 * mt + r][16 * t + 4 * g + i] = acc[t][mt][i];
+    }
     __syncthreads();
     for (int e = threadIdx.x; e < BM * BN; e += NW * 64) {
         const int m = e / BN, nl = e % BN, n = n0 + nl;
         if (m >= M || n >= N) continue;
         float s = 0.f;
 #pragma unroll
-        for (int wv = 0; wv < NW; ++wv) s += red[wv][m][nl];
+        for (int wv = 0; wv < HALF; ++wv) s += red[wv][m][nl];
         if (scale) s *= scale[n];
         store_out<OUT>(y, (size_t)m * ldy + n, s);
     }
@@ -123,9 +152,7 @@ __device__ __forceinline__ void gemv_finish(const f32x4 (&acc)[NTS][MT], float (
 // [kqb, kqb + kqn) of 32, written to y[m * ldy + n] (the partial sum of that K range).
 template <int NTS, int MT, int NW, int PD, int OUT, int WL, int XL>
 __device__ __forceinline__ void gemv_block(const u16* __restrict__ x, const u16* __restrict__ w, int M, int N, int K,
-                                           void* __restrict__ y, int ldy, int n0, int kqb, int kqn) {
-    constexpr int BN = NTS * 16, BM = MT * 16;
-    __shared__ float red[NW][BM][BN + 1];
+                                           void* __restrict__ y, int ldy, int n0, int kqb, int kqn, float* red) {
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
@@ -206,9 +233,7 @@ __device__ __forceinline__ void gemv_block(const u16* __restrict__ x, const u16*
 template <int NTS, int MT, int NW, int PD, int OUT, int XL>
 __device__ __forceinline__ void gemv_block_f8(const u16* __restrict__ x, const u8* __restrict__ w,
                                               const float* __restrict__ scale, int M, int N, int K,
-                                              void* __restrict__ y, int ldy, int n0, int kpb, int kpn) {
-    constexpr int BN = NTS * 16, BM = MT * 16;
-    __shared__ float red[NW][BM][BN + 1];
+                                              void* __restrict__ y, int ldy, int n0, int kpb, int kpn, float* red) {
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
@@ -291,12 +316,13 @@ template <int NTS, int MT, int NW, int PD, int OUT, int WL, int XL>
 __global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x, const void* __restrict__ w,
                                                       const float* __restrict__ scale, int M, int N, int K,
                                                       void* __restrict__ y, int ldy) {
+    __shared__ float red[gemv_red_floats<NTS, MT, NW>()];
     if constexpr (WL == W_F8)
         gemv_block_f8<NTS, MT, NW, PD, OUT, XL>(x, (const u8*)w, scale, M, N, K, y, ldy, blockIdx.x * NTS * 16, 0,
-                                                K >> 6);
+                                                K >> 6, red);
     else
         gemv_block<NTS, MT, NW, PD, OUT, WL, XL>(x, (const u16*)w, M, N, K, y, ldy, blockIdx.x * NTS * 16, 0,
-                                                 K >> 5);
+                                                 K >> 5, red);
 }
 
 // Decode in_proj (fragment-layout weights and activations, fp32 out), balanced over the CUs: workgroups
@@ -310,20 +336,23 @@ __global__ __launch_bounds__(NW * 64) void in_proj_decode_kernel(const u16* __re
                                                                 const u16* __restrict__ w2, int M, int N1, int N2,
                                                                 int K, int G, int KS, float* __restrict__ P, int ldp,
                                                                 float* __restrict__ Pab) {
+    // one LDS buffer for both kinds of workgroup, so that the split workgroups fit beside the others
+    constexpr int R1 = gemv_red_floats<NTS, MT, NW>(), R2 = gemv_red_floats<1, MT, NW>();
+    __shared__ float red[R1 > R2 ? R1 : R2];
     const int bid = blockIdx.x;
     if (bid < G) {
         if constexpr (WL == W_F8)
             gemv_block_f8<NTS, MT, NW, PD, OUT_F32, W_FRAG>(x, (const u8*)w, scale, M, N1, K, P, ldp, bid * NTS * 16,
-                                                           0, K >> 6);
+                                                           0, K >> 6, red);
         else
             gemv_block<NTS, MT, NW, PD, OUT_F32, W_FRAG, W_FRAG>(x, (const u16*)w, M, N1, K, P, ldp, bid * NTS * 16,
-                                                                0, K >> 5);
+                                                                0, K >> 5, red);
     } else {
         const int e = bid - G, nt = e % ((N2 + 15) >> 4), ks = e / ((N2 + 15) >> 4);
         const int KQ = K >> 5, per = (KQ + KS - 1) / KS;
         const int kqb = min(KQ, ks * per), kqn = min(KQ, kqb + per) - kqb;
         gemv_block<1, MT, NW, PD, OUT_F32, W_FRAG, W_FRAG>(x, w2, M, N2, K, Pab + (size_t)ks * M * N2, N2, nt * 16,
-                                                          kqb, kqn);
+                                                          kqb, kqn, red);
     }
 }
 
@@ -681,7 +710,7 @@ struct LinArgs {
 
 template <int NTS, int MT, int NW, int WL, int XL>
 hipError_t gemv(const LinArgs& a, hipStream_t stream) {
-    constexpr int PD = 4;
+    constexpr int PD = WL == W_F8 ? 2 : 4;  // an E4M3 ring slot covers two k-steps
     const dim3 grid((a.N + NTS * 16 - 1) / (NTS * 16));
     const dim3 block(NW * 64);
     if (a.out_kind == OUT_F32)
@@ -784,9 +813,12 @@ struct DecodeArgs {
     float* Pab;
 };
 
+// 8 waves per workgroup (two per SIMD) with a two-deep ring.  Measured on the 9B shape at M = 64 (with
+// the split a|b workgroups): bf16 23.6 us against 23.9 us for 4 waves and a four-deep ring (bf16 needs
+// <= 128 VGPRs so that the split workgroups can run beside the others), E4M3 18.8 us.
 template <int NTS, int MT, int WL>
 void in_proj_decode_launch(const DecodeArgs& a, hipStream_t stream) {
-    constexpr int PD = 4, NW = 4;
+    constexpr int NW = 8, PD = 2;
     const dim3 grid(a.G + ((a.N2 + 15) >> 4) * a.KS), block(NW * 64);
     hipLaunchKernelGGL((in_proj_decode_kernel<NTS, MT, NW, PD, WL>), grid, block, 0, stream, a.x, a.w, a.scale, a.w2,
                        a.M, a.N1, a.N2, a.K, a.G, a.KS, a.P, a.ldp, a.Pab);

@@ -171,7 +171,9 @@ def test_fused_and_split_paths_agree(layer08):
     torch.cuda.synchronize()
     assert rel(out_a, out_b) < 2e-3
     assert rel(a.get_recurrent_state(), b.get_recurrent_state()) < 1e-5
-    assert torch.equal(a.get_conv_state(), b.get_conv_state())
+    # the history holds projection outputs; the decode in_proj splits K over more waves than the per-op
+    # projection, so the fp32 sums differ in the last bits
+    assert rel(a.get_conv_state(), b.get_conv_state()) < 1e-6
 
 
 def test_slot_indirection(layer08):
