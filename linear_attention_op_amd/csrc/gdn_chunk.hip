@@ -42,22 +42,20 @@ __device__ __forceinline__ void load8(const float* p, float* v) {
     v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
 }
 
-// The key tile is stored split, as bf16 hi and lo planes (x = hi + lo), which the state pass feeds to
-// the MFMAs without converting; W and Q' are fp32, split by the state pass.
+// The state pass's operands, written by the prep pass split into bf16 hi + lo (x = hi + lo) and in the
+// exact per-lane order of the state pass's MFMA operands, so that the state pass loads each lane's
+// fragment with one 16-byte access and converts nothing (lane = 16 grp + m):
 struct ChunkWs {
-    float* W;   // [B, Hv, NC, CK, dk]
-    float* Q;   // [B, Hv, NC, CK, dk]   Q'
-    u16* Kh;    // [B, Hv, NC, dk, CK]   normalised keys, transposed, scaled by e^{G_last - G}
-    u16* Kl;
-    float* U;   // [B, Hv, NC, CK, dv]
+    u16* Wf;    // [B, Hv, NC][4 rt][8 w][64 lane][8]: W[16 rt + m][16 w + 4 grp + j], hi j < 4, then lo
+    u16* Qf;    // the same for Q'
+    u16* Kf;    // [B, Hv, NC][8 w][2 s][64 lane][16]: Kt[16 w + m][32 s + 8 grp + j], hi j < 8, then lo
+    float* Ut;  // [B, Hv, NC][DV][CK]   U, transposed
     float* G;   // [B, Hv, NC, CK]       G (in-chunk cumulative log decay)
     int NC;     // chunks per sequence
 };
 
-__device__ __forceinline__ void split_store(u16* hi, u16* lo, size_t i, float x) {
-    const u16 h = f2bf(x);
-    hi[i] = h;
-    lo[i] = f2bf(x - bf2f(h));
+__device__ __forceinline__ uint32_t bf16_bits(float x) {
+    return (uint32_t)__builtin_bit_cast(u16, (__bf16)x);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -85,7 +83,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
     __shared__ __attribute__((aligned(16))) float sLA[2 * CK * LDT];     // queries, then L | Aqk (M2)
     __shared__ __attribute__((aligned(16))) float sT[CK * LDT];          // T
     __shared__ __attribute__((aligned(16))) float sX[4][16 * LDX];       // per-wave 16 x 16 scratch
-    __shared__ float sG[CK], sEG[CK], sBeta[CK];
+    __shared__ float sG[CK], sEG[CK], sDec[CK], sBeta[CK];
     float* sQ = sLA;                 // [CK][LDK] fits in the 2 * CK * LDT floats of sLA
     float* sL = sLA;                 // [CK][LDT]
     float* sA = sLA + CK * LDT;      // [CK][LDT]
@@ -139,18 +137,17 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
         }
         sG[lane] = gv;
         sEG[lane] = __expf(gv);
+        sDec[lane] = __expf(__shfl(gv, CK - 1, 64) - gv);
         sBeta[lane] = bv;
     }
     __syncthreads();
 
     // ---- 2. k k^T and q k^T: wave w owns row tile w, column tiles <= w ------------------------------
-    // the queries this wave needs later for Q' (rows 16 w + 4 grp + i, columns 16 n + m) are read now,
-    // before sQ is overwritten
-    float qe[DK / 16][4];
+    // the queries this wave needs later for Q' (token 16 w + m, columns 16 n + 4 grp + i: the C layout of
+    // the transposed product below) are read now, before sQ is overwritten
+    float4 qe[DK / 16];
 #pragma unroll
-    for (int n = 0; n < DK / 16; ++n)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) qe[n][i] = sQ[(16 * wave + 4 * grp + i) * LDK + 16 * n + m];
+    for (int n = 0; n < DK / 16; ++n) qe[n] = *reinterpret_cast<const float4*>(&sQ[(16 * wave + m) * LDK + 16 * n + 4 * grp]);
     {
         const int mi = wave;
         f32x4 akk[4], aqk[4];
@@ -288,9 +285,13 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
         At[s] = split8(tv);
         Am[s] = split8(mv);
     }
-    float* Ub = ws.U + hc * CK * DV;
-    const size_t wq0 = hc * CK * DK, kt0 = hc * DK * CK;
-    const float glast = sG[CK - 1];
+    float* Ut = ws.Ut + hc * DV * CK;
+    u16* Wf = ws.Wf + hc * CK * DK * 2;
+    u16* Qf = ws.Qf + hc * CK * DK * 2;
+    // 5. W and Q' as transposed products (X^T T^T and X^T M2^T: the operands of [T; M2] X swapped), whose
+    //    C layout is the state pass's A-operand layout: lane (m, grp) holds W[16 mi + m][16 n + 4 grp + i]
+    const float egm = sEG[16 * mi + m];
+    const bool tok_ok = 16 * mi + m < len;
 #pragma unroll 1
     for (int n = 0; n < 8; ++n) {
         const int col = 16 * n + m;
@@ -305,20 +306,43 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
                 xb[jj] = sK[tk * LDK + col] * sBeta[tk] * sEG[tk];
             }
             const Split8 X = split8(xb);
-            accT = mfma3(At[s], X, accT);
-            accM = mfma3(Am[s], X, accM);
+            accT = mfma3(X, At[s], accT);
+            accM = mfma3(X, Am[s], accM);
         }
+        const float qv[4] = {qe[n].x, qe[n].y, qe[n].z, qe[n].w};
+        u16x8 fw, fq;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int r = 16 * mi + 4 * grp + i;
-            ws.W[wq0 + (size_t)r * DK + col] = accT[i];
-            ws.Q[wq0 + (size_t)r * DK + col] = r < len ? qe[n][i] * sEG[r] - accM[i] : 0.f;
+            const float wv = accT[i];
+            const float qq = tok_ok ? qv[i] * egm - accM[i] : 0.f;
+            const __bf16 wh = (__bf16)wv, qh = (__bf16)qq;
+            fw[i] = __builtin_bit_cast(u16, wh);
+            fw[4 + i] = (u16)bf16_bits(wv - (float)wh);
+            fq[i] = __builtin_bit_cast(u16, qh);
+            fq[4 + i] = (u16)bf16_bits(qq - (float)qh);
         }
+        const size_t f = ((size_t)(mi * 8 + n) * 64 + lane) * 8;
+        *reinterpret_cast<u16x8*>(Wf + f) = fw;
+        *reinterpret_cast<u16x8*>(Qf + f) = fq;
     }
-    // transposed, decay-scaled keys for the state pass: Kt[r][tok] = k[tok][r] e^{G_last - G_tok}
-    for (int e = tid; e < DK * CK; e += 256) {
-        const int r = e / CK, tok = e % CK;
-        split_store(ws.Kh, ws.Kl, kt0 + e, sK[tok * LDK + r] * __expf(glast - sG[tok]));
+    // transposed, decay-scaled keys Kt[r][tok] = k[tok][r] e^{G_last - G_tok} in the update's A-operand
+    // order: unit u = (w, s, lane) holds Kt[16 w + m][32 s + 8 grp + j], j < 8
+    {
+        u16* Kf = ws.Kf + hc * DK * CK * 2;
+        for (int u = tid; u < 8 * 2 * 64; u += 256) {
+            const int ln = u & 63, s = (u >> 6) & 1, w = u >> 7;
+            const int r = 16 * w + (ln & 15), tb = 32 * s + 8 * (ln >> 4);
+            u16x8 hi, lo;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float x = sK[(tb + j) * LDK + r] * sDec[tb + j];
+                const __bf16 xh = (__bf16)x;
+                hi[j] = __builtin_bit_cast(u16, xh);
+                lo[j] = (u16)bf16_bits(x - (float)xh);
+            }
+            *reinterpret_cast<u16x8*>(Kf + (size_t)u * 16) = hi;
+            *reinterpret_cast<u16x8*>(Kf + (size_t)u * 16 + 8) = lo;
+        }
     }
     // beta V replaces the keys
     __syncthreads();
@@ -330,6 +354,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
             make_float4(vr[j].x * bt, vr[j].y * bt, vr[j].z * bt, vr[j].w * bt);
     }
     __syncthreads();
+    // 6. U = T (beta V), stored transposed (lane (m, grp): tokens 16 mi + 4 grp + i of column 16 n + m, one
+    //    16-byte store), and the intra-chunk output M2 (beta V) into o
 #pragma unroll 1
     for (int n = 0; n < 8; ++n) {
         const int col = 16 * n + m;
@@ -344,10 +370,10 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
             accT = mfma3(At[s], X, accT);
             accM = mfma3(Am[s], X, accM);
         }
+        *reinterpret_cast<f32x4*>(Ut + (size_t)col * CK + 16 * mi + 4 * grp) = accT;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = 16 * mi + 4 * grp + i;
-            Ub[r * DV + col] = accT[i];
             if (r < len) a.o[((row0 + r) * Hv + h) * DV + col] = accM[i];
         }
     }
@@ -385,20 +411,29 @@ __device__ __forceinline__ f32x4 mfma3k16(const Split4& a, const Split4& b, f32x
 
 // One chunk's operands for one lane (about 50 VGPRs, so three chunks fit in registers).
 struct StateOps {
-    f32x4 w[4];           // W  [16 rt + m][16 wave + 4 grp + j]
-    f32x4 q[4];           // Q' at the same place
-    bf16x8 kh[2], kl[2];  // key tile [16 wave + m][32 s + 8 grp + j] (hi / lo)
+    u16x8 w[4];           // W [16 rt + m][16 wave + 4 grp + j]: hi j < 4, then lo
+    u16x8 q[4];           // Q' at the same place
+    u16x8 kh[2], kl[2];   // Kt [16 wave + m][32 s + 8 grp + j] (hi / lo)
     float glast;          // G of the chunk's last token
-    float2 u;             // U[tk][n0 + c2 ..]
-    float2 o;             // intra-chunk output at the same place
+    float2 u;             // U[2 p + e][n0 + col], e < 2
+    float2 o;             // intra-chunk output at the same places
 };
+
+__device__ __forceinline__ Split4 frag4(const u16x8 v) {
+    Split4 r;
+    r.h = __builtin_bit_cast(s16x4, __builtin_shufflevector(v, v, 0, 1, 2, 3));
+    r.l = __builtin_bit_cast(s16x4, __builtin_shufflevector(v, v, 4, 5, 6, 7));
+    return r;
+}
 
 template <int DK, int DV>
 __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs ws) {
     static_assert(DK == 128 && DV == 128, "chunked path is specialised for 128-wide heads");
-    constexpr int NWV = 8, VP = 17;
-    __shared__ __attribute__((aligned(16))) float red[NWV][2][CK][16];  // per-wave partials of W S, Q' S
-    __shared__ float vn[CK][VP];                                       // Vn for this column block
+    constexpr int NWV = 8, RS = CK + 4;
+    // per-wave partials of W S and Q' S, [column][token] (a lane's four tokens are one 16-byte store)
+    __shared__ __attribute__((aligned(16))) float red[NWV][2][16][RS];
+    // Vn split into bf16 hi | lo, in the update's B-operand order: token t at [t / 32][(t / 8) % 4][col][t % 8]
+    __shared__ __attribute__((aligned(16))) u16 vnf[2][4][16][16];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int Hv = a.Hv, T = a.T;
@@ -407,7 +442,7 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
     const int slot = a.slot_ids ? a.slot_ids[b] : b;
     const int m = lane & 15, grp = lane >> 4;
     const int NC = (T + CK - 1) / CK;
-    const int tk = tid >> 3, c2 = 2 * (tid & 7);  // Vn / output elements of this thread
+    const int col = tid & 15, p = tid >> 4;  // Vn / output elements of this thread: tokens 2p, 2p + 1
 
     // This wave's 16 state rows 16 w + 4 grp + i (i < 4), column n0 + m: the C layout of the 16x16 MFMA,
     // so the update accumulates in place.  As the B operand of W S (16x16x16: k-slot j of lane (m, grp)
@@ -421,23 +456,23 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
         const size_t hc = ((size_t)b * Hv + h) * ws.NC + c;
         const int t0 = c * CK, len = min(CK, T - t0);
         const size_t row0 = (size_t)b * T + t0;
-        const size_t wq = hc * CK * DK + 16 * wave + 4 * grp;
+        const size_t f = hc * CK * DK * 2 + ((size_t)wave * 64 + lane) * 8;
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
-            const size_t e = wq + (size_t)(16 * rt + m) * DK;
-            op.w[rt] = *reinterpret_cast<const f32x4*>(ws.W + e);
-            op.q[rt] = *reinterpret_cast<const f32x4*>(ws.Q + e);
+            op.w[rt] = *reinterpret_cast<const u16x8*>(ws.Wf + f + (size_t)rt * 8 * 64 * 8);
+            op.q[rt] = *reinterpret_cast<const u16x8*>(ws.Qf + f + (size_t)rt * 8 * 64 * 8);
         }
-        const size_t kt = hc * DK * CK + (size_t)(16 * wave + m) * CK + 8 * grp;
+        const size_t kf = hc * DK * CK * 2 + ((size_t)wave * 2 * 64 + lane) * 16;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            op.kh[s] = *reinterpret_cast<const bf16x8*>(ws.Kh + kt + 32 * s);
-            op.kl[s] = *reinterpret_cast<const bf16x8*>(ws.Kl + kt + 32 * s);
+            op.kh[s] = *reinterpret_cast<const u16x8*>(ws.Kf + kf + (size_t)s * 64 * 16);
+            op.kl[s] = *reinterpret_cast<const u16x8*>(ws.Kf + kf + (size_t)s * 64 * 16 + 8);
         }
         op.glast = ws.G[hc * CK + CK - 1];
-        op.u = *reinterpret_cast<const float2*>(ws.U + hc * CK * DV + (size_t)tk * DV + n0 + c2);
+        op.u = *reinterpret_cast<const float2*>(ws.Ut + hc * DV * CK + (size_t)(n0 + col) * CK + 2 * p);
         // rows past the end of a partial chunk read a valid row (the value is not used): no branch
-        op.o = *reinterpret_cast<const float2*>(a.o + ((row0 + min(tk, len - 1)) * Hv + h) * DV + n0 + c2);
+        op.o.x = a.o[((row0 + min(2 * p, len - 1)) * Hv + h) * DV + n0 + col];
+        op.o.y = a.o[((row0 + min(2 * p + 1, len - 1)) * Hv + h) * DV + n0 + col];
     };
 
     // FULL: the chunk has CK tokens (no per-token bounds test)
@@ -451,31 +486,32 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
 #pragma unroll
         for (int rt = 0; rt < 4; ++rt) {
             const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-            const f32x4 pw = mfma3k16(split4(cur.w[rt]), Sb, z);
-            const f32x4 pq = mfma3k16(split4(cur.q[rt]), Sb, z);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                red[wave][0][16 * rt + 4 * grp + i][m] = pw[i];
-                red[wave][1][16 * rt + 4 * grp + i][m] = pq[i];
-            }
+            const f32x4 pw = mfma3k16(frag4(cur.w[rt]), Sb, z);
+            const f32x4 pq = mfma3k16(frag4(cur.q[rt]), Sb, z);
+            *reinterpret_cast<f32x4*>(&red[wave][0][m][16 * rt + 4 * grp]) = pw;
+            *reinterpret_cast<f32x4*>(&red[wave][1][m][16 * rt + 4 * grp]) = pq;
         }
         lds_barrier();
 
-        // Vn = U - W S and O += Q' S for token tk, columns c2, c2 + 1
+        // Vn = U - W S and O += Q' S for tokens 2p, 2p + 1 of column n0 + col
         {
             float2 sw = make_float2(0.f, 0.f), sq = sw;
 #pragma unroll
             for (int w = 0; w < NWV; ++w) {
-                const float2 x = *reinterpret_cast<const float2*>(&red[w][0][tk][c2]);
-                const float2 y = *reinterpret_cast<const float2*>(&red[w][1][tk][c2]);
+                const float2 x = *reinterpret_cast<const float2*>(&red[w][0][col][2 * p]);
+                const float2 y = *reinterpret_cast<const float2*>(&red[w][1][col][2 * p]);
                 sw.x += x.x, sw.y += x.y;
                 sq.x += y.x, sq.y += y.y;
             }
-            vn[tk][c2] = cur.u.x - sw.x;
-            vn[tk][c2 + 1] = cur.u.y - sw.y;
-            if (FULL || tk < len)
-                *reinterpret_cast<float2*>(a.o + ((row0 + tk) * Hv + h) * DV + n0 + c2) =
-                    make_float2(cur.o.x + sq.x, cur.o.y + sq.y);
+            const float v0 = cur.u.x - sw.x, v1 = cur.u.y - sw.y;
+            const __bf16 h0 = (__bf16)v0, h1 = (__bf16)v1;
+            const int t = 2 * p;
+            u16* vp = &vnf[t >> 5][(t >> 3) & 3][col][t & 7];
+            *reinterpret_cast<uint32_t*>(vp) = bf16_bits((float)h0) | (bf16_bits((float)h1) << 16);
+            *reinterpret_cast<uint32_t*>(vp + 8) = bf16_bits(v0 - (float)h0) | (bf16_bits(v1 - (float)h1) << 16);
+            float* op = a.o + ((row0 + t) * Hv + h) * DV + n0 + col;
+            if (FULL || t < len) op[0] = cur.o.x + sq.x;
+            if (FULL || t + 1 < len) op[(size_t)Hv * DV] = cur.o.y + sq.y;
         }
         lds_barrier();
 
@@ -485,10 +521,11 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
         for (int i = 0; i < 4; ++i) st[i] *= egl;
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-            float vb[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) vb[j] = vn[32 * s + 8 * grp + j][m];
-            st = mfma3(Split8{cur.kh[s], cur.kl[s]}, split8(vb), st);
+            const u16x8 vh = *reinterpret_cast<const u16x8*>(&vnf[s][grp][m][0]);
+            const u16x8 vl = *reinterpret_cast<const u16x8*>(&vnf[s][grp][m][8]);
+            const Split8 kt{__builtin_bit_cast(bf16x8, cur.kh[s]), __builtin_bit_cast(bf16x8, cur.kl[s])};
+            const Split8 vs{__builtin_bit_cast(bf16x8, vh), __builtin_bit_cast(bf16x8, vl)};
+            st = mfma3(kt, vs, st);
         }
     };
 
@@ -528,7 +565,7 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
 
 size_t delta_chunked_workspace(int B, int T, int Hv, int dk, int dv) {
     const size_t NC = (size_t)(T + CK - 1) / CK;
-    // W, Q': fp32; keys: hi + lo bf16 (= 4 bytes per value); U, G: fp32
+    // W, Q', keys: bf16 hi + lo (4 bytes per value); U, G: fp32
     return (size_t)B * Hv * NC * ((size_t)CK * dk * 3 + (size_t)CK * dv + CK) * sizeof(float);
 }
 
@@ -542,14 +579,12 @@ hipError_t launch_delta_chunked(const DeltaArgs& a, int dk, int dv, void* worksp
     ChunkWs ws;
     ws.NC = (a.T + CK - 1) / CK;
     const size_t n = (size_t)a.B * a.Hv * ws.NC;
-    float* f = static_cast<float*>(workspace);
-    ws.W = f, f += n * CK * dk;
-    ws.Q = f, f += n * CK * dk;
-    u16* p = reinterpret_cast<u16*>(f);
-    ws.Kh = p, p += n * CK * dk;
-    ws.Kl = p, p += n * CK * dk;
-    f = reinterpret_cast<float*>(p);
-    ws.U = f, f += n * CK * dv;
+    u16* p = static_cast<u16*>(workspace);
+    ws.Wf = p, p += n * CK * dk * 2;
+    ws.Qf = p, p += n * CK * dk * 2;
+    ws.Kf = p, p += n * CK * dk * 2;
+    float* f = reinterpret_cast<float*>(p);
+    ws.Ut = f, f += n * CK * dv;
     ws.G = f;
     hipLaunchKernelGGL((chunk_prep_kernel<128, 128>), dim3(ws.NC, a.Hv, a.B), dim3(256), 0, stream, a, ws);
     hipError_t e = hipGetLastError();
