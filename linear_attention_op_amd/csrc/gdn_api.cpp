@@ -227,14 +227,20 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, u16* o
             f.conv_state = L->conv;
             f.qn = L->qn + r0 * Kd, f.kn = L->kn + r0 * Kd, f.v = L->v + r0 * Vd;
             f.g = L->g + r0 * nv, f.beta = L->beta + r0 * nv;
-            HIP_OK(gdn::launch_conv_front(f, st));
-            HIP_OK(gdn::launch_conv_commit(P, L->NP, g.B, g.T, g.slots, d.num_k_heads, nv, d.head_k_dim,
-                                           d.head_v_dim, L->conv, st));
             gdn::DeltaArgs r{};
             r.q = f.qn, r.k = f.kn, r.v = f.v, r.g = f.g, r.beta = f.beta;
             r.B = g.B, r.T = g.T, r.Hk = d.num_k_heads, r.Hv = nv, r.slot_ids = g.slots;
             r.state = L->rec, r.o = L->o + r0 * Vd, r.normalize = 0, r.scale = 1.f;
-            HIP_OK(run_delta(L, r, st));
+            if (L->chunk_ws && gdn::delta_chunked_supported(d.head_k_dim, d.head_v_dim) &&
+                gdn::delta_chunked_workspace(g.B, g.T, nv, d.head_k_dim, d.head_v_dim) <= L->chunk_ws_bytes) {
+                // chunked recurrence with the front end computed inside its chunk preparation
+                HIP_OK(gdn::launch_front_chunked(f, L->conv, r, L->chunk_ws, L->chunk_ws_bytes, st));
+            } else {
+                HIP_OK(gdn::launch_conv_front(f, st));
+                HIP_OK(gdn::launch_conv_commit(P, L->NP, g.B, g.T, g.slots, d.num_k_heads, nv, d.head_k_dim,
+                                               d.head_v_dim, L->conv, st));
+                HIP_OK(run_delta(L, r, st));
+            }
             HIP_OK(gdn::launch_gated_rmsnorm(r.o, Mg, nv, d.head_v_dim, P + L->CD, L->NP, L->norm_w,
                                              d.rms_norm_eps, L->y + r0 * Vd, st));
         }

@@ -26,6 +26,7 @@
 //
 // Precision: every product that feeds the state or the output goes through split bf16 (hi + lo, three
 // MFMAs, ~2^-17 relative), so the chunked state matches the fp32 sequential rule to ~1e-5.
+#include <cmath>
 #include <type_traits>
 
 #include "gdn_common.h"
@@ -73,8 +74,8 @@ __device__ __forceinline__ uint32_t bf16_bits(float x) {
 //   5. [T; M2] x (beta K e^G): W and Q' = Q e^G - Aqk W; the transposed key tile for the state pass.
 //   6. beta V over the key tile; [T; M2] x (beta V): U and the intra-chunk output.
 // ------------------------------------------------------------------------------------------------
-template <int DK, int DV>
-__global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws) {
+template <int DK, int DV, bool FUSED>
+__global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws, FrontArgs f) {
     static_assert(DK == 128 && DV == 128, "chunked path is specialised for 128-wide heads");
     constexpr int LDK = DK + 4;  // row stride (floats) of the 64 x 128 tiles
     constexpr int LDT = CK + 4;  // row stride of the 64 x 64 tiles
@@ -89,34 +90,83 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
     float* sA = sLA + CK * LDT;      // [CK][LDT]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    // heads fastest: the v-heads that share a k-head run back to back and share its rows in L2
+    const int h = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
     const int T = a.T, Hk = a.Hk, Hv = a.Hv, kh = h / (Hv / Hk);
     const int t0 = c * CK, len = min(CK, T - t0);
     const size_t row0 = (size_t)b * T + t0;
     const int m = lane & 15, grp = lane >> 4;
     const size_t hc = ((size_t)b * Hv + h) * ws.NC + c;
 
-    // ---- 0. loads: piece e = tid + 256 j of a 64 x 128 tile is row e / 32 (= tid / 32 + 8 j), float4 e % 32
+    // ---- 0. inputs: thread (prow, pc4) owns tokens 8 prow + j (j < 8), channels pc4 .. pc4 + 3 of q, k, v
     const int prow = tid >> 5, pc4 = (tid & 31) * 4;
+    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
     float4 kr[8], qr[8], vr[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int tok = prow + 8 * j;
-        const bool ok = tok < len;
-        const size_t row = row0 + (ok ? tok : 0);
-        const size_t qk = (row * Hk + kh) * DK + pc4;
-        const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
-        kr[j] = ok ? *reinterpret_cast<const float4*>(a.k + qk) : z;
-        qr[j] = ok ? *reinterpret_cast<const float4*>(a.q + qk) : z;
-        vr[j] = ok ? *reinterpret_cast<const float4*>(a.v + (row * Hv + h) * DV + pc4) : z;
-    }
     float gv = 0.f, bv = 0.f;
-    if (wave == 0 && lane < len) gv = a.g[(row0 + lane) * Hv + h], bv = a.beta[(row0 + lane) * Hv + h];
+    if constexpr (FUSED) {
+        // The front end, from the projection rows: causal conv (4 taps over the inputs at t - 3 .. t, the
+        // slot's history before t = 0) + SiLU, as conv_front_kernel (layer_compute.cpp C1, 74-103).  The
+        // window of the thread's 8 tokens is 11 input rows; all 33 loads are issued before any use.
+        const int Kd = f.nk * DK, Vd = f.nv * DV, CD = 2 * Kd + Vd, CH = 2 * DK + DV;
+        const int slot = f.slot_ids ? f.slot_ids[b] : b;
+        const float* hq = f.conv_state + ((size_t)slot * f.nv + kh * (Hv / Hk)) * 3 * CH;  // q | k history copy
+        const float* hv = f.conv_state + ((size_t)slot * f.nv + h) * 3 * CH;
+        const int colq = kh * DK + pc4, colk = Kd + kh * DK + pc4, colv = 2 * Kd + h * DV + pc4;
+        auto in_row = [&](int tk, int col, const float* hist, int local) -> float4 {
+            if (tk >= len) return z4;
+            const int t = t0 + tk;
+            return t >= 0 ? *reinterpret_cast<const float4*>(f.P + (size_t)((long long)row0 + tk) * f.NP + col)
+                          : *reinterpret_cast<const float4*>(hist + (3 + t) * CH + local);
+        };
+        float4 xq[11], xk[11], xv[11];
+#pragma unroll
+        for (int r = 0; r < 11; ++r) {
+            const int tk = 8 * prow - 3 + r;
+            xq[r] = in_row(tk, colq, hq, pc4);
+            xk[r] = in_row(tk, colk, hq, DK + pc4);
+            xv[r] = in_row(tk, colv, hv, 2 * DK + pc4);
+        }
+        if (wave == 0 && lane < len) {
+            const float* Pr = f.P + (row0 + lane) * f.NP + CD + Vd;
+            gv = f.neg_A[h] * softplusf_(Pr[h] + f.dt_bias[h]);
+            bv = sigmoidf_(Pr[f.nv + h]);
+        }
+        auto conv8 = [&](const float4* x, int col, float4* out) {
+            float4 w[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w[i] = f.conv_w[col + i];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float4 x0 = x[j], x1 = x[j + 1], x2 = x[j + 2], x3 = x[j + 3];
+                float4 o;
+                o.x = siluf_(w[0].x * x0.x + w[0].y * x1.x + w[0].z * x2.x + w[0].w * x3.x);
+                o.y = siluf_(w[1].x * x0.y + w[1].y * x1.y + w[1].z * x2.y + w[1].w * x3.y);
+                o.z = siluf_(w[2].x * x0.z + w[2].y * x1.z + w[2].z * x2.z + w[2].w * x3.z);
+                o.w = siluf_(w[3].x * x0.w + w[3].y * x1.w + w[3].z * x2.w + w[3].w * x3.w);
+                out[j] = 8 * prow + j < len ? o : z4;
+            }
+        };
+        conv8(xk, colk, kr);
+        conv8(xq, colq, qr);
+        conv8(xv, colv, vr);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int tok = 8 * prow + j;
+            const bool ok = tok < len;
+            const size_t row = row0 + (ok ? tok : 0);
+            const size_t qk = (row * Hk + kh) * DK + pc4;
+            kr[j] = ok ? *reinterpret_cast<const float4*>(a.k + qk) : z4;
+            qr[j] = ok ? *reinterpret_cast<const float4*>(a.q + qk) : z4;
+            vr[j] = ok ? *reinterpret_cast<const float4*>(a.v + (row * Hv + h) * DV + pc4) : z4;
+        }
+        if (wave == 0 && lane < len) gv = a.g[(row0 + lane) * Hv + h], bv = a.beta[(row0 + lane) * Hv + h];
+    }
 
     // ---- 1. normalisers (the 32 lanes of a half-wave hold one row), sK, sQ, G ---------------------------
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int tok = prow + 8 * j;
+        const int tok = 8 * prow + j;
         float sk = kr[j].x * kr[j].x + kr[j].y * kr[j].y + kr[j].z * kr[j].z + kr[j].w * kr[j].w;
         float sq = qr[j].x * qr[j].x + qr[j].y * qr[j].y + qr[j].z * qr[j].z + qr[j].w * qr[j].w;
 #pragma unroll
@@ -348,7 +398,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-        const int tok = prow + 8 * j;
+        const int tok = 8 * prow + j;
         const float bt = sBeta[tok];
         *reinterpret_cast<float4*>(&sK[tok * LDK + pc4]) =
             make_float4(vr[j].x * bt, vr[j].y * bt, vr[j].z * bt, vr[j].w * bt);
@@ -563,6 +613,22 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
 
 }  // namespace
 
+// Carve the workspace of a launch (128-wide heads).
+static ChunkWs chunk_ws(const DeltaArgs& a, void* workspace) {
+    constexpr int D = 128;
+    ChunkWs ws;
+    ws.NC = (a.T + CK - 1) / CK;
+    const size_t n = (size_t)a.B * a.Hv * ws.NC;
+    u16* p = static_cast<u16*>(workspace);
+    ws.Wf = p, p += n * CK * D * 2;
+    ws.Qf = p, p += n * CK * D * 2;
+    ws.Kf = p, p += n * CK * D * 2;
+    float* f = reinterpret_cast<float*>(p);
+    ws.Ut = f, f += n * CK * D;
+    ws.G = f;
+    return ws;
+}
+
 size_t delta_chunked_workspace(int B, int T, int Hv, int dk, int dv) {
     const size_t NC = (size_t)(T + CK - 1) / CK;
     // W, Q', keys: bf16 hi + lo (4 bytes per value); U, G: fp32
@@ -576,18 +642,30 @@ hipError_t launch_delta_chunked(const DeltaArgs& a, int dk, int dv, void* worksp
     if (!delta_chunked_supported(dk, dv)) return hipErrorInvalidValue;
     if (a.B <= 0 || a.T <= 0) return hipSuccess;
     if (!workspace || ws_bytes < delta_chunked_workspace(a.B, a.T, a.Hv, dk, dv)) return hipErrorInvalidValue;
-    ChunkWs ws;
-    ws.NC = (a.T + CK - 1) / CK;
-    const size_t n = (size_t)a.B * a.Hv * ws.NC;
-    u16* p = static_cast<u16*>(workspace);
-    ws.Wf = p, p += n * CK * dk * 2;
-    ws.Qf = p, p += n * CK * dk * 2;
-    ws.Kf = p, p += n * CK * dk * 2;
-    float* f = reinterpret_cast<float*>(p);
-    ws.Ut = f, f += n * CK * dv;
-    ws.G = f;
-    hipLaunchKernelGGL((chunk_prep_kernel<128, 128>), dim3(ws.NC, a.Hv, a.B), dim3(256), 0, stream, a, ws);
+    ChunkWs ws = chunk_ws(a, workspace);
+    hipLaunchKernelGGL((chunk_prep_kernel<128, 128, false>), dim3(a.Hv, ws.NC, a.B), dim3(256), 0, stream, a, ws,
+                       FrontArgs{});
     hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((chunk_state_kernel<128, 128>), dim3(a.Hv * (128 / 16), a.B), dim3(512), 0, stream, a, ws);
+    return hipGetLastError();
+}
+
+hipError_t launch_front_chunked(const FrontArgs& f, float* conv_state, const DeltaArgs& r, void* workspace,
+                                size_t ws_bytes, hipStream_t stream) {
+    if (!delta_chunked_supported(f.dk, f.dv) || f.B != r.B || f.T != r.T) return hipErrorInvalidValue;
+    if (r.B <= 0 || r.T <= 0) return hipSuccess;
+    if (!workspace || ws_bytes < delta_chunked_workspace(r.B, r.T, r.Hv, f.dk, f.dv)) return hipErrorInvalidValue;
+    ChunkWs ws = chunk_ws(r, workspace);
+    DeltaArgs a = r;
+    a.q = a.k = a.v = a.g = a.beta = nullptr;  // computed by the prep pass
+    a.normalize = 1;
+    a.scale = 1.0f / std::sqrt((float)f.dk);
+    hipLaunchKernelGGL((chunk_prep_kernel<128, 128, true>), dim3(a.Hv, ws.NC, a.B), dim3(256), 0, stream, a, ws, f);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    // the prep pass has read the old history: roll it forward now
+    e = launch_conv_commit(f.P, f.NP, f.B, f.T, f.slot_ids, f.nk, f.nv, f.dk, f.dv, conv_state, stream);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((chunk_state_kernel<128, 128>), dim3(a.Hv * (128 / 16), a.B), dim3(512), 0, stream, a, ws);
     return hipGetLastError();

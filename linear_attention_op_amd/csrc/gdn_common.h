@@ -219,6 +219,11 @@ hipError_t launch_delta_seq(const DeltaArgs& a, int dk, int dv, hipStream_t stre
 hipError_t launch_delta_chunked(const DeltaArgs& a, int dk, int dv, void* workspace, size_t ws_bytes,
                                 hipStream_t stream);
 size_t delta_chunked_workspace(int B, int T, int Hv, int dk, int dv);
+// The same with the front end fused into the chunk preparation: q, k, v, g, beta of each chunk are computed
+// from the projection rows f.P (conv history f.conv_state, then rolled forward in conv_state), so f.qn ..
+// f.beta and r.q .. r.beta are not used; r carries B, T, heads, slots, the state and o.
+hipError_t launch_front_chunked(const FrontArgs& f, float* conv_state, const DeltaArgs& r, void* workspace,
+                                size_t ws_bytes, hipStream_t stream);
 bool delta_chunked_supported(int dk, int dv);
 
 // y = o * rsqrt(mean(o^2) + eps) * w * silu(z), per head of dv; y bf16.
