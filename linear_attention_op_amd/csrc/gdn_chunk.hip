@@ -60,19 +60,20 @@ __device__ __forceinline__ uint32_t bf16_bits(float x) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// chunk_prep_kernel: grid (NC, Hv, B), 256 threads.
+// chunk_prep_kernel: grid (Hv, NC, B), 256 threads.
 //
 // Phases (wave w of 4):
 //   0. issue the chunk's loads: keys and queries (coalesced float4) and values (kept in registers until
 //      the last phase), g, beta.
-//   1. per-token normalisers (32-lane reductions), normalised keys -> sK, queries -> sQ (aliases the
-//      L / Aqk tiles, which are not written yet), G = cumsum(g).
-//   2. k k^T and q k^T (wave w: row tile w, column tiles <= w) -> L into sL, Aqk into sA.
+//   1. per-token normalisers (32-lane reductions), normalised keys -> sK (and kept in registers),
+//      queries -> sQ (aliases the L / Aqk tiles, which are not written yet), G = cumsum(g).
+//   2. k k^T and q k^T (wave w: row tile w, column tiles <= w) -> L into sL, Aqk into sA; from the keys
+//      in registers, the state pass's key fragments and X = beta K e^G transposed and split into sK.
 //   3. T = (I + L)^-1, blocked: the four 16 x 16 diagonal blocks by forward substitution (one wave
 //      each), then T_ij = -T_ii sum_{k=j}^{i-1} L_ik T_kj by distance i - j = 1, 2, 3 -> sT.
 //   4. M2 = Aqk T in place over Aqk.
-//   5. [T; M2] x (beta K e^G): W and Q' = Q e^G - Aqk W; the transposed key tile for the state pass.
-//   6. beta V over the key tile; [T; M2] x (beta V): U and the intra-chunk output.
+//   5. T and M2 into registers; (beta V)^T split into sLA; [T; M2] x X: W and Q' = Q e^G - Aqk W.
+//   6. [T; M2] x (beta V): U and the intra-chunk output.
 // ------------------------------------------------------------------------------------------------
 template <int DK, int DV, bool FUSED>
 __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws, FrontArgs f) {
@@ -173,10 +174,10 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
         for (int off = 1; off < 32; off <<= 1) sk += __shfl_xor(sk, off, 64), sq += __shfl_xor(sq, off, 64);
         const float rk = a.normalize ? rsqrtf(sk + 1e-6f) : 1.f;
         const float rq = (a.normalize ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
-        float4 kn = kr[j], qn = qr[j];
-        kn.x *= rk, kn.y *= rk, kn.z *= rk, kn.w *= rk;
+        float4 qn = qr[j];
+        kr[j].x *= rk, kr[j].y *= rk, kr[j].z *= rk, kr[j].w *= rk;  // the normalised keys stay in registers
         qn.x *= rq, qn.y *= rq, qn.z *= rq, qn.w *= rq;
-        *reinterpret_cast<float4*>(&sK[tok * LDK + pc4]) = kn;
+        *reinterpret_cast<float4*>(&sK[tok * LDK + pc4]) = kr[j];
         *reinterpret_cast<float4*>(&sQ[tok * LDK + pc4]) = qn;
     }
     if (wave == 0) {
@@ -220,7 +221,46 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
                 aqk[ni] = mfma3(A2, Bk, aqk[ni]);
             }
         }
-        __syncthreads();  // every wave is done with sQ before L / Aqk overwrite it
+        __syncthreads();  // every wave is done with sK and sQ before they are overwritten
+        // From the normalised keys in registers (thread (prow, pc4): tokens 8 prow + j of channels pc4 + cc):
+        //  * the state pass's key fragments Kt[r][tok] = k[tok][r] e^{G_last - G_tok}, split: unit
+        //    (w, s, grp, m) with r = 16 w + m and 8 prow = 32 s + 8 grp;
+        //  * X = beta K e^G, transposed and split into bf16 hi | lo planes over sK: element (r, tok) at
+        //    r * CK + ((tok / 8) ^ (r % 8)) * 8 + tok % 8 (the xor puts the 16-byte reads of eight
+        //    consecutive rows in distinct banks).
+        {
+            u16* Kf = ws.Kf + hc * DK * CK * 2;
+            u16* XTh = reinterpret_cast<u16*>(sK);
+            u16* XTl = XTh + DK * CK;
+            float dec[8], sc[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int tok = 8 * prow + j;
+                dec[j] = sDec[tok];
+                sc[j] = sBeta[tok] * sEG[tok];
+            }
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+                const int r = pc4 + cc;
+                u16x8 kh8, kl8, xh8, xl8;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float kv = cc == 0 ? kr[j].x : (cc == 1 ? kr[j].y : (cc == 2 ? kr[j].z : kr[j].w));
+                    const float x = kv * dec[j], y = kv * sc[j];
+                    const __bf16 xh = (__bf16)x, yh = (__bf16)y;
+                    kh8[j] = __builtin_bit_cast(u16, xh);
+                    kl8[j] = (u16)bf16_bits(x - (float)xh);
+                    xh8[j] = __builtin_bit_cast(u16, yh);
+                    xl8[j] = (u16)bf16_bits(y - (float)yh);
+                }
+                const int u = ((r >> 4) * 2 + (prow >> 2)) * 64 + (prow & 3) * 16 + (r & 15);
+                *reinterpret_cast<u16x8*>(Kf + (size_t)u * 16) = kh8;
+                *reinterpret_cast<u16x8*>(Kf + (size_t)u * 16 + 8) = kl8;
+                const int xo = r * CK + ((prow ^ (r & 7)) << 3);
+                *reinterpret_cast<u16x8*>(XTh + xo) = xh8;
+                *reinterpret_cast<u16x8*>(XTl + xo) = xl8;
+            }
+        }
 #pragma unroll
         for (int ni = 0; ni < 4; ++ni)
 #pragma unroll
@@ -335,27 +375,52 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
         At[s] = split8(tv);
         Am[s] = split8(mv);
     }
-    float* Ut = ws.Ut + hc * DV * CK;
-    u16* Wf = ws.Wf + hc * CK * DK * 2;
-    u16* Qf = ws.Qf + hc * CK * DK * 2;
+    __syncthreads();  // T and M2 are in registers: sLA is free
+    // 6a. (beta V)^T split into sLA, laid out as X^T (thread (prow, pc4): tokens 8 prow + j of channels pc4 + cc)
+    const u16* XTh = reinterpret_cast<const u16*>(sK);
+    const u16* XTl = XTh + DK * CK;
+    u16* VTh = reinterpret_cast<u16*>(sLA);
+    u16* VTl = VTh + DV * CK;
+    {
+        float bt[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) bt[j] = sBeta[8 * prow + j];
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            const int r = pc4 + cc;
+            u16x8 vh8, vl8;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float vv = cc == 0 ? vr[j].x : (cc == 1 ? vr[j].y : (cc == 2 ? vr[j].z : vr[j].w));
+                const float y = vv * bt[j];
+                const __bf16 yh = (__bf16)y;
+                vh8[j] = __builtin_bit_cast(u16, yh);
+                vl8[j] = (u16)bf16_bits(y - (float)yh);
+            }
+            const int vo = r * CK + ((prow ^ (r & 7)) << 3);
+            *reinterpret_cast<u16x8*>(VTh + vo) = vh8;
+            *reinterpret_cast<u16x8*>(VTl + vo) = vl8;
+        }
+    }
+    // operand of token group (4 s + grp) for row r (16-byte reads, the xor layout above)
+    auto tfrag = [&](const u16* hp, const u16* lp, int r, int s) {
+        const int o = r * CK + (((4 * s + grp) ^ (r & 7)) << 3);
+        return Split8{*reinterpret_cast<const bf16x8*>(hp + o), *reinterpret_cast<const bf16x8*>(lp + o)};
+    };
+
     // 5. W and Q' as transposed products (X^T T^T and X^T M2^T: the operands of [T; M2] X swapped), whose
     //    C layout is the state pass's A-operand layout: lane (m, grp) holds W[16 mi + m][16 n + 4 grp + i]
+    u16* Wf = ws.Wf + hc * CK * DK * 2;
+    u16* Qf = ws.Qf + hc * CK * DK * 2;
     const float egm = sEG[16 * mi + m];
     const bool tok_ok = 16 * mi + m < len;
-#pragma unroll 1
+#pragma unroll
     for (int n = 0; n < 8; ++n) {
-        const int col = 16 * n + m;
         f32x4 accT = {0.f, 0.f, 0.f, 0.f}, accM = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             if (s >= nks) continue;
-            float xb[8];
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) {
-                const int tk = 32 * s + 8 * grp + jj;
-                xb[jj] = sK[tk * LDK + col] * sBeta[tk] * sEG[tk];
-            }
-            const Split8 X = split8(xb);
+            const Split8 X = tfrag(XTh, XTl, 16 * n + m, s);
             accT = mfma3(X, At[s], accT);
             accM = mfma3(X, Am[s], accM);
         }
@@ -371,54 +436,24 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
             fq[i] = __builtin_bit_cast(u16, qh);
             fq[4 + i] = (u16)bf16_bits(qq - (float)qh);
         }
-        const size_t f = ((size_t)(mi * 8 + n) * 64 + lane) * 8;
-        *reinterpret_cast<u16x8*>(Wf + f) = fw;
-        *reinterpret_cast<u16x8*>(Qf + f) = fq;
+        const size_t f8 = ((size_t)(mi * 8 + n) * 64 + lane) * 8;
+        *reinterpret_cast<u16x8*>(Wf + f8) = fw;
+        *reinterpret_cast<u16x8*>(Qf + f8) = fq;
     }
-    // transposed, decay-scaled keys Kt[r][tok] = k[tok][r] e^{G_last - G_tok} in the update's A-operand
-    // order: unit u = (w, s, lane) holds Kt[16 w + m][32 s + 8 grp + j], j < 8
-    {
-        u16* Kf = ws.Kf + hc * DK * CK * 2;
-        for (int u = tid; u < 8 * 2 * 64; u += 256) {
-            const int ln = u & 63, s = (u >> 6) & 1, w = u >> 7;
-            const int r = 16 * w + (ln & 15), tb = 32 * s + 8 * (ln >> 4);
-            u16x8 hi, lo;
+    __syncthreads();  // (beta V)^T is complete
+    // 6b. U = T (beta V), stored transposed (lane (m, grp): tokens 16 mi + 4 grp + i of column 16 n + m, one
+    //     16-byte store), and the intra-chunk output M2 (beta V) into o
+    float* Ut = ws.Ut + hc * DV * CK;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float x = sK[(tb + j) * LDK + r] * sDec[tb + j];
-                const __bf16 xh = (__bf16)x;
-                hi[j] = __builtin_bit_cast(u16, xh);
-                lo[j] = (u16)bf16_bits(x - (float)xh);
-            }
-            *reinterpret_cast<u16x8*>(Kf + (size_t)u * 16) = hi;
-            *reinterpret_cast<u16x8*>(Kf + (size_t)u * 16 + 8) = lo;
-        }
-    }
-    // beta V replaces the keys
-    __syncthreads();
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int tok = 8 * prow + j;
-        const float bt = sBeta[tok];
-        *reinterpret_cast<float4*>(&sK[tok * LDK + pc4]) =
-            make_float4(vr[j].x * bt, vr[j].y * bt, vr[j].z * bt, vr[j].w * bt);
-    }
-    __syncthreads();
-    // 6. U = T (beta V), stored transposed (lane (m, grp): tokens 16 mi + 4 grp + i of column 16 n + m, one
-    //    16-byte store), and the intra-chunk output M2 (beta V) into o
-#pragma unroll 1
     for (int n = 0; n < 8; ++n) {
         const int col = 16 * n + m;
         f32x4 accT = {0.f, 0.f, 0.f, 0.f}, accM = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
             if (s >= nks) continue;
-            float xb[8];
-#pragma unroll
-            for (int jj = 0; jj < 8; ++jj) xb[jj] = sK[(32 * s + 8 * grp + jj) * LDK + col];
-            const Split8 X = split8(xb);
-            accT = mfma3(At[s], X, accT);
-            accM = mfma3(Am[s], X, accM);
+            const Split8 V = tfrag(VTh, VTl, col, s);
+            accT = mfma3(At[s], V, accT);
+            accM = mfma3(Am[s], V, accM);
         }
         *reinterpret_cast<f32x4*>(Ut + (size_t)col * CK + 16 * mi + 4 * grp) = accT;
 #pragma unroll

@@ -106,8 +106,9 @@ __device__ __forceinline__ void e4m3x16_to_bf16(const u32x4 q, bf16x8& lo, bf16x
 // global loads, so loads issued for the next step stay in flight across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
-__device__ __forceinline__ float siluf_(float x) { return x / (1.0f + __expf(-x)); }
+// The reciprocals use the hardware v_rcp_f32 (1 ulp) instead of an IEEE division sequence.
+__device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+__device__ __forceinline__ float siluf_(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 // torch.nn.functional.softplus with beta = 1, threshold = 20
 __device__ __forceinline__ float softplusf_(float x) { return x > 20.0f ? x : log1pf(__expf(x)); }
 
