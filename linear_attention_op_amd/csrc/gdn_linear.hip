@@ -20,7 +20,7 @@
 //    every x load into 1 KB of contiguous memory as well.
 //  * gemm_kernel / gemm256_kernel (M > 64, prefill): LDS-tiled GEMM on v_mfma_f32_32x32x16_bf16, 128x128
 //    tiles (4 waves of 64x64, register-staged double buffering) for small problems and software-pipelined
-//    256x256 tiles (4 waves of 128x128) once there are enough tiles to fill the chip;
+//    256x256 tiles (8 waves of 128x64) once there are enough tiles to fill the chip;
 //    tiles are rasterised per XCD in groups of 8 M-tiles so that workgroups running together on one
 //    XCD share A and B tiles in its L2.
 #include "gdn_common.h"
@@ -522,14 +522,16 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
 
 
 // ------------------------------------------------------------------------------------------------
-// Large GEMM: 256 x 256 x 64 block tile, 4 waves of 128 x 128 (4 x 4 tiles of 32x32x16 MFMA, 256 fp32
-// accumulators per lane in AGPRs), software-pipelined:
+// Large GEMM: 256 x 256 x 64 block tile on 8 waves (2 along M x 4 along N) of 128 x 64 (4 x 2 tiles of
+// 32x32x16 MFMA), two waves per SIMD so that one computes while the other waits; software-pipelined:
 //  * two register staging sets: the global loads of k-tile kt + 2 are issued while tile kt is computed
 //    and tile kt + 1 (loaded one step earlier) is stored to the other LDS buffer;
 //  * LDS rows padded to 72 bf16 (conflict-free 16-byte fragment reads), double-buffered (147 KB);
 //  * in each k-tile the fragment reads of the next k-16 sub-step, the global loads and the LDS stores are
-//    threaded one by one between the 64 MFMAs (scheduling groups), and the tile ends with an LDS-only
-//    barrier, so global loads stay in flight across it.
+//    threaded between the 32 MFMAs (scheduling groups), and the tile ends with an LDS-only barrier, so
+//    global loads stay in flight across it.
+// Measured at M = 16384, K = 4096: N = 12352 1.46 ms (1.13 PFLOP/s), N = 4096 0.47 ms, against 1.81 and
+// 0.52 ms for 4 waves of 128 x 128 on the same data (same sums, bit for bit).
 // The main loop is branch-free (loads past the last k-tile re-read it); K % 128 == 0.
 // ------------------------------------------------------------------------------------------------
 constexpr int LBM = 256, LBN = 256, LBK = 64, LLD = LBK + 8;
@@ -537,14 +539,15 @@ constexpr int LBM = 256, LBN = 256, LBK = 64, LLD = LBK + 8;
 __device__ __forceinline__ int lds_off(int row, int ch) { return row * LLD + (ch << 3); }
 
 template <int OUT, int WL>
-__global__ __launch_bounds__(256, 1) void gemm256_kernel(const u16* __restrict__ x, const void* __restrict__ wv,
+__global__ __launch_bounds__(512, 1) void gemm256_kernel(const u16* __restrict__ x, const void* __restrict__ wv,
                                                          const float* __restrict__ scale, int M, int N, int K,
                                                          void* __restrict__ y, int ldy) {
     __shared__ __attribute__((aligned(16))) u16 As[2][LBM * LLD];
     __shared__ __attribute__((aligned(16))) u16 Bs[2][LBN * LLD];
+    constexpr int WNW = 4, FA = 4, FB = 2;  // waves along N; 32-row fragments per wave along M and N
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WNW, wn = wave % WNW;
 
     const int TM = (M + LBM - 1) / LBM, TN = (N + LBN - 1) / LBN, total = TM * TN;
     const int id = blockIdx.x, per = total / 8;
@@ -556,18 +559,18 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(const u16* __restrict__
     const int m0 = tm * LBM, n0 = tn * LBN;
     const int KQ = K >> 5, NT = (N + 15) >> 4;
 
-    // staging: 8 A and 8 B pieces of 16 bytes per thread and k-tile (W_F8: 4 B pieces of 16 codes, each
+    // staging: 4 A and 4 B pieces of 16 bytes per thread and k-tile (W_F8: 2 B pieces of 16 codes, each
     // widened to two bf16 pieces on the way to LDS)
-    constexpr int NB = WL == W_F8 ? 4 : 8;
+    constexpr int NB = WL == W_F8 ? 2 : 4;
     const u16* w = (const u16*)wv;
     const u8* w8 = (const u8*)wv;
-    const u16* ag[8];
-    const u16* bg[8];
-    const u8* bq[4];
-    int sa[8], sb[8];
+    const u16* ag[4];
+    const u16* bg[4];
+    const u8* bq[2];
+    int sa[4], sb[4];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int c = tid + 256 * j;
+    for (int j = 0; j < 4; ++j) {
+        const int c = tid + 512 * j;
         const int row = c >> 3, ch = c & 7;
         ag[j] = x + (size_t)min(m0 + row, M - 1) * K + ch * 8;
         sa[j] = lds_off(row, ch);
@@ -592,12 +595,12 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(const u16* __restrict__
     constexpr int BSTEP = WL == W_ROW ? LBK : 1024;
     const int nk = K / LBK;
 
-    // B staging: 8 bf16 pieces, or 4 code pieces in the first half of the same registers
-    u16x8 ra0[8], rb0[8], ra1[8], rb1[8];
+    // B staging: 4 bf16 pieces, or 2 code pieces in the first half of the same registers
+    u16x8 ra0[4], rb0[4], ra1[4], rb1[4];
     auto gload = [&](u16x8* ra, u16x8* rb, int kt) {
         const int k = min(kt, nk - 1);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) ra[j] = *reinterpret_cast<const u16x8*>(ag[j] + (size_t)k * LBK);
+        for (int j = 0; j < 4; ++j) ra[j] = *reinterpret_cast<const u16x8*>(ag[j] + (size_t)k * LBK);
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
             if constexpr (WL == W_F8)
@@ -608,7 +611,7 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(const u16* __restrict__
     };
     auto lstore = [&](const u16x8* ra, const u16x8* rb, int buf) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) *reinterpret_cast<u16x8*>(&As[buf][sa[j]]) = ra[j];
+        for (int j = 0; j < 4; ++j) *reinterpret_cast<u16x8*>(&As[buf][sa[j]]) = ra[j];
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
             if constexpr (WL == W_F8) {
@@ -622,38 +625,36 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(const u16* __restrict__
         }
     };
 
-    f32x16 acc[4][4];
+    f32x16 acc[FA][FB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < FA; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < FB; ++j)
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
     const int fr = lane & 31, fh = lane >> 5;
-    int aoff[4], boff[4];
+    int aoff[FA], boff[FB];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        aoff[i] = wm * 128 + i * 32 + fr;
-        boff[i] = wn * 128 + i * 32 + fr;
-    }
+    for (int i = 0; i < FA; ++i) aoff[i] = wm * 128 + i * 32 + fr;
+#pragma unroll
+    for (int j = 0; j < FB; ++j) boff[j] = wn * 64 + j * 32 + fr;
     auto rdfrag = [&](int buf, int s, bf16x8* a, bf16x8* b) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            a[i] = *reinterpret_cast<const bf16x8*>(&As[buf][lds_off(aoff[i], 2 * s + fh)]);
-            b[i] = *reinterpret_cast<const bf16x8*>(&Bs[buf][lds_off(boff[i], 2 * s + fh)]);
-        }
+        for (int i = 0; i < FA; ++i) a[i] = *reinterpret_cast<const bf16x8*>(&As[buf][lds_off(aoff[i], 2 * s + fh)]);
+#pragma unroll
+        for (int j = 0; j < FB; ++j) b[j] = *reinterpret_cast<const bf16x8*>(&Bs[buf][lds_off(boff[j], 2 * s + fh)]);
     };
     auto mma = [&](const bf16x8* a, const bf16x8* b) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < FA; ++i)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+            for (int j = 0; j < FB; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
     };
     // one k-tile on LDS buffer `buf`, loading tile kt_ld into (ra_ld, rb_ld) and storing (ra_st, rb_st)
     // into the other buffer
     auto tile = [&](int buf, u16x8* ra_ld, u16x8* rb_ld, const u16x8* ra_st, const u16x8* rb_st, int kt_ld) {
-        bf16x8 a0[4], b0[4], a1[4], b1[4];
+        bf16x8 a0[FA], b0[FB], a1[FA], b1[FB];
         rdfrag(buf, 0, a0, b0);
         rdfrag(buf, 1, a1, b1);
         gload(ra_ld, rb_ld, kt_ld);
@@ -664,18 +665,18 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(const u16* __restrict__
         lstore(ra_st, rb_st, buf ^ 1);
         mma(a0, b0);
         mma(a1, b1);
-        // 8 fragment reads up front; then per k-16 sub-step 16 MFMAs, each of the first 8 followed by a
-        // fragment read (sub-steps 0-2), the last 8 by two global loads (0-1) or an LDS store (2); in
-        // sub-step 3 the first 8 by an LDS store
-        __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);
+        // 6 fragment reads up front; per k-16 sub-step 8 MFMAs, the first 6 each followed by a fragment
+        // read (sub-steps 0-2), the last two by two global loads (sub-steps 0-1) or an LDS store (sub-step
+        // 2); in sub-step 3 the first six by an LDS store
+        __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
         for (int ss = 0; ss < 4; ++ss)
-            for (int m = 0; m < 16; ++m) {
+            for (int m = 0; m < 8; ++m) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                if (ss < 3 && m < 8)
+                if (ss < 3 && m < 6)
                     __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
                 else if (ss < 2)
                     __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);
-                else if ((ss == 2 && m >= 8) || (ss == 3 && m < 8))
+                else if ((ss == 2 && m >= 6) || (ss == 3 && m < 6))
                     __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);
             }
         lds_barrier();
@@ -691,10 +692,10 @@ __global__ __launch_bounds__(256, 1) void gemm256_kernel(const u16* __restrict__
     }
 
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < FA; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
-            store_tile32<OUT>(acc[i][j], m0 + wm * 128 + i * 32, n0 + wn * 128 + j * 32 + (lane & 31), M, N, y, ldy,
+        for (int j = 0; j < FB; ++j)
+            store_tile32<OUT>(acc[i][j], m0 + wm * 128 + i * 32, n0 + wn * 64 + j * 32 + (lane & 31), M, N, y, ldy,
                               WL == W_F8 ? scale : nullptr);
 }
 
@@ -759,10 +760,10 @@ hipError_t linear_wl(const LinArgs& a, int xlayout, hipStream_t stream) {
     if ((size_t)a.M * a.N >= (size_t)256 * 256 * 256) {  // >= one round of 256 x 256 tiles over the CUs
         const dim3 grid(((a.M + LBM - 1) / LBM) * ((a.N + LBN - 1) / LBN));
         if (a.out_kind == OUT_F32)
-            hipLaunchKernelGGL((gemm256_kernel<OUT_F32, WL>), grid, dim3(256), 0, stream, x, a.w, a.scale, a.M, a.N,
+            hipLaunchKernelGGL((gemm256_kernel<OUT_F32, WL>), grid, dim3(512), 0, stream, x, a.w, a.scale, a.M, a.N,
                                a.K, a.y, a.ldy);
         else
-            hipLaunchKernelGGL((gemm256_kernel<OUT_BF16, WL>), grid, dim3(256), 0, stream, x, a.w, a.scale, a.M,
+            hipLaunchKernelGGL((gemm256_kernel<OUT_BF16, WL>), grid, dim3(512), 0, stream, x, a.w, a.scale, a.M,
                                a.N, a.K, a.y, a.ldy);
         return hipGetLastError();
     }
