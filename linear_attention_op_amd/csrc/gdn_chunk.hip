@@ -60,37 +60,41 @@ __device__ __forceinline__ uint32_t bf16_bits(float x) {
 }
 
 // ------------------------------------------------------------------------------------------------
-// chunk_prep_kernel: grid (Hv, NC, B), 256 threads.
+// chunk_prep_kernel: grid (Hv, NC, B), 512 threads (8 waves, two per SIMD).
 //
-// Phases (wave w of 4):
-//   0. issue the chunk's loads: keys and queries (coalesced float4) and values (kept in registers until
-//      the last phase), g, beta.
+// Phases (wave w of 8; mi = w % 4 is a 16-token row tile, hf = w / 4 a half of the column tiles):
+//   0. the chunk's inputs: thread (prow, pc4) owns tokens 4 prow .. 4 prow + 3, channels pc4 .. pc4 + 3 of
+//      q, k, v (coalesced float4; in the layer computed by the fused front end), g, beta.
 //   1. per-token normalisers (32-lane reductions), normalised keys -> sK (and kept in registers),
 //      queries -> sQ (aliases the L / Aqk tiles, which are not written yet), G = cumsum(g).
-//   2. k k^T and q k^T (wave w: row tile w, column tiles <= w) -> L into sL, Aqk into sA; from the keys
-//      in registers, the state pass's key fragments and X = beta K e^G transposed and split into sK.
+//   2. k k^T and q k^T (wave w: row tile mi, column tiles 2 hf, 2 hf + 1 at or below it) -> L into sL,
+//      Aqk into sA; from the keys in registers, the state pass's key fragments and X = beta K e^G
+//      transposed and split into sK.
 //   3. T = (I + L)^-1, blocked: the four 16 x 16 diagonal blocks by forward substitution (one wave
 //      each), then T_ij = -T_ii sum_{k=j}^{i-1} L_ik T_kj by distance i - j = 1, 2, 3 -> sT.
 //   4. M2 = Aqk T in place over Aqk.
-//   5. T and M2 into registers; (beta V)^T split into sLA; [T; M2] x X: W and Q' = Q e^G - Aqk W.
+//   5. T and M2 into registers; (beta V)^T split into sLA; [T; M2] x X: W and Q' = Q e^G - Aqk W
+//      (wave w: row tile mi, column tiles 4 hf .. 4 hf + 3).
 //   6. [T; M2] x (beta V): U and the intra-chunk output.
 // ------------------------------------------------------------------------------------------------
 template <int DK, int DV, bool FUSED>
-__global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws, FrontArgs f) {
+__global__ __launch_bounds__(512) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws, FrontArgs f) {
     static_assert(DK == 128 && DV == 128, "chunked path is specialised for 128-wide heads");
+    constexpr int NT = 512;      // threads
     constexpr int LDK = DK + 4;  // row stride (floats) of the 64 x 128 tiles
     constexpr int LDT = CK + 4;  // row stride of the 64 x 64 tiles
     constexpr int LDX = 17;      // row stride of the 16 x 16 scratch blocks
-    __shared__ __attribute__((aligned(16))) float sK[CK * LDK];          // keys, then beta V
-    __shared__ __attribute__((aligned(16))) float sLA[2 * CK * LDT];     // queries, then L | Aqk (M2)
+    __shared__ __attribute__((aligned(16))) float sK[CK * LDK];          // keys, then X^T split
+    __shared__ __attribute__((aligned(16))) float sLA[2 * CK * LDT];     // queries, then L | Aqk (M2), then (beta V)^T
     __shared__ __attribute__((aligned(16))) float sT[CK * LDT];          // T
-    __shared__ __attribute__((aligned(16))) float sX[4][16 * LDX];       // per-wave 16 x 16 scratch
+    __shared__ __attribute__((aligned(16))) float sX[4][16 * LDX];       // per-wave 16 x 16 scratch (phase 3)
     __shared__ float sG[CK], sEG[CK], sDec[CK], sBeta[CK];
     float* sQ = sLA;                 // [CK][LDK] fits in the 2 * CK * LDT floats of sLA
     float* sL = sLA;                 // [CK][LDT]
     float* sA = sLA + CK * LDT;      // [CK][LDT]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int mi = wave & 3, hf = wave >> 2;
     // heads fastest: the v-heads that share a k-head run back to back and share its rows in L2
     const int h = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
     const int T = a.T, Hk = a.Hk, Hv = a.Hv, kh = h / (Hv / Hk);
@@ -99,15 +103,15 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
     const int m = lane & 15, grp = lane >> 4;
     const size_t hc = ((size_t)b * Hv + h) * ws.NC + c;
 
-    // ---- 0. inputs: thread (prow, pc4) owns tokens 8 prow + j (j < 8), channels pc4 .. pc4 + 3 of q, k, v
+    // ---- 0. inputs: thread (prow, pc4) owns tokens 4 prow + j (j < 4), channels pc4 .. pc4 + 3 of q, k, v
     const int prow = tid >> 5, pc4 = (tid & 31) * 4;
     const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 kr[8], qr[8], vr[8];
+    float4 kr[4], qr[4], vr[4];
     float gv = 0.f, bv = 0.f;
     if constexpr (FUSED) {
         // The front end, from the projection rows: causal conv (4 taps over the inputs at t - 3 .. t, the
         // slot's history before t = 0) + SiLU, as conv_front_kernel (layer_compute.cpp C1, 74-103).  The
-        // window of the thread's 8 tokens is 11 input rows; all 33 loads are issued before any use.
+        // window of the thread's 4 tokens is 7 input rows; all 21 loads are issued before any use.
         const int Kd = f.nk * DK, Vd = f.nv * DV, CD = 2 * Kd + Vd, CH = 2 * DK + DV;
         const int slot = f.slot_ids ? f.slot_ids[b] : b;
         const float* hq = f.conv_state + ((size_t)slot * f.nv + kh * (Hv / Hk)) * 3 * CH;  // q | k history copy
@@ -119,10 +123,10 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
             return t >= 0 ? *reinterpret_cast<const float4*>(f.P + (size_t)((long long)row0 + tk) * f.NP + col)
                           : *reinterpret_cast<const float4*>(hist + (3 + t) * CH + local);
         };
-        float4 xq[11], xk[11], xv[11];
+        float4 xq[7], xk[7], xv[7];
 #pragma unroll
-        for (int r = 0; r < 11; ++r) {
-            const int tk = 8 * prow - 3 + r;
+        for (int r = 0; r < 7; ++r) {
+            const int tk = 4 * prow - 3 + r;
             xq[r] = in_row(tk, colq, hq, pc4);
             xk[r] = in_row(tk, colk, hq, DK + pc4);
             xv[r] = in_row(tk, colv, hv, 2 * DK + pc4);
@@ -132,28 +136,28 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
             gv = f.neg_A[h] * softplusf_(Pr[h] + f.dt_bias[h]);
             bv = sigmoidf_(Pr[f.nv + h]);
         }
-        auto conv8 = [&](const float4* x, int col, float4* out) {
+        auto conv4 = [&](const float4* x, int col, float4* out) {
             float4 w[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) w[i] = f.conv_w[col + i];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
+            for (int j = 0; j < 4; ++j) {
                 const float4 x0 = x[j], x1 = x[j + 1], x2 = x[j + 2], x3 = x[j + 3];
                 float4 o;
                 o.x = siluf_(w[0].x * x0.x + w[0].y * x1.x + w[0].z * x2.x + w[0].w * x3.x);
                 o.y = siluf_(w[1].x * x0.y + w[1].y * x1.y + w[1].z * x2.y + w[1].w * x3.y);
                 o.z = siluf_(w[2].x * x0.z + w[2].y * x1.z + w[2].z * x2.z + w[2].w * x3.z);
                 o.w = siluf_(w[3].x * x0.w + w[3].y * x1.w + w[3].z * x2.w + w[3].w * x3.w);
-                out[j] = 8 * prow + j < len ? o : z4;
+                out[j] = 4 * prow + j < len ? o : z4;
             }
         };
-        conv8(xk, colk, kr);
-        conv8(xq, colq, qr);
-        conv8(xv, colv, vr);
+        conv4(xk, colk, kr);
+        conv4(xq, colq, qr);
+        conv4(xv, colv, vr);
     } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            const int tok = 8 * prow + j;
+        for (int j = 0; j < 4; ++j) {
+            const int tok = 4 * prow + j;
             const bool ok = tok < len;
             const size_t row = row0 + (ok ? tok : 0);
             const size_t qk = (row * Hk + kh) * DK + pc4;
@@ -166,8 +170,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
 
     // ---- 1. normalisers (the 32 lanes of a half-wave hold one row), sK, sQ, G ---------------------------
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int tok = 8 * prow + j;
+    for (int j = 0; j < 4; ++j) {
+        const int tok = 4 * prow + j;
         float sk = kr[j].x * kr[j].x + kr[j].y * kr[j].y + kr[j].z * kr[j].z + kr[j].w * kr[j].w;
         float sq = qr[j].x * qr[j].x + qr[j].y * qr[j].y + qr[j].z * qr[j].z + qr[j].w * qr[j].w;
 #pragma unroll
@@ -193,38 +197,42 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
     }
     __syncthreads();
 
-    // ---- 2. k k^T and q k^T: wave w owns row tile w, column tiles <= w ------------------------------
-    // the queries this wave needs later for Q' (token 16 w + m, columns 16 n + 4 grp + i: the C layout of
-    // the transposed product below) are read now, before sQ is overwritten
-    float4 qe[DK / 16];
+    // ---- 2. k k^T and q k^T: wave w owns row tile mi, column tiles 2 hf, 2 hf + 1 -----------------------
+    // the queries this wave needs later for Q' (token 16 mi + m, columns 16 n + 4 grp + i for its column tiles
+    // n = 4 hf .. 4 hf + 3: the C layout of the transposed product below) are read now, before sQ is overwritten
+    float4 qe[4];
 #pragma unroll
-    for (int n = 0; n < DK / 16; ++n) qe[n] = *reinterpret_cast<const float4*>(&sQ[(16 * wave + m) * LDK + 16 * n + 4 * grp]);
+    for (int n = 0; n < 4; ++n)
+        qe[n] = *reinterpret_cast<const float4*>(&sQ[(16 * mi + m) * LDK + 16 * (4 * hf + n) + 4 * grp]);
     {
-        const int mi = wave;
-        f32x4 akk[4], aqk[4];
+        f32x4 akk[2], aqk[2];
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) akk[ni] = aqk[ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < 2; ++q) akk[q] = aqk[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (2 * hf <= mi) {
 #pragma unroll
-        for (int s = 0; s < DK / 32; ++s) {
-            const int k0 = 32 * s + 8 * grp;
-            float ka[8], qa[8];
-            load8(&sK[(16 * mi + m) * LDK + k0], ka);
-            load8(&sQ[(16 * mi + m) * LDK + k0], qa);
-            const Split8 A1 = split8(ka), A2 = split8(qa);
+            for (int s = 0; s < DK / 32; ++s) {
+                const int k0 = 32 * s + 8 * grp;
+                float ka[8], qa[8];
+                load8(&sK[(16 * mi + m) * LDK + k0], ka);
+                load8(&sQ[(16 * mi + m) * LDK + k0], qa);
+                const Split8 A1 = split8(ka), A2 = split8(qa);
 #pragma unroll
-            for (int ni = 0; ni < 4; ++ni) {
-                if (ni > mi) continue;
-                float kb[8];
-                load8(&sK[(16 * ni + m) * LDK + k0], kb);
-                const Split8 Bk = split8(kb);
-                akk[ni] = mfma3(A1, Bk, akk[ni]);
-                aqk[ni] = mfma3(A2, Bk, aqk[ni]);
+                for (int q = 0; q < 2; ++q) {
+                    const int ni = 2 * hf + q;
+                    if (ni > mi) continue;
+                    float kb[8];
+                    load8(&sK[(16 * ni + m) * LDK + k0], kb);
+                    const Split8 Bk = split8(kb);
+                    akk[q] = mfma3(A1, Bk, akk[q]);
+                    aqk[q] = mfma3(A2, Bk, aqk[q]);
+                }
             }
         }
         __syncthreads();  // every wave is done with sK and sQ before they are overwritten
-        // From the normalised keys in registers (thread (prow, pc4): tokens 8 prow + j of channels pc4 + cc):
+        // From the normalised keys in registers (thread (prow, pc4): tokens 4 prow + j of channels pc4 + cc,
+        // half `prow % 2` of the 8-token group prow / 2):
         //  * the state pass's key fragments Kt[r][tok] = k[tok][r] e^{G_last - G_tok}, split: unit
-        //    (w, s, grp, m) with r = 16 w + m and 8 prow = 32 s + 8 grp;
+        //    (w, s, grp, m) with r = 16 w + m and 8-token group 4 s + grp;
         //  * X = beta K e^G, transposed and split into bf16 hi | lo planes over sK: element (r, tok) at
         //    r * CK + ((tok / 8) ^ (r % 8)) * 8 + tok % 8 (the xor puts the 16-byte reads of eight
         //    consecutive rows in distinct banks).
@@ -232,45 +240,47 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
             u16* Kf = ws.Kf + hc * DK * CK * 2;
             u16* XTh = reinterpret_cast<u16*>(sK);
             u16* XTl = XTh + DK * CK;
-            float dec[8], sc[8];
+            const int tg = prow >> 1, half = (prow & 1) * 4;
+            float dec[4], sc[4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int tok = 8 * prow + j;
+            for (int j = 0; j < 4; ++j) {
+                const int tok = 4 * prow + j;
                 dec[j] = sDec[tok];
                 sc[j] = sBeta[tok] * sEG[tok];
             }
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc) {
                 const int r = pc4 + cc;
-                u16x8 kh8, kl8, xh8, xl8;
+                u16x4 kh4, kl4, xh4, xl4;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
+                for (int j = 0; j < 4; ++j) {
                     const float kv = cc == 0 ? kr[j].x : (cc == 1 ? kr[j].y : (cc == 2 ? kr[j].z : kr[j].w));
                     const float x = kv * dec[j], y = kv * sc[j];
                     const __bf16 xh = (__bf16)x, yh = (__bf16)y;
-                    kh8[j] = __builtin_bit_cast(u16, xh);
-                    kl8[j] = (u16)bf16_bits(x - (float)xh);
-                    xh8[j] = __builtin_bit_cast(u16, yh);
-                    xl8[j] = (u16)bf16_bits(y - (float)yh);
+                    kh4[j] = __builtin_bit_cast(u16, xh);
+                    kl4[j] = (u16)bf16_bits(x - (float)xh);
+                    xh4[j] = __builtin_bit_cast(u16, yh);
+                    xl4[j] = (u16)bf16_bits(y - (float)yh);
                 }
-                const int u = ((r >> 4) * 2 + (prow >> 2)) * 64 + (prow & 3) * 16 + (r & 15);
-                *reinterpret_cast<u16x8*>(Kf + (size_t)u * 16) = kh8;
-                *reinterpret_cast<u16x8*>(Kf + (size_t)u * 16 + 8) = kl8;
-                const int xo = r * CK + ((prow ^ (r & 7)) << 3);
-                *reinterpret_cast<u16x8*>(XTh + xo) = xh8;
-                *reinterpret_cast<u16x8*>(XTl + xo) = xl8;
+                const int u = ((r >> 4) * 2 + (tg >> 2)) * 64 + (tg & 3) * 16 + (r & 15);
+                *reinterpret_cast<u16x4*>(Kf + (size_t)u * 16 + half) = kh4;
+                *reinterpret_cast<u16x4*>(Kf + (size_t)u * 16 + 8 + half) = kl4;
+                const int xo = r * CK + ((tg ^ (r & 7)) << 3) + half;
+                *reinterpret_cast<u16x4*>(XTh + xo) = xh4;
+                *reinterpret_cast<u16x4*>(XTl + xo) = xl4;
             }
         }
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni)
+        for (int q = 0; q < 2; ++q)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
+                const int ni = 2 * hf + q;
                 const int r = 16 * mi + 4 * grp + i, cc = 16 * ni + m;
                 float L = 0.f, A = 0.f;
                 if (ni <= mi && cc <= r) {
                     const float dec = __expf(sG[r] - sG[cc]);
-                    A = aqk[ni][i] * dec;
-                    if (cc < r) L = sBeta[r] * akk[ni][i] * dec;
+                    A = aqk[q][i] * dec;
+                    if (cc < r) L = sBeta[r] * akk[q][i] * dec;
                 }
                 sL[r * LDT + cc] = L;
                 sA[r * LDT + cc] = A;
@@ -279,8 +289,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
     __syncthreads();
 
     // ---- 3. T = (I + L)^-1 ---------------------------------------------------------------------------
-    // 3a. diagonal block w: lane c < 16 owns column c, rows by forward substitution
-    if (lane < 16) {
+    // 3a. diagonal block w (waves 0-3): lane c < 16 owns column c, rows by forward substitution
+    if (wave < 4 && lane < 16) {
         const int o = 16 * wave;
         float t[16];
 #pragma unroll
@@ -294,13 +304,13 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
         for (int r = 0; r < 16; ++r) sT[(o + r) * LDT + o + lane] = t[r];
     }
     // upper blocks of T are zero
-    for (int e = tid; e < CK * CK; e += 256) {
+    for (int e = tid; e < CK * CK; e += NT) {
         const int r = e / CK, cc = e % CK;
         if ((cc >> 4) > (r >> 4)) sT[r * LDT + cc] = 0.f;
     }
     __syncthreads();
-    // 3b. T_ij = -T_ii X, X = sum_{k=j}^{i-1} L_ik T_kj.  Lane (r4, cc) = (lane / 16, lane % 16) makes
-    //     rows 4 r4 .. 4 r4 + 3 of column cc of the block.
+    // 3b. T_ij = -T_ii X, X = sum_{k=j}^{i-1} L_ik T_kj (wave j).  Lane (r4, cc) = (lane / 16, lane % 16)
+    //     makes rows 4 r4 .. 4 r4 + 3 of column cc of the block.
 #pragma unroll
     for (int dist = 1; dist < 4; ++dist) {
         const int j = wave, i = wave + dist;
@@ -331,39 +341,43 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
         __syncthreads();
     }
 
-    // ---- 4. M2 = Aqk T, in place over Aqk (wave w reads and writes only its own row tile) ----------------
+    // ---- 4. M2 = Aqk T, in place over Aqk: wave w makes tiles (mi, 2 hf), (mi, 2 hf + 1) at or below the
+    //      diagonal (tiles above it stay zero); both waves of a row tile read all of it first --------------
     {
-        const int mi = wave;
-        f32x4 acc[4];
+        f32x4 acc[2];
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) acc[ni] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int q = 0; q < 2; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (2 * hf <= mi) {
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            if (32 * s > 16 * mi + 15) continue;  // Aqk row tile mi is zero past column 16 mi + 15
-            const int k0 = 32 * s + 8 * grp;
-            float av[8];
-            load8(&sA[(16 * mi + m) * LDT + k0], av);
-            const Split8 A = split8(av);
+            for (int s = 0; s < 2; ++s) {
+                if (32 * s > 16 * mi + 15) continue;  // Aqk row tile mi is zero past column 16 mi + 15
+                const int k0 = 32 * s + 8 * grp;
+                float av[8];
+                load8(&sA[(16 * mi + m) * LDT + k0], av);
+                const Split8 A = split8(av);
 #pragma unroll
-            for (int ni = 0; ni < 4; ++ni) {
-                if (ni > mi || 32 * s + 31 < 16 * ni) continue;  // T column tile ni is zero above row 16 ni
-                float tb[8];
+                for (int q = 0; q < 2; ++q) {
+                    const int ni = 2 * hf + q;
+                    if (ni > mi || 32 * s + 31 < 16 * ni) continue;  // T column tile ni is zero above row 16 ni
+                    float tb[8];
 #pragma unroll
-                for (int jj = 0; jj < 8; ++jj) tb[jj] = sT[(k0 + jj) * LDT + 16 * ni + m];
-                acc[ni] = mfma3(A, split8(tb), acc[ni]);
+                    for (int jj = 0; jj < 8; ++jj) tb[jj] = sT[(k0 + jj) * LDT + 16 * ni + m];
+                    acc[q] = mfma3(A, split8(tb), acc[q]);
+                }
             }
         }
+        __syncthreads();
 #pragma unroll
-        for (int ni = 0; ni < 4; ++ni) {
+        for (int q = 0; q < 2; ++q) {
+            const int ni = 2 * hf + q;
             if (ni > mi) continue;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) sA[(16 * mi + 4 * grp + i) * LDT + 16 * ni + m] = acc[ni][i];
+            for (int i = 0; i < 4; ++i) sA[(16 * mi + 4 * grp + i) * LDT + 16 * ni + m] = acc[q][i];
         }
     }
     __syncthreads();
 
     // ---- 5, 6. [T; M2] x (beta K e^G | beta V) -----------------------------------------------------------
-    const int mi = wave;
     const int nks = (16 * mi + 15 >= 32) ? 2 : 1;  // row tile mi of T and M2 is zero past column 16 mi + 15
     Split8 At[2], Am[2];
 #pragma unroll
@@ -376,30 +390,31 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
         Am[s] = split8(mv);
     }
     __syncthreads();  // T and M2 are in registers: sLA is free
-    // 6a. (beta V)^T split into sLA, laid out as X^T (thread (prow, pc4): tokens 8 prow + j of channels pc4 + cc)
+    // 6a. (beta V)^T split into sLA, laid out as X^T (thread (prow, pc4): tokens 4 prow + j of channels pc4 + cc)
     const u16* XTh = reinterpret_cast<const u16*>(sK);
     const u16* XTl = XTh + DK * CK;
     u16* VTh = reinterpret_cast<u16*>(sLA);
     u16* VTl = VTh + DV * CK;
     {
-        float bt[8];
+        const int tg = prow >> 1, half = (prow & 1) * 4;
+        float bt[4];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) bt[j] = sBeta[8 * prow + j];
+        for (int j = 0; j < 4; ++j) bt[j] = sBeta[4 * prow + j];
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
             const int r = pc4 + cc;
-            u16x8 vh8, vl8;
+            u16x4 vh4, vl4;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
+            for (int j = 0; j < 4; ++j) {
                 const float vv = cc == 0 ? vr[j].x : (cc == 1 ? vr[j].y : (cc == 2 ? vr[j].z : vr[j].w));
                 const float y = vv * bt[j];
                 const __bf16 yh = (__bf16)y;
-                vh8[j] = __builtin_bit_cast(u16, yh);
-                vl8[j] = (u16)bf16_bits(y - (float)yh);
+                vh4[j] = __builtin_bit_cast(u16, yh);
+                vl4[j] = (u16)bf16_bits(y - (float)yh);
             }
-            const int vo = r * CK + ((prow ^ (r & 7)) << 3);
-            *reinterpret_cast<u16x8*>(VTh + vo) = vh8;
-            *reinterpret_cast<u16x8*>(VTl + vo) = vl8;
+            const int vo = r * CK + ((tg ^ (r & 7)) << 3) + half;
+            *reinterpret_cast<u16x4*>(VTh + vo) = vh4;
+            *reinterpret_cast<u16x4*>(VTl + vo) = vl4;
         }
     }
     // operand of token group (4 s + grp) for row r (16-byte reads, the xor layout above)
@@ -415,7 +430,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
     const float egm = sEG[16 * mi + m];
     const bool tok_ok = 16 * mi + m < len;
 #pragma unroll
-    for (int n = 0; n < 8; ++n) {
+    for (int nn = 0; nn < 4; ++nn) {
+        const int n = 4 * hf + nn;
         f32x4 accT = {0.f, 0.f, 0.f, 0.f}, accM = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
@@ -424,7 +440,7 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
             accT = mfma3(X, At[s], accT);
             accM = mfma3(X, Am[s], accM);
         }
-        const float qv[4] = {qe[n].x, qe[n].y, qe[n].z, qe[n].w};
+        const float qv[4] = {qe[nn].x, qe[nn].y, qe[nn].z, qe[nn].w};
         u16x8 fw, fq;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -445,8 +461,8 @@ __global__ __launch_bounds__(256) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
     //     16-byte store), and the intra-chunk output M2 (beta V) into o
     float* Ut = ws.Ut + hc * DV * CK;
 #pragma unroll
-    for (int n = 0; n < 8; ++n) {
-        const int col = 16 * n + m;
+    for (int nn = 0; nn < 4; ++nn) {
+        const int col = 16 * (4 * hf + nn) + m;
         f32x4 accT = {0.f, 0.f, 0.f, 0.f}, accM = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
@@ -678,7 +694,7 @@ hipError_t launch_delta_chunked(const DeltaArgs& a, int dk, int dv, void* worksp
     if (a.B <= 0 || a.T <= 0) return hipSuccess;
     if (!workspace || ws_bytes < delta_chunked_workspace(a.B, a.T, a.Hv, dk, dv)) return hipErrorInvalidValue;
     ChunkWs ws = chunk_ws(a, workspace);
-    hipLaunchKernelGGL((chunk_prep_kernel<128, 128, false>), dim3(a.Hv, ws.NC, a.B), dim3(256), 0, stream, a, ws,
+    hipLaunchKernelGGL((chunk_prep_kernel<128, 128, false>), dim3(a.Hv, ws.NC, a.B), dim3(512), 0, stream, a, ws,
                        FrontArgs{});
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -696,7 +712,7 @@ hipError_t launch_front_chunked(const FrontArgs& f, float* conv_state, const Del
     a.q = a.k = a.v = a.g = a.beta = nullptr;  // computed by the prep pass
     a.normalize = 1;
     a.scale = 1.0f / std::sqrt((float)f.dk);
-    hipLaunchKernelGGL((chunk_prep_kernel<128, 128, true>), dim3(a.Hv, ws.NC, a.B), dim3(256), 0, stream, a, ws, f);
+    hipLaunchKernelGGL((chunk_prep_kernel<128, 128, true>), dim3(a.Hv, ws.NC, a.B), dim3(512), 0, stream, a, ws, f);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // the prep pass has read the old history: roll it forward now
