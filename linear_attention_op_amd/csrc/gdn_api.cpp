@@ -153,10 +153,15 @@ bool fp8(const gdn_layer* L) { return L->wfmt == GDN_WEIGHTS_FP8_E4M3; }
 
 // in_proj of M rows (x row-major, or W_FRAG for M <= 64) into P [M, NP] (9B/gdn_layer.py:255-259).  FP8
 // layers run the q | k | v | z rows on E4M3 weights and the a | b rows on bf16 ones.
+// Prefill-sized launches take the q | k | v | z rows (a multiple of 256 at the model shapes, so whole
+// 256-wide GEMM tiles) and the a | b rows as two GEMMs: one partial column of 256-wide tiles would cost a
+// full round of workgroups for 64 useful columns.
 hipError_t in_proj_rows(const gdn_layer* L, const void* x, int xl, int M, float* P, hipStream_t st) {
     const int H = L->d.hidden, N1 = L->CD + L->Vd, nab = 2 * L->d.num_v_heads;
-    if (!fp8(L)) return gdn::launch_linear(x, xl, L->w_in, gdn::W_FRAG, nullptr, M, L->NP, H, P, L->NP, gdn::OUT_F32, st);
-    hipError_t e = gdn::launch_linear(x, xl, L->w_in8, gdn::W_F8, L->s_in, M, N1, H, P, L->NP, gdn::OUT_F32, st);
+    if (!fp8(L) && M <= 64)
+        return gdn::launch_linear(x, xl, L->w_in, gdn::W_FRAG, nullptr, M, L->NP, H, P, L->NP, gdn::OUT_F32, st);
+    hipError_t e = fp8(L) ? gdn::launch_linear(x, xl, L->w_in8, gdn::W_F8, L->s_in, M, N1, H, P, L->NP, gdn::OUT_F32, st)
+                          : gdn::launch_linear(x, xl, L->w_in, gdn::W_FRAG, nullptr, M, N1, H, P, L->NP, gdn::OUT_F32, st);
     if (e != hipSuccess) return e;
     return gdn::launch_linear(x, xl, L->w_ab, gdn::W_FRAG, nullptr, M, nab, H, P + N1, L->NP, gdn::OUT_F32, st);
 }
