@@ -347,9 +347,50 @@ __global__ __launch_bounds__(256) void gated_rmsnorm_kernel(const float* __restr
     }
 }
 
+// The same with 16-byte accesses: a head's dv values are dv / 4 consecutive lanes (one float4 each), its
+// sum of squares a shuffle over those lanes; o is read once, y written as 8-byte pieces.
+template <int DV>
+__global__ __launch_bounds__(256) void gated_rmsnorm4_kernel(const float* __restrict__ o, int Vd,
+                                                             const float* __restrict__ z, int z_stride,
+                                                             const float* __restrict__ w, float eps,
+                                                             u16* __restrict__ y) {
+    constexpr int TPH = DV / 4;  // lanes per head
+    const int m = blockIdx.x, t = threadIdx.x;
+    const float* orow = o + (size_t)m * Vd;
+    const float* zrow = z + (size_t)m * z_stride;
+    u16* yrow = y + (size_t)m * Vd;
+    const float4 wv = *reinterpret_cast<const float4*>(w + (t % TPH) * 4);
+    for (int e = 4 * t; e < Vd; e += 1024) {  // whole heads per round: Vd % dv == 0
+        const float4 ov = *reinterpret_cast<const float4*>(orow + e);
+        const float4 zv = *reinterpret_cast<const float4*>(zrow + e);
+        float ss = ov.x * ov.x + ov.y * ov.y + ov.z * ov.z + ov.w * ov.w;
+#pragma unroll
+        for (int off = 1; off < TPH; off <<= 1) ss += __shfl_xor(ss, off, 64);
+        const float rstd = rsqrtf(ss / (float)DV + eps);
+        const float y0 = ov.x * rstd * wv.x * siluf_(zv.x), y1 = ov.y * rstd * wv.y * siluf_(zv.y);
+        const float y2 = ov.z * rstd * wv.z * siluf_(zv.z), y3 = ov.w * rstd * wv.w * siluf_(zv.w);
+        uint2 pk;
+        pk.x = (uint32_t)__builtin_bit_cast(u16, (__bf16)y0) | ((uint32_t)__builtin_bit_cast(u16, (__bf16)y1) << 16);
+        pk.y = (uint32_t)__builtin_bit_cast(u16, (__bf16)y2) | ((uint32_t)__builtin_bit_cast(u16, (__bf16)y3) << 16);
+        *reinterpret_cast<uint2*>(yrow + e) = pk;
+    }
+}
+
 hipError_t launch_gated_rmsnorm(const float* o, int M, int nv, int dv, const float* z, int z_stride,
                                 const float* w, float eps, u16* y, hipStream_t stream) {
     if (M <= 0) return hipSuccess;
+    const bool vec = z_stride % 4 == 0 && ((uintptr_t)z & 15) == 0 && ((uintptr_t)o & 15) == 0 &&
+                     ((uintptr_t)y & 7) == 0 && ((uintptr_t)w & 15) == 0 && (dv == 32 || dv == 64 || dv == 128);
+    if (vec) {
+        const int Vd = nv * dv;
+        if (dv == 128)
+            hipLaunchKernelGGL(gated_rmsnorm4_kernel<128>, dim3(M), dim3(256), 0, stream, o, Vd, z, z_stride, w, eps, y);
+        else if (dv == 64)
+            hipLaunchKernelGGL(gated_rmsnorm4_kernel<64>, dim3(M), dim3(256), 0, stream, o, Vd, z, z_stride, w, eps, y);
+        else
+            hipLaunchKernelGGL(gated_rmsnorm4_kernel<32>, dim3(M), dim3(256), 0, stream, o, Vd, z, z_stride, w, eps, y);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(gated_rmsnorm_kernel, dim3(M), dim3(256), 0, stream, o, nv, dv, z, z_stride, w, eps, y);
     return hipGetLastError();
 }
