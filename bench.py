@@ -188,6 +188,54 @@ def measure_traffic(kernel="mixer_kernel", timeout=180):
     return {"bytes": out["FETCH_SIZE"]["bytes"] + out["WRITE_SIZE"]["bytes"], "passes": out}, None
 
 
+def small_batch_decode(shape, B, copies=8, steps=400, warmup=40):
+    """Decode latency of one layer at a small batch, one HIP graph per layer copy (launch overhead is most
+    of such a step), rotating over `copies` layers so that the weights come from HBM."""
+    import torch
+
+    from linear_attention_op_amd import Qwen35GatedDeltaNetHIP
+    from linear_attention_op_amd import synthetic as syn
+
+    d = syn.SHAPES[shape]
+    dev = torch.device("cuda", 0)
+    w0, _ = syn.make_weights(d, seed=0)
+    layers, xin = [], []
+    for i in range(copies):
+        gg = torch.Generator(device=dev).manual_seed(200 + i)
+        w = {k: (torch.randn(v.shape, generator=gg, device=dev) * v.float().std()).to(v.dtype)
+             if k.startswith("w_") or k == "conv_w" else v for k, v in w0.items()}
+        lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B, max_tokens=64)
+        lay.set_state(rec=torch.randn(B, d["num_v_heads"], d["head_k_dim"], d["head_v_dim"], device=dev) * 0.01)
+        layers.append(lay)
+        xin.append(torch.randn(B, 1, d["hidden"], device=dev).to(torch.bfloat16))
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for lay, x in zip(layers, xin):
+            lay(x)
+    torch.cuda.current_stream().wait_stream(side)
+    graphs = []
+    for lay, x in zip(layers, xin):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            lay(x)
+        graphs.append(g)
+    for i in range(warmup):
+        graphs[i % copies].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        graphs[i % copies].replay()
+    torch.cuda.synchronize()
+    us = (time.perf_counter() - t0) / steps * 1e6
+    W, s = decode_bytes(d, B)
+    out = {"shape": shape, "batch": B, "us_per_step": us, "tok_per_s": B / (us * 1e-6),
+           "hbm_frac": (W + B * s) / (us * 1e-6) / HBM_PEAK, "mode": "HIP graph per step"}
+    for lay in layers:
+        lay.close()
+    return out
+
+
 def stack_bench(d, n_layers=24, n_prefill=8, prefill_len=2048, n_decode=56, steps=3, warmup=1, seed=4):
     """Continuous batching through a stack of 9B-shape layers with the decoder RMSNorm between layers:
     every step carries the next prefill_len tokens of n_prefill prompts (chunked prefill, states carried)
@@ -263,6 +311,7 @@ def main():
                     help="1: replay the decode step from HIP graphs; 0: launch eagerly (faster here: 104 vs 112 us)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fp8", action="store_true", help="skip the FP8-weight decode measurement")
+    ap.add_argument("--no-small", action="store_true", help="skip the batch-1/8 decode latencies")
     ap.add_argument("--stack", action="store_true",
                     help="also run the 24-layer continuous-batching stack (8 x 2048 prefill + 56 decode per step)")
     ap.add_argument("--no-traffic", action="store_true",
@@ -434,6 +483,14 @@ def main():
         print(f"[bench] prefill T={T}: {ev * 1e3:.2f} ms, {T / ev:.0f} tok/s", file=sys.stderr, flush=True)
         lay.close()
 
+    # small-batch decode latency (the reference's headline configurations are batch 1)
+    small = None
+    if not args.no_small:
+        small = [small_batch_decode("0.8b", 1), small_batch_decode("9b", 1), small_batch_decode("9b", 8)]
+        for r in small:
+            print(f"[bench] decode {r['shape']} B={r['batch']}: {r['us_per_step']:.1f} us/step (graph), "
+                  f"{r['hbm_frac'] * 100:.0f}% of HBM roofline", file=sys.stderr, flush=True)
+
     stack = None
     if args.stack:
         print("[bench] 24-layer continuous-batching stack", file=sys.stderr, flush=True)
@@ -454,7 +511,7 @@ def main():
                                f"rotating over {L} layer copies" + (", HIP-graph replay" if args.graph else ""),
                    "hidden": d["hidden"], "num_k_heads": d["num_k_heads"], "num_v_heads": d["num_v_heads"],
                    "head_dim": 128, "batch": B, "state_dtype": "fp32", "weights": "bf16 N(0,0.02) seed 2"},
-        "roofline": roofline, "layer_roofline": layer_roof, "prefill": prefill, "stack": stack, "fp8_decode": fp8,
+        "roofline": roofline, "layer_roofline": layer_roof, "prefill": prefill, "stack": stack, "fp8_decode": fp8, "small_batch_decode": small,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

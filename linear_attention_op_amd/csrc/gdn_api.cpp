@@ -196,15 +196,18 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, u16* o
     const bool split_ab = frag && L->CD + Vd == L->NP - 2 * nv;
     bool ab_split = false;
     if (frag) {
-        HIP_OK(gdn::launch_frag_tile(x, M, d.hidden, L->x_frag, st));
         bool mixer_only = true;
         for (int gi = 0; gi < ng; ++gi) mixer_only = mixer_only && grp[gi].T <= kFusedMaxT;
         ab_split = split_ab && mixer_only;
     }
+    // up to 16 rows the decode in_proj reads the activations row-major: re-tiling them would cost a launch
+    const bool x_rows = ab_split && M <= 16;
+    if (frag && !x_rows) HIP_OK(gdn::launch_frag_tile(x, M, d.hidden, L->x_frag, st));
     if (ab_split)
-        HIP_OK(gdn::launch_in_proj_decode(L->x_frag, fp8(L) ? (const void*)L->w_in8 : L->w_in,
-                                          fp8(L) ? gdn::W_F8 : gdn::W_FRAG, L->s_in, L->w_ab, M, L->CD + Vd, 2 * nv,
-                                          d.hidden, L->P, L->NP, L->ab, kAbSplits, st));
+        HIP_OK(gdn::launch_in_proj_decode(x_rows ? (const void*)x : L->x_frag, x_rows ? gdn::W_ROW : gdn::W_FRAG,
+                                          fp8(L) ? (const void*)L->w_in8 : L->w_in, fp8(L) ? gdn::W_F8 : gdn::W_FRAG,
+                                          L->s_in, L->w_ab, M, L->CD + Vd, 2 * nv, d.hidden, L->P, L->NP, L->ab,
+                                          kAbSplits, st));
     else
         HIP_OK(in_proj_rows(L, frag ? L->x_frag : x, frag ? gdn::W_FRAG : gdn::W_ROW, M, L->P, st));
     if (ev[1]) HIP_OK(hipEventRecord(ev[1], st));

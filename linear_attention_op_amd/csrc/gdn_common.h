@@ -130,11 +130,11 @@ enum WLayout { W_ROW = 0, W_FRAG = 1, W_F8 = 2 };
 // activations only for M <= 64).
 hipError_t launch_linear(const void* x, int xlayout, const void* w, int wlayout, const float* w_scale, int M, int N,
                          int K, void* y, int ldy, int out_kind, hipStream_t stream);
-// Decode in_proj on fragment-layout activations (M <= 64): rows [0, N1) of w (W_FRAG, or W_F8 with
-// w_scale) into P (fp32, row stride ldp) with the workgroups balanced over the CUs; the N2 rows of w2
-// (W_FRAG) as ab_splits partial sums over k ranges into Pab [ab_splits][M][N2] (the consumer adds the
-// slices).  N1 % 16 == 0.
-hipError_t launch_in_proj_decode(const void* x_frag, const void* w, int wlayout, const float* w_scale,
+// Decode in_proj (M <= 64; activations in W_FRAG layout, or row-major W_ROW for M <= 16): rows [0, N1) of w
+// (W_FRAG, or W_F8 with w_scale) into P (fp32, row stride ldp) with the workgroups balanced over the CUs;
+// the N2 rows of w2 (W_FRAG) as ab_splits partial sums over k ranges into Pab [ab_splits][M][N2] (the
+// consumer adds the slices).  N1 % 16 == 0.
+hipError_t launch_in_proj_decode(const void* x, int xlayout, const void* w, int wlayout, const float* w_scale,
                                  const void* w2, int M, int N1, int N2, int K, float* P, int ldp, float* Pab,
                                  int ab_splits, hipStream_t stream);
 // Elements of an [N, K] matrix in W_FRAG layout (rows padded to a multiple of 16); also the bytes of the

@@ -329,8 +329,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x
 // [0, G) own NTS row tiles each of the first N1 rows (G = N1 / (16 NTS), chosen ~ one per CU) and write
 // them to P (row stride ldp); the remaining N2 rows (the a | b projection, 64 rows at 9B) are split into
 // KS k-ranges over workgroups [G, G + ceil(N2 / 16) KS), each writing its partial sums to slice ks of
-// Pab [KS][M][N2], which the mixer adds up.  One launch, no tail of half-used CUs.
-template <int NTS, int MT, int NW, int PD, int WL>
+// Pab [KS][M][N2], which the mixer adds up.  One launch, no tail of half-used CUs.  Activations in fragment
+// layout, or row-major (XL = W_ROW, for at most 16 rows, where re-tiling them would cost a launch).
+template <int NTS, int MT, int NW, int PD, int WL, int XL>
 __global__ __launch_bounds__(NW * 64) void in_proj_decode_kernel(const u16* __restrict__ x, const void* __restrict__ w,
                                                                 const float* __restrict__ scale,
                                                                 const u16* __restrict__ w2, int M, int N1, int N2,
@@ -342,17 +343,17 @@ __global__ __launch_bounds__(NW * 64) void in_proj_decode_kernel(const u16* __re
     const int bid = blockIdx.x;
     if (bid < G) {
         if constexpr (WL == W_F8)
-            gemv_block_f8<NTS, MT, NW, PD, OUT_F32, W_FRAG>(x, (const u8*)w, scale, M, N1, K, P, ldp, bid * NTS * 16,
-                                                           0, K >> 6, red);
+            gemv_block_f8<NTS, MT, NW, PD, OUT_F32, XL>(x, (const u8*)w, scale, M, N1, K, P, ldp, bid * NTS * 16, 0,
+                                                       K >> 6, red);
         else
-            gemv_block<NTS, MT, NW, PD, OUT_F32, W_FRAG, W_FRAG>(x, (const u16*)w, M, N1, K, P, ldp, bid * NTS * 16,
-                                                                0, K >> 5, red);
+            gemv_block<NTS, MT, NW, PD, OUT_F32, W_FRAG, XL>(x, (const u16*)w, M, N1, K, P, ldp, bid * NTS * 16, 0,
+                                                            K >> 5, red);
     } else {
         const int e = bid - G, nt = e % ((N2 + 15) >> 4), ks = e / ((N2 + 15) >> 4);
         const int KQ = K >> 5, per = (KQ + KS - 1) / KS;
         const int kqb = min(KQ, ks * per), kqn = min(KQ, kqb + per) - kqb;
-        gemv_block<1, MT, NW, PD, OUT_F32, W_FRAG, W_FRAG>(x, w2, M, N2, K, Pab + (size_t)ks * M * N2, N2, nt * 16,
-                                                          kqb, kqn, red);
+        gemv_block<1, MT, NW, PD, OUT_F32, W_FRAG, XL>(x, w2, M, N2, K, Pab + (size_t)ks * M * N2, N2, nt * 16, kqb,
+                                                      kqn, red);
     }
 }
 
@@ -817,15 +818,15 @@ struct DecodeArgs {
 // 8 waves per workgroup (two per SIMD) with a two-deep ring.  Measured on the 9B shape at M = 64 (with
 // the split a|b workgroups): bf16 23.6 us against 23.9 us for 4 waves and a four-deep ring (bf16 needs
 // <= 128 VGPRs so that the split workgroups can run beside the others), E4M3 18.8 us.
-template <int NTS, int MT, int WL>
+template <int NTS, int MT, int WL, int XL>
 void in_proj_decode_launch(const DecodeArgs& a, hipStream_t stream) {
     constexpr int NW = 8, PD = 2;
     const dim3 grid(a.G + ((a.N2 + 15) >> 4) * a.KS), block(NW * 64);
-    hipLaunchKernelGGL((in_proj_decode_kernel<NTS, MT, NW, PD, WL>), grid, block, 0, stream, a.x, a.w, a.scale, a.w2,
-                       a.M, a.N1, a.N2, a.K, a.G, a.KS, a.P, a.ldp, a.Pab);
+    hipLaunchKernelGGL((in_proj_decode_kernel<NTS, MT, NW, PD, WL, XL>), grid, block, 0, stream, a.x, a.w, a.scale,
+                       a.w2, a.M, a.N1, a.N2, a.K, a.G, a.KS, a.P, a.ldp, a.Pab);
 }
 
-template <int MT, int WL>
+template <int MT, int WL, int XL = W_FRAG>
 hipError_t in_proj_decode_mt(DecodeArgs a, hipStream_t stream) {
     const int NT1 = a.N1 >> 4;
     // tiles per workgroup: the smallest that keeps the main workgroups within one per CU
@@ -833,16 +834,17 @@ hipError_t in_proj_decode_mt(DecodeArgs a, hipStream_t stream) {
     if (NT1 % nts) return hipErrorInvalidValue;
     a.G = NT1 / nts;
     switch (nts) {
-        case 1: in_proj_decode_launch<1, MT, WL>(a, stream); break;
-        case 2: in_proj_decode_launch<2, MT, WL>(a, stream); break;
-        case 3: in_proj_decode_launch<3, MT, WL>(a, stream); break;
-        default: in_proj_decode_launch<4, MT, WL>(a, stream); break;
+        case 1: in_proj_decode_launch<1, MT, WL, XL>(a, stream); break;
+        case 2: in_proj_decode_launch<2, MT, WL, XL>(a, stream); break;
+        case 3: in_proj_decode_launch<3, MT, WL, XL>(a, stream); break;
+        default: in_proj_decode_launch<4, MT, WL, XL>(a, stream); break;
     }
     return hipGetLastError();
 }
 
 template <int WL>
-hipError_t in_proj_decode_wl(const DecodeArgs& a, hipStream_t stream) {
+hipError_t in_proj_decode_wl(const DecodeArgs& a, int xlayout, hipStream_t stream) {
+    if (xlayout == W_ROW) return in_proj_decode_mt<1, WL, W_ROW>(a, stream);  // M <= 16
     if (a.M <= 16) return in_proj_decode_mt<1, WL>(a, stream);
     if (a.M <= 32) return in_proj_decode_mt<2, WL>(a, stream);
     if (a.M <= 48) return in_proj_decode_mt<3, WL>(a, stream);
@@ -851,16 +853,17 @@ hipError_t in_proj_decode_wl(const DecodeArgs& a, hipStream_t stream) {
 
 }  // namespace
 
-hipError_t launch_in_proj_decode(const void* x_frag, const void* w, int wlayout, const float* w_scale,
+hipError_t launch_in_proj_decode(const void* x, int xlayout, const void* w, int wlayout, const float* w_scale,
                                  const void* w2, int M, int N1, int N2, int K, float* P, int ldp, float* Pab,
                                  int ab_splits, hipStream_t stream) {
     if (M <= 0) return hipSuccess;
     if (M > 64 || N1 % 16 || ab_splits <= 0 || K % 32) return hipErrorInvalidValue;
     if (wlayout != W_FRAG && wlayout != W_F8) return hipErrorInvalidValue;
     if (wlayout == W_F8 && (K % 64 || !w_scale)) return hipErrorInvalidValue;
-    const DecodeArgs a{(const u16*)x_frag, w, w_scale, (const u16*)w2, M, N1, N2, K, 0, ab_splits, P, ldp, Pab};
-    if (wlayout == W_F8) return in_proj_decode_wl<W_F8>(a, stream);
-    return in_proj_decode_wl<W_FRAG>(a, stream);
+    if (xlayout != W_FRAG && (xlayout != W_ROW || M > 16)) return hipErrorInvalidValue;
+    const DecodeArgs a{(const u16*)x, w, w_scale, (const u16*)w2, M, N1, N2, K, 0, ab_splits, P, ldp, Pab};
+    if (wlayout == W_F8) return in_proj_decode_wl<W_F8>(a, xlayout, stream);
+    return in_proj_decode_wl<W_FRAG>(a, xlayout, stream);
 }
 
 hipError_t launch_linear(const void* x, int xlayout, const void* w, int wlayout, const float* w_scale, int M, int N,
