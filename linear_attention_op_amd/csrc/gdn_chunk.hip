@@ -66,32 +66,37 @@ __device__ __forceinline__ uint32_t bf16_bits(float x) {
 //   0. the chunk's inputs: thread (prow, pc4) owns tokens 4 prow .. 4 prow + 3, channels pc4 .. pc4 + 3 of
 //      q, k, v (coalesced float4; in the layer computed by the fused front end), g, beta.
 //   1. per-token normalisers (32-lane reductions), normalised keys -> sK (and kept in registers),
-//      queries -> sQ (aliases the L / Aqk tiles, which are not written yet), G = cumsum(g).
+//      queries -> sQ (aliases the L / Aqk tiles, which are not written yet); G = cumsum(g).
 //   2. k k^T and q k^T (wave w: row tile mi, column tiles 2 hf, 2 hf + 1 at or below it) -> L into sL,
-//      Aqk into sA; from the keys in registers, the state pass's key fragments and X = beta K e^G
-//      transposed and split into sK.
+//      Aqk into sA; from the keys in registers, the state pass's key fragments.
 //   3. T = (I + L)^-1, blocked: the four 16 x 16 diagonal blocks by forward substitution (one wave
 //      each), then T_ij = -T_ii sum_{k=j}^{i-1} L_ik T_kj by distance i - j = 1, 2, 3 -> sT.
 //   4. M2 = Aqk T in place over Aqk.
-//   5. T and M2 into registers; (beta V)^T split into sLA; [T; M2] x X: W and Q' = Q e^G - Aqk W
-//      (wave w: row tile mi, column tiles 4 hf .. 4 hf + 3).
+//   5. T and M2 into registers; X = beta K e^G and beta V, from the keys and values still in registers,
+//      transposed and split into the two regions; [T; M2] x X: W and Q' = Q e^G - Aqk W (wave w: row
+//      tile mi, column tiles 4 hf .. 4 hf + 3).
 //   6. [T; M2] x (beta V): U and the intra-chunk output.
 // ------------------------------------------------------------------------------------------------
 template <int DK, int DV, bool FUSED>
-__global__ __launch_bounds__(512) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws, FrontArgs f) {
+__global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws, FrontArgs f) {
     static_assert(DK == 128 && DV == 128, "chunked path is specialised for 128-wide heads");
     constexpr int NT = 512;      // threads
     constexpr int LDK = DK + 4;  // row stride (floats) of the 64 x 128 tiles
     constexpr int LDT = CK + 4;  // row stride of the 64 x 64 tiles
     constexpr int LDX = 17;      // row stride of the 16 x 16 scratch blocks
-    __shared__ __attribute__((aligned(16))) float sK[CK * LDK];          // keys, then X^T split
-    __shared__ __attribute__((aligned(16))) float sLA[2 * CK * LDT];     // queries, then L | Aqk (M2), then (beta V)^T
-    __shared__ __attribute__((aligned(16))) float sT[CK * LDT];          // T
-    __shared__ __attribute__((aligned(16))) float sX[4][16 * LDX];       // per-wave 16 x 16 scratch (phase 3)
+    // Two regions, 68 KB with the scalars, so that two workgroups share a CU:
+    //   sK:  keys (phases 1-2), then T and the phase-3 scratch (3-5), then X^T split (5)
+    //   sLA: queries (1-2), then L | Aqk (M2) (2-5), then (beta V)^T split (5-6)
+    __shared__ __attribute__((aligned(16))) float sK[CK * LDK];
+    __shared__ __attribute__((aligned(16))) float sLA[2 * CK * LDT];
     __shared__ float sG[CK], sEG[CK], sDec[CK], sBeta[CK];
+    static_assert(CK * LDT + 4 * 16 * LDX <= CK * LDK && CK * LDK <= 2 * CK * LDT && DK * CK <= CK * LDK,
+                  "region sizes");
     float* sQ = sLA;                 // [CK][LDK] fits in the 2 * CK * LDT floats of sLA
     float* sL = sLA;                 // [CK][LDT]
     float* sA = sLA + CK * LDT;      // [CK][LDT]
+    float* sT = sK;                  // [CK][LDT]
+    float* sX = sK + CK * LDT;       // [4 waves][16 * LDX]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int mi = wave & 3, hf = wave >> 2;
@@ -106,12 +111,24 @@ __global__ __launch_bounds__(512) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
     // ---- 0. inputs: thread (prow, pc4) owns tokens 4 prow + j (j < 4), channels pc4 .. pc4 + 3 of q, k, v
     const int prow = tid >> 5, pc4 = (tid & 31) * 4;
     const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
-    float4 kr[4], qr[4], vr[4];
+    float4 kr[4], vr[4];
     float gv = 0.f, bv = 0.f;
+    // l2norm over the 32 lanes of a half-wave (one token's row), times `mult`, and the row into LDS
+    auto l2store = [&](float4* x, float mult, float* dst) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float ss = x[j].x * x[j].x + x[j].y * x[j].y + x[j].z * x[j].z + x[j].w * x[j].w;
+#pragma unroll
+            for (int off = 1; off < 32; off <<= 1) ss += __shfl_xor(ss, off, 64);
+            const float r = (a.normalize ? rsqrtf(ss + 1e-6f) : 1.f) * mult;
+            x[j].x *= r, x[j].y *= r, x[j].z *= r, x[j].w *= r;
+            *reinterpret_cast<float4*>(&dst[(4 * prow + j) * LDK + pc4]) = x[j];
+        }
+    };
     if constexpr (FUSED) {
         // The front end, from the projection rows: causal conv (4 taps over the inputs at t - 3 .. t, the
         // slot's history before t = 0) + SiLU, as conv_front_kernel (layer_compute.cpp C1, 74-103).  The
-        // window of the thread's 4 tokens is 7 input rows; all 21 loads are issued before any use.
+        // window of the thread's 4 tokens is 7 input rows, loaded one tensor at a time (register budget).
         const int Kd = f.nk * DK, Vd = f.nv * DV, CD = 2 * Kd + Vd, CH = 2 * DK + DV;
         const int slot = f.slot_ids ? f.slot_ids[b] : b;
         const float* hq = f.conv_state + ((size_t)slot * f.nv + kh * (Hv / Hk)) * 3 * CH;  // q | k history copy
@@ -123,21 +140,15 @@ __global__ __launch_bounds__(512) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
             return t >= 0 ? *reinterpret_cast<const float4*>(f.P + (size_t)((long long)row0 + tk) * f.NP + col)
                           : *reinterpret_cast<const float4*>(hist + (3 + t) * CH + local);
         };
-        float4 xq[7], xk[7], xv[7];
-#pragma unroll
-        for (int r = 0; r < 7; ++r) {
-            const int tk = 4 * prow - 3 + r;
-            xq[r] = in_row(tk, colq, hq, pc4);
-            xk[r] = in_row(tk, colk, hq, DK + pc4);
-            xv[r] = in_row(tk, colv, hv, 2 * DK + pc4);
-        }
         if (wave == 0 && lane < len) {
             const float* Pr = f.P + (row0 + lane) * f.NP + CD + Vd;
             gv = f.neg_A[h] * softplusf_(Pr[h] + f.dt_bias[h]);
             bv = sigmoidf_(Pr[f.nv + h]);
         }
-        auto conv4 = [&](const float4* x, int col, float4* out) {
-            float4 w[4];
+        auto conv4 = [&](int col, const float* hist, int local, float4* out) {
+            float4 x[7], w[4];
+#pragma unroll
+            for (int r = 0; r < 7; ++r) x[r] = in_row(4 * prow - 3 + r, col, hist, local);
 #pragma unroll
             for (int i = 0; i < 4; ++i) w[i] = f.conv_w[col + i];
 #pragma unroll
@@ -151,10 +162,17 @@ __global__ __launch_bounds__(512) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
                 out[j] = 4 * prow + j < len ? o : z4;
             }
         };
-        conv4(xk, colk, kr);
-        conv4(xq, colq, qr);
-        conv4(xv, colv, vr);
+        // one tensor at a time, the queries normalised and stored before the next window is loaded
+        {
+            float4 qr[4];
+            conv4(colq, hq, pc4, qr);
+            l2store(qr, a.scale, sQ);
+        }
+        conv4(colk, hq, DK + pc4, kr);
+        l2store(kr, 1.f, sK);
+        conv4(colv, hv, 2 * DK + pc4, vr);
     } else {
+        float4 qr[4];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             const int tok = 4 * prow + j;
@@ -166,24 +184,12 @@ __global__ __launch_bounds__(512) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
             vr[j] = ok ? *reinterpret_cast<const float4*>(a.v + (row * Hv + h) * DV + pc4) : z4;
         }
         if (wave == 0 && lane < len) gv = a.g[(row0 + lane) * Hv + h], bv = a.beta[(row0 + lane) * Hv + h];
+        l2store(qr, a.scale, sQ);
+        l2store(kr, 1.f, sK);
     }
+    // (the normalised keys stay in registers)
 
-    // ---- 1. normalisers (the 32 lanes of a half-wave hold one row), sK, sQ, G ---------------------------
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const int tok = 4 * prow + j;
-        float sk = kr[j].x * kr[j].x + kr[j].y * kr[j].y + kr[j].z * kr[j].z + kr[j].w * kr[j].w;
-        float sq = qr[j].x * qr[j].x + qr[j].y * qr[j].y + qr[j].z * qr[j].z + qr[j].w * qr[j].w;
-#pragma unroll
-        for (int off = 1; off < 32; off <<= 1) sk += __shfl_xor(sk, off, 64), sq += __shfl_xor(sq, off, 64);
-        const float rk = a.normalize ? rsqrtf(sk + 1e-6f) : 1.f;
-        const float rq = (a.normalize ? rsqrtf(sq + 1e-6f) : 1.f) * a.scale;
-        float4 qn = qr[j];
-        kr[j].x *= rk, kr[j].y *= rk, kr[j].z *= rk, kr[j].w *= rk;  // the normalised keys stay in registers
-        qn.x *= rq, qn.y *= rq, qn.z *= rq, qn.w *= rq;
-        *reinterpret_cast<float4*>(&sK[tok * LDK + pc4]) = kr[j];
-        *reinterpret_cast<float4*>(&sQ[tok * LDK + pc4]) = qn;
-    }
+    // ---- 1. G ---------------------------------------------------------------------------------------------
     if (wave == 0) {
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
@@ -198,12 +204,7 @@ __global__ __launch_bounds__(512) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
     __syncthreads();
 
     // ---- 2. k k^T and q k^T: wave w owns row tile mi, column tiles 2 hf, 2 hf + 1 -----------------------
-    // the queries this wave needs later for Q' (token 16 mi + m, columns 16 n + 4 grp + i for its column tiles
-    // n = 4 hf .. 4 hf + 3: the C layout of the transposed product below) are read now, before sQ is overwritten
     float4 qe[4];
-#pragma unroll
-    for (int n = 0; n < 4; ++n)
-        qe[n] = *reinterpret_cast<const float4*>(&sQ[(16 * mi + m) * LDK + 16 * (4 * hf + n) + 4 * grp]);
     {
         f32x4 akk[2], aqk[2];
 #pragma unroll
@@ -228,46 +229,38 @@ __global__ __launch_bounds__(512) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
                 }
             }
         }
+        // the queries this wave needs later for Q' (token 16 mi + m, columns 16 n + 4 grp + i for its column
+        // tiles n = 4 hf .. 4 hf + 3: the C layout of the transposed product in phase 5), before sQ is
+        // overwritten
+#pragma unroll
+        for (int n = 0; n < 4; ++n)
+            qe[n] = *reinterpret_cast<const float4*>(&sQ[(16 * mi + m) * LDK + 16 * (4 * hf + n) + 4 * grp]);
         __syncthreads();  // every wave is done with sK and sQ before they are overwritten
-        // From the normalised keys in registers (thread (prow, pc4): tokens 4 prow + j of channels pc4 + cc,
-        // half `prow % 2` of the 8-token group prow / 2):
-        //  * the state pass's key fragments Kt[r][tok] = k[tok][r] e^{G_last - G_tok}, split: unit
-        //    (w, s, grp, m) with r = 16 w + m and 8-token group 4 s + grp;
-        //  * X = beta K e^G, transposed and split into bf16 hi | lo planes over sK: element (r, tok) at
-        //    r * CK + ((tok / 8) ^ (r % 8)) * 8 + tok % 8 (the xor puts the 16-byte reads of eight
-        //    consecutive rows in distinct banks).
+        // The state pass's key fragments from the normalised keys in registers (thread (prow, pc4): tokens
+        // 4 prow + j of channels pc4 + cc, half `prow % 2` of the 8-token group prow / 2):
+        // Kt[r][tok] = k[tok][r] e^{G_last - G_tok}, split: unit (w, s, grp, m) with r = 16 w + m and
+        // 8-token group 4 s + grp.
         {
             u16* Kf = ws.Kf + hc * DK * CK * 2;
-            u16* XTh = reinterpret_cast<u16*>(sK);
-            u16* XTl = XTh + DK * CK;
             const int tg = prow >> 1, half = (prow & 1) * 4;
-            float dec[4], sc[4];
+            float dec[4];
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int tok = 4 * prow + j;
-                dec[j] = sDec[tok];
-                sc[j] = sBeta[tok] * sEG[tok];
-            }
+            for (int j = 0; j < 4; ++j) dec[j] = sDec[4 * prow + j];
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc) {
                 const int r = pc4 + cc;
-                u16x4 kh4, kl4, xh4, xl4;
+                u16x4 kh4, kl4;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const float kv = cc == 0 ? kr[j].x : (cc == 1 ? kr[j].y : (cc == 2 ? kr[j].z : kr[j].w));
-                    const float x = kv * dec[j], y = kv * sc[j];
-                    const __bf16 xh = (__bf16)x, yh = (__bf16)y;
+                    const float x = kv * dec[j];
+                    const __bf16 xh = (__bf16)x;
                     kh4[j] = __builtin_bit_cast(u16, xh);
                     kl4[j] = (u16)bf16_bits(x - (float)xh);
-                    xh4[j] = __builtin_bit_cast(u16, yh);
-                    xl4[j] = (u16)bf16_bits(y - (float)yh);
                 }
                 const int u = ((r >> 4) * 2 + (tg >> 2)) * 64 + (tg & 3) * 16 + (r & 15);
                 *reinterpret_cast<u16x4*>(Kf + (size_t)u * 16 + half) = kh4;
                 *reinterpret_cast<u16x4*>(Kf + (size_t)u * 16 + 8 + half) = kl4;
-                const int xo = r * CK + ((tg ^ (r & 7)) << 3) + half;
-                *reinterpret_cast<u16x4*>(XTh + xo) = xh4;
-                *reinterpret_cast<u16x4*>(XTl + xo) = xl4;
             }
         }
 #pragma unroll
@@ -325,13 +318,13 @@ __global__ __launch_bounds__(512) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
                     for (int rr = 0; rr < 4; ++rr) x[rr] += sL[(16 * i + 4 * r4 + rr) * LDT + 16 * k + q] * tkj;
                 }
 #pragma unroll
-            for (int rr = 0; rr < 4; ++rr) sX[wave][(4 * r4 + rr) * LDX + cc] = x[rr];
+            for (int rr = 0; rr < 4; ++rr) sX[wave * 16 * LDX + (4 * r4 + rr) * LDX + cc] = x[rr];
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
             float y[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
-                const float xq = sX[wave][q * LDX + cc];
+                const float xq = sX[wave * 16 * LDX + q * LDX + cc];
 #pragma unroll
                 for (int rr = 0; rr < 4; ++rr) y[rr] += sT[(16 * i + 4 * r4 + rr) * LDT + 16 * i + q] * xq;
             }
@@ -389,34 +382,47 @@ __global__ __launch_bounds__(512) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
         At[s] = split8(tv);
         Am[s] = split8(mv);
     }
-    __syncthreads();  // T and M2 are in registers: sLA is free
-    // 6a. (beta V)^T split into sLA, laid out as X^T (thread (prow, pc4): tokens 4 prow + j of channels pc4 + cc)
-    const u16* XTh = reinterpret_cast<const u16*>(sK);
-    const u16* XTl = XTh + DK * CK;
+    __syncthreads();  // T and M2 are in registers: both regions are free
+    // X = beta K e^G (over sK) and beta V (over sLA), transposed and split into bf16 hi | lo planes, from the
+    // keys and values in registers (thread (prow, pc4): tokens 4 prow + j of channels pc4 + cc, half
+    // `prow % 2` of the 8-token group prow / 2).  Element (r, tok) at r * CK + ((tok / 8) ^ (r % 8)) * 8 +
+    // tok % 8: the xor puts the 16-byte reads of eight consecutive rows in distinct banks.
+    u16* XTh = reinterpret_cast<u16*>(sK);
+    u16* XTl = XTh + DK * CK;
     u16* VTh = reinterpret_cast<u16*>(sLA);
     u16* VTl = VTh + DV * CK;
     {
         const int tg = prow >> 1, half = (prow & 1) * 4;
-        float bt[4];
+        float bt[4], sc[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) bt[j] = sBeta[4 * prow + j];
+        for (int j = 0; j < 4; ++j) {
+            const int tok = 4 * prow + j;
+            bt[j] = sBeta[tok];
+            sc[j] = bt[j] * sEG[tok];
+        }
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
             const int r = pc4 + cc;
-            u16x4 vh4, vl4;
+            u16x4 xh4, xl4, vh4, vl4;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
+                const float kv = cc == 0 ? kr[j].x : (cc == 1 ? kr[j].y : (cc == 2 ? kr[j].z : kr[j].w));
                 const float vv = cc == 0 ? vr[j].x : (cc == 1 ? vr[j].y : (cc == 2 ? vr[j].z : vr[j].w));
-                const float y = vv * bt[j];
-                const __bf16 yh = (__bf16)y;
+                const float x = kv * sc[j], y = vv * bt[j];
+                const __bf16 xh = (__bf16)x, yh = (__bf16)y;
+                xh4[j] = __builtin_bit_cast(u16, xh);
+                xl4[j] = (u16)bf16_bits(x - (float)xh);
                 vh4[j] = __builtin_bit_cast(u16, yh);
                 vl4[j] = (u16)bf16_bits(y - (float)yh);
             }
-            const int vo = r * CK + ((tg ^ (r & 7)) << 3) + half;
-            *reinterpret_cast<u16x4*>(VTh + vo) = vh4;
-            *reinterpret_cast<u16x4*>(VTl + vo) = vl4;
+            const int o = r * CK + ((tg ^ (r & 7)) << 3) + half;
+            *reinterpret_cast<u16x4*>(XTh + o) = xh4;
+            *reinterpret_cast<u16x4*>(XTl + o) = xl4;
+            *reinterpret_cast<u16x4*>(VTh + o) = vh4;
+            *reinterpret_cast<u16x4*>(VTl + o) = vl4;
         }
     }
+    __syncthreads();  // X^T and (beta V)^T are complete
     // operand of token group (4 s + grp) for row r (16-byte reads, the xor layout above)
     auto tfrag = [&](const u16* hp, const u16* lp, int r, int s) {
         const int o = r * CK + (((4 * s + grp) ^ (r & 7)) << 3);
@@ -456,8 +462,7 @@ __global__ __launch_bounds__(512) void chunk_prep_kernel(DeltaArgs a, ChunkWs ws
         *reinterpret_cast<u16x8*>(Wf + f8) = fw;
         *reinterpret_cast<u16x8*>(Qf + f8) = fq;
     }
-    __syncthreads();  // (beta V)^T is complete
-    // 6b. U = T (beta V), stored transposed (lane (m, grp): tokens 16 mi + 4 grp + i of column 16 n + m, one
+    // 6. U = T (beta V), stored transposed (lane (m, grp): tokens 16 mi + 4 grp + i of column 16 n + m, one
     //     16-byte store), and the intra-chunk output M2 (beta V) into o
     float* Ut = ws.Ut + hc * DV * CK;
 #pragma unroll
