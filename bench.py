@@ -188,6 +188,28 @@ def measure_traffic(kernel="mixer_kernel", timeout=180):
     return {"bytes": out["FETCH_SIZE"]["bytes"] + out["WRITE_SIZE"]["bytes"], "passes": out}, None
 
 
+def stream_ceiling(nbytes, copies=4, reps=40):
+    """In-place read + write of `nbytes` (torch's elementwise scale) over `copies` rotating buffers, so that the
+    256 MB last-level cache cannot hold them: the HBM rate a plain streaming kernel with the decode state's
+    access pattern (read once, write once) reaches on this device."""
+    import torch
+
+    bufs = [torch.ones(nbytes // 4, device="cuda") for _ in range(copies)]
+    for b in bufs:
+        b.mul_(1.0000001)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(reps):
+        bufs[i % copies].mul_(1.0000001)
+    e1.record()
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) / 1e3 / reps
+    del bufs
+    return {"op": f"torch in-place fp32 scale, {copies} rotating buffers of {nbytes / 1e6:.1f} MB",
+            "bytes": 2 * nbytes, "us": sec * 1e6, "GBps": 2 * nbytes / sec / 1e9, "frac": 2 * nbytes / sec / HBM_PEAK}
+
+
 def small_batch_decode(shape, B, copies=8, steps=400, warmup=40):
     """Decode latency of one layer at a small batch, one HIP graph per layer copy (launch overhead is most
     of such a step), rotating over `copies` layers so that the weights come from HBM."""
@@ -425,6 +447,11 @@ def main():
                   "event_step_us": stage_avg_ms["total"] * 1e3,
                   "event_frac": step_bytes / (stage_avg_ms["total"] / 1e3) / HBM_PEAK,
                   "stage_us": {k: v * 1e3 for k, v in stage_avg_ms.items()}}
+    # the practical ceiling for the mixer's traffic: a plain stream over the same state bytes
+    ceiling = stream_ceiling(B * d["num_v_heads"] * 128 * 128 * 4)
+    roofline["frac_of_stream"] = roofline["achieved"] / ceiling["GBps"]
+    print(f"[bench] stream ceiling: {ceiling['GBps']:.0f} GB/s ({ceiling['frac'] * 100:.0f}% of peak); mixer "
+          f"{roofline['achieved']:.0f} GB/s", file=sys.stderr, flush=True)
     print(f"[bench] decode B={B}: {ms_per_step * 1e3:.1f} us/step wall ({'graph' if args.graph else 'eager'}), "
           f"eager stages (us) "
           f"{ {k: round(v * 1e3, 1) for k, v in stage_avg_ms.items()} }", file=sys.stderr, flush=True)
@@ -511,7 +538,8 @@ def main():
                                f"rotating over {L} layer copies" + (", HIP-graph replay" if args.graph else ""),
                    "hidden": d["hidden"], "num_k_heads": d["num_k_heads"], "num_v_heads": d["num_v_heads"],
                    "head_dim": 128, "batch": B, "state_dtype": "fp32", "weights": "bf16 N(0,0.02) seed 2"},
-        "roofline": roofline, "layer_roofline": layer_roof, "prefill": prefill, "stack": stack, "fp8_decode": fp8, "small_batch_decode": small,
+        "roofline": roofline, "layer_roofline": layer_roof, "stream_ceiling": ceiling, "prefill": prefill,
+        "stack": stack, "fp8_decode": fp8, "small_batch_decode": small,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

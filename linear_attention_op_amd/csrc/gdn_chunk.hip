@@ -68,7 +68,8 @@ __device__ __forceinline__ uint32_t bf16_bits(float x) {
 //   1. per-token normalisers (32-lane reductions), normalised keys -> sK (and kept in registers),
 //      queries -> sQ (aliases the L / Aqk tiles, which are not written yet); G = cumsum(g).
 //   2. k k^T and q k^T (wave w: row tile mi, column tiles 2 hf, 2 hf + 1 at or below it) -> L into sL,
-//      Aqk into sA; from the keys in registers, the state pass's key fragments.
+//      Aqk into sA; the decay-scaled keys transposed through the key region into the state pass's key
+//      fragments.
 //   3. T = (I + L)^-1, blocked: the four 16 x 16 diagonal blocks by forward substitution (one wave
 //      each), then T_ij = -T_ii sum_{k=j}^{i-1} L_ik T_kj by distance i - j = 1, 2, 3 -> sT.
 //   4. M2 = Aqk T in place over Aqk.
@@ -85,7 +86,7 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
     constexpr int LDT = CK + 4;  // row stride of the 64 x 64 tiles
     constexpr int LDX = 17;      // row stride of the 16 x 16 scratch blocks
     // Two regions, 68 KB with the scalars, so that two workgroups share a CU:
-    //   sK:  keys (phases 1-2), then T and the phase-3 scratch (3-5), then X^T split (5)
+    //   sK:  keys (phases 1-2), transposed decay-scaled keys (2), T and the phase-3 scratch (3-5), X^T split (5)
     //   sLA: queries (1-2), then L | Aqk (M2) (2-5), then (beta V)^T split (5-6)
     __shared__ __attribute__((aligned(16))) float sK[CK * LDK];
     __shared__ __attribute__((aligned(16))) float sLA[2 * CK * LDT];
@@ -110,7 +111,11 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
 
     // ---- 0. inputs: thread (prow, pc4) owns tokens 4 prow + j (j < 4), channels pc4 .. pc4 + 3 of q, k, v
     const int prow = tid >> 5, pc4 = (tid & 31) * 4;
-    const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    // v if ok, else zeros: per-component selects after an unconditional load from a valid address (a select
+    // between a loaded and a constant vector would be turned into a load from a private copy of the constant)
+    auto keep_if = [](bool ok, float4 v) {
+        return make_float4(ok ? v.x : 0.f, ok ? v.y : 0.f, ok ? v.z : 0.f, ok ? v.w : 0.f);
+    };
     float4 kr[4], vr[4];
     float gv = 0.f, bv = 0.f;
     // l2norm over the 32 lanes of a half-wave (one token's row), times `mult`, and the row into LDS
@@ -135,10 +140,10 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
         const float* hv = f.conv_state + ((size_t)slot * f.nv + h) * 3 * CH;
         const int colq = kh * DK + pc4, colk = Kd + kh * DK + pc4, colv = 2 * Kd + h * DV + pc4;
         auto in_row = [&](int tk, int col, const float* hist, int local) -> float4 {
-            if (tk >= len) return z4;
-            const int t = t0 + tk;
-            return t >= 0 ? *reinterpret_cast<const float4*>(f.P + (size_t)((long long)row0 + tk) * f.NP + col)
-                          : *reinterpret_cast<const float4*>(hist + (3 + t) * CH + local);
+            const int tkc = min(tk, len - 1);  // rows past the end read a valid row, zeroed below
+            const int t = t0 + tkc;
+            const float* p = t >= 0 ? f.P + (size_t)((long long)row0 + tkc) * f.NP + col : hist + (3 + t) * CH + local;
+            return keep_if(tk < len, *reinterpret_cast<const float4*>(p));
         };
         if (wave == 0 && lane < len) {
             const float* Pr = f.P + (row0 + lane) * f.NP + CD + Vd;
@@ -159,7 +164,7 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
                 o.y = siluf_(w[1].x * x0.y + w[1].y * x1.y + w[1].z * x2.y + w[1].w * x3.y);
                 o.z = siluf_(w[2].x * x0.z + w[2].y * x1.z + w[2].z * x2.z + w[2].w * x3.z);
                 o.w = siluf_(w[3].x * x0.w + w[3].y * x1.w + w[3].z * x2.w + w[3].w * x3.w);
-                out[j] = 4 * prow + j < len ? o : z4;
+                out[j] = keep_if(4 * prow + j < len, o);
             }
         };
         // one tensor at a time, the queries normalised and stored before the next window is loaded
@@ -179,9 +184,9 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
             const bool ok = tok < len;
             const size_t row = row0 + (ok ? tok : 0);
             const size_t qk = (row * Hk + kh) * DK + pc4;
-            kr[j] = ok ? *reinterpret_cast<const float4*>(a.k + qk) : z4;
-            qr[j] = ok ? *reinterpret_cast<const float4*>(a.q + qk) : z4;
-            vr[j] = ok ? *reinterpret_cast<const float4*>(a.v + (row * Hv + h) * DV + pc4) : z4;
+            kr[j] = keep_if(ok, *reinterpret_cast<const float4*>(a.k + qk));
+            qr[j] = keep_if(ok, *reinterpret_cast<const float4*>(a.q + qk));
+            vr[j] = keep_if(ok, *reinterpret_cast<const float4*>(a.v + (row * Hv + h) * DV + pc4));
         }
         if (wave == 0 && lane < len) gv = a.g[(row0 + lane) * Hv + h], bv = a.beta[(row0 + lane) * Hv + h];
         l2store(qr, a.scale, sQ);
@@ -236,31 +241,22 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
         for (int n = 0; n < 4; ++n)
             qe[n] = *reinterpret_cast<const float4*>(&sQ[(16 * mi + m) * LDK + 16 * (4 * hf + n) + 4 * grp]);
         __syncthreads();  // every wave is done with sK and sQ before they are overwritten
-        // The state pass's key fragments from the normalised keys in registers (thread (prow, pc4): tokens
-        // 4 prow + j of channels pc4 + cc, half `prow % 2` of the 8-token group prow / 2):
-        // Kt[r][tok] = k[tok][r] e^{G_last - G_tok}, split: unit (w, s, grp, m) with r = 16 w + m and
-        // 8-token group 4 s + grp.
+        // Kt[r][tok] = k[tok][r] e^{G_last - G_tok} (the state pass's keys) transposed into the key region, fp32
+        // with 16-byte chunks xor-swizzled: element (r, tok) at r * CK + ((tok / 4) ^ ((r / 4) % 16)) * 4 +
+        // tok % 4 (thread (prow, pc4) holds tokens 4 prow + j of channels pc4 + cc: one chunk per channel)
         {
-            u16* Kf = ws.Kf + hc * DK * CK * 2;
-            const int tg = prow >> 1, half = (prow & 1) * 4;
             float dec[4];
 #pragma unroll
             for (int j = 0; j < 4; ++j) dec[j] = sDec[4 * prow + j];
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc) {
                 const int r = pc4 + cc;
-                u16x4 kh4, kl4;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float kv = cc == 0 ? kr[j].x : (cc == 1 ? kr[j].y : (cc == 2 ? kr[j].z : kr[j].w));
-                    const float x = kv * dec[j];
-                    const __bf16 xh = (__bf16)x;
-                    kh4[j] = __builtin_bit_cast(u16, xh);
-                    kl4[j] = (u16)bf16_bits(x - (float)xh);
-                }
-                const int u = ((r >> 4) * 2 + (tg >> 2)) * 64 + (tg & 3) * 16 + (r & 15);
-                *reinterpret_cast<u16x4*>(Kf + (size_t)u * 16 + half) = kh4;
-                *reinterpret_cast<u16x4*>(Kf + (size_t)u * 16 + 8 + half) = kl4;
+                float4 v;
+                v.x = (cc == 0 ? kr[0].x : (cc == 1 ? kr[0].y : (cc == 2 ? kr[0].z : kr[0].w))) * dec[0];
+                v.y = (cc == 0 ? kr[1].x : (cc == 1 ? kr[1].y : (cc == 2 ? kr[1].z : kr[1].w))) * dec[1];
+                v.z = (cc == 0 ? kr[2].x : (cc == 1 ? kr[2].y : (cc == 2 ? kr[2].z : kr[2].w))) * dec[2];
+                v.w = (cc == 0 ? kr[3].x : (cc == 1 ? kr[3].y : (cc == 2 ? kr[3].z : kr[3].w))) * dec[3];
+                *reinterpret_cast<float4*>(&sK[r * CK + ((prow ^ ((r >> 2) & 15)) << 2)]) = v;
             }
         }
 #pragma unroll
@@ -281,11 +277,37 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
     }
     __syncthreads();
 
+    // The state pass's key fragments from the transposed keys: thread t writes units t and t + 512 of the
+    // chunk's Kf block (unit u: row r = 16 (u / 128) + u % 16, 8-token group 4 ((u / 64) % 2) + (u / 16) % 4;
+    // 16 bytes hi, 16 bytes lo), so that a wave writes 2 KB of contiguous memory.
+    {
+        u16* Kf = ws.Kf + hc * DK * CK * 2;
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+            const int u = tid + NT * e;
+            const int r = 16 * (u >> 7) + (u & 15), tg = 4 * ((u >> 6) & 1) + ((u >> 4) & 3), sw = (r >> 2) & 15;
+            float x[8];
+            const float4 a0 = *reinterpret_cast<const float4*>(&sK[r * CK + (((2 * tg) ^ sw) << 2)]);
+            const float4 a1 = *reinterpret_cast<const float4*>(&sK[r * CK + (((2 * tg + 1) ^ sw) << 2)]);
+            x[0] = a0.x, x[1] = a0.y, x[2] = a0.z, x[3] = a0.w, x[4] = a1.x, x[5] = a1.y, x[6] = a1.z, x[7] = a1.w;
+            u16x8 hi, lo;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const __bf16 xh = (__bf16)x[j];
+                hi[j] = __builtin_bit_cast(u16, xh);
+                lo[j] = (u16)bf16_bits(x[j] - (float)xh);
+            }
+            *reinterpret_cast<u16x8*>(Kf + (size_t)u * 16) = hi;
+            *reinterpret_cast<u16x8*>(Kf + (size_t)u * 16 + 8) = lo;
+        }
+    }
+
     // ---- 3. T = (I + L)^-1 ---------------------------------------------------------------------------
-    // 3a. diagonal block w (waves 0-3): lane c < 16 owns column c, rows by forward substitution
+    // 3a. diagonal block w (waves 0-3): lane c < 16 owns column c, rows by forward substitution (into
+    //     registers; written after every wave has read the transposed keys that T overwrites)
+    float t[16];
     if (wave < 4 && lane < 16) {
         const int o = 16 * wave;
-        float t[16];
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
             float acc = (r == lane) ? 1.f : 0.f;
@@ -293,8 +315,11 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
             for (int k = 0; k < r; ++k) acc -= sL[(o + r) * LDT + o + k] * t[k];
             t[r] = acc;
         }
+    }
+    __syncthreads();
+    if (wave < 4 && lane < 16) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sT[(o + r) * LDT + o + lane] = t[r];
+        for (int r = 0; r < 16; ++r) sT[(16 * wave + r) * LDT + 16 * wave + lane] = t[r];
     }
     // upper blocks of T are zero
     for (int e = tid; e < CK * CK; e += NT) {
@@ -302,34 +327,32 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
         if ((cc >> 4) > (r >> 4)) sT[r * LDT + cc] = 0.f;
     }
     __syncthreads();
-    // 3b. T_ij = -T_ii X, X = sum_{k=j}^{i-1} L_ik T_kj (wave j).  Lane (r4, cc) = (lane / 16, lane % 16)
-    //     makes rows 4 r4 .. 4 r4 + 3 of column cc of the block.
+    // 3b. T_ij = -T_ii X, X = sum_{k=j}^{i-1} L_ik T_kj (wave j, i = j + dist), on 16x16x4 fp32 MFMAs (fp32
+    //     products like the substitution above): A lane (m, grp) = L[16 i + m][16 k + 4 s + grp], B lane (m, grp)
+    //     = T[16 k + 4 s + grp][16 j + m].  X leaves in the C layout (rows 4 grp + r of column m) and passes
+    //     through the wave's scratch block to become the B operand of T_ii X.
 #pragma unroll
     for (int dist = 1; dist < 4; ++dist) {
         const int j = wave, i = wave + dist;
         if (i < 4) {
-            const int r4 = lane >> 4, cc = lane & 15;
-            float x[4] = {0.f, 0.f, 0.f, 0.f};
+            f32x4 x = {0.f, 0.f, 0.f, 0.f};
             for (int k = j; k < i; ++k)
 #pragma unroll
-                for (int q = 0; q < 16; ++q) {
-                    const float tkj = sT[(16 * k + q) * LDT + 16 * j + cc];
+                for (int s = 0; s < 4; ++s)
+                    x = __builtin_amdgcn_mfma_f32_16x16x4f32(sL[(16 * i + m) * LDT + 16 * k + 4 * s + grp],
+                                                            sT[(16 * k + 4 * s + grp) * LDT + 16 * j + m], x, 0, 0, 0);
+            float* xs = sX + wave * 16 * LDX;
 #pragma unroll
-                    for (int rr = 0; rr < 4; ++rr) x[rr] += sL[(16 * i + 4 * r4 + rr) * LDT + 16 * k + q] * tkj;
-                }
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) sX[wave * 16 * LDX + (4 * r4 + rr) * LDX + cc] = x[rr];
+            for (int r = 0; r < 4; ++r) xs[(4 * grp + r) * LDX + m] = x[r];
             __builtin_amdgcn_wave_barrier();
             __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-            float y[4] = {0.f, 0.f, 0.f, 0.f};
+            f32x4 y = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                const float xq = sX[wave * 16 * LDX + q * LDX + cc];
+            for (int s = 0; s < 4; ++s)
+                y = __builtin_amdgcn_mfma_f32_16x16x4f32(sT[(16 * i + m) * LDT + 16 * i + 4 * s + grp],
+                                                        xs[(4 * s + grp) * LDX + m], y, 0, 0, 0);
 #pragma unroll
-                for (int rr = 0; rr < 4; ++rr) y[rr] += sT[(16 * i + 4 * r4 + rr) * LDT + 16 * i + q] * xq;
-            }
-#pragma unroll
-            for (int rr = 0; rr < 4; ++rr) sT[(16 * i + 4 * r4 + rr) * LDT + 16 * j + cc] = -y[rr];
+            for (int r = 0; r < 4; ++r) sT[(16 * i + 4 * grp + r) * LDT + 16 * j + m] = -y[r];
         }
         __syncthreads();
     }
