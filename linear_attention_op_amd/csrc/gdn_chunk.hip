@@ -21,7 +21,8 @@
 //    (sequence, v-head) state; its eight waves own 16 state rows each, held in MFMA accumulators for the
 //    whole launch (state read once, written once).  Per chunk: W S and Q' S (partials over the waves'
 //    rows, summed through LDS), Vn, O += Q' S, S update.  The operands of the next two chunks are in
-//    flight while the current one is computed.  Workgroup ids put the 8 column blocks of a head on one XCD so that they
+//    flight while the current one is computed; each step issues the loads of the chunk two ahead in four
+//    parts spread over its own work.  Workgroup ids put the 8 column blocks of a head on one XCD so that they
 //    share that XCD's L2 copy of W, Q' and the keys.
 //
 // Precision: every product that feeds the state or the output goes through split bf16 (hi + lo, three
@@ -49,8 +50,8 @@ __device__ __forceinline__ void load8(const float* p, float* v) {
 struct ChunkWs {
     u16* Wf;    // [B, Hv, NC][4 rt][8 w][64 lane][8]: W[16 rt + m][16 w + 4 grp + j], hi j < 4, then lo
     u16* Qf;    // the same for Q'
-    u16* Kf;    // [B, Hv, NC][8 w][2 s][64 lane][16]: Kt[16 w + m][32 s + 8 grp + j], hi j < 8, then lo
-    float* Ut;  // [B, Hv, NC][DV][CK]   U, transposed
+    u16* Kf;    // [B, Hv, NC][8 w][2 s][2 plane][64 lane][8]: Kt[16 w + m][32 s + 8 grp + j], plane 0 hi, 1 lo
+    float* U;   // [B, Hv, NC][CK][DV]   U
     float* G;   // [B, Hv, NC, CK]       G (in-chunk cumulative log decay)
     int NC;     // chunks per sequence
 };
@@ -279,7 +280,7 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
 
     // The state pass's key fragments from the transposed keys: thread t writes units t and t + 512 of the
     // chunk's Kf block (unit u: row r = 16 (u / 128) + u % 16, 8-token group 4 ((u / 64) % 2) + (u / 16) % 4;
-    // 16 bytes hi, 16 bytes lo), so that a wave writes 2 KB of contiguous memory.
+    // 16 bytes into each plane of its 64-unit block), so that a wave writes two 1 KB runs.
     {
         u16* Kf = ws.Kf + hc * DK * CK * 2;
 #pragma unroll
@@ -297,8 +298,8 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
                 hi[j] = __builtin_bit_cast(u16, xh);
                 lo[j] = (u16)bf16_bits(x[j] - (float)xh);
             }
-            *reinterpret_cast<u16x8*>(Kf + (size_t)u * 16) = hi;
-            *reinterpret_cast<u16x8*>(Kf + (size_t)u * 16 + 8) = lo;
+            *reinterpret_cast<u16x8*>(Kf + (size_t)(u >> 6) * 1024 + (u & 63) * 8) = hi;
+            *reinterpret_cast<u16x8*>(Kf + (size_t)(u >> 6) * 1024 + 512 + (u & 63) * 8) = lo;
         }
     }
 
@@ -485,9 +486,9 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
         *reinterpret_cast<u16x8*>(Wf + f8) = fw;
         *reinterpret_cast<u16x8*>(Qf + f8) = fq;
     }
-    // 6. U = T (beta V), stored transposed (lane (m, grp): tokens 16 mi + 4 grp + i of column 16 n + m, one
-    //     16-byte store), and the intra-chunk output M2 (beta V) into o
-    float* Ut = ws.Ut + hc * DV * CK;
+    // 6. U = T (beta V) (lane (m, grp): tokens 16 mi + 4 grp + i of column 16 n + m) and the intra-chunk
+    //    output M2 (beta V) into o
+    float* U = ws.U + hc * CK * DV;
 #pragma unroll
     for (int nn = 0; nn < 4; ++nn) {
         const int col = 16 * (4 * hf + nn) + m;
@@ -499,10 +500,10 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
             accT = mfma3(At[s], V, accT);
             accM = mfma3(Am[s], V, accM);
         }
-        *reinterpret_cast<f32x4*>(Ut + (size_t)col * CK + 16 * mi + 4 * grp) = accT;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = 16 * mi + 4 * grp + i;
+            U[r * DV + col] = accT[i];
             if (r < len) a.o[((row0 + r) * Hv + h) * DV + col] = accM[i];
         }
     }
@@ -581,34 +582,65 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
 #pragma unroll
     for (int i = 0; i < 4; ++i) st[i] = S[(size_t)(16 * wave + 4 * grp + i) * DV + n0 + m];
 
-    auto load_ops = [&](int c, StateOps& op) {
+    // One chunk's operands, loaded in four parts (W; Q'; keys and G; U and o).  A step issues the parts of the
+    // chunk two ahead at four points of its own work, so the address units stream them while it computes
+    // rather than stalling every wave on a burst of loads between steps.
+    auto load_part = [&](int c, StateOps& op, auto part) {
+        constexpr int P = decltype(part)::value;
         const size_t hc = ((size_t)b * Hv + h) * ws.NC + c;
-        const int t0 = c * CK, len = min(CK, T - t0);
-        const size_t row0 = (size_t)b * T + t0;
-        const size_t f = hc * CK * DK * 2 + ((size_t)wave * 64 + lane) * 8;
+        if constexpr (P == 0 || P == 1) {
+            const u16* src = (P == 0 ? ws.Wf : ws.Qf) + hc * CK * DK * 2 + ((size_t)wave * 64 + lane) * 8;
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-            op.w[rt] = *reinterpret_cast<const u16x8*>(ws.Wf + f + (size_t)rt * 8 * 64 * 8);
-            op.q[rt] = *reinterpret_cast<const u16x8*>(ws.Qf + f + (size_t)rt * 8 * 64 * 8);
-        }
-        const size_t kf = hc * DK * CK * 2 + ((size_t)wave * 2 * 64 + lane) * 16;
+            for (int rt = 0; rt < 4; ++rt) {
+                const u16x8 v = *reinterpret_cast<const u16x8*>(src + (size_t)rt * 8 * 64 * 8);
+                if constexpr (P == 0) op.w[rt] = v;
+                else op.q[rt] = v;
+            }
+        } else if constexpr (P == 2) {
+            const size_t kf = hc * DK * CK * 2 + (size_t)wave * 2 * 1024 + lane * 8;
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            op.kh[s] = *reinterpret_cast<const u16x8*>(ws.Kf + kf + (size_t)s * 64 * 16);
-            op.kl[s] = *reinterpret_cast<const u16x8*>(ws.Kf + kf + (size_t)s * 64 * 16 + 8);
+            for (int s = 0; s < 2; ++s) {
+                op.kh[s] = *reinterpret_cast<const u16x8*>(ws.Kf + kf + (size_t)s * 1024);
+                op.kl[s] = *reinterpret_cast<const u16x8*>(ws.Kf + kf + (size_t)s * 1024 + 512);
+            }
+            op.glast = ws.G[hc * CK + CK - 1];
+        } else {
+            const int t0 = c * CK, len = min(CK, T - t0);
+            const size_t row0 = (size_t)b * T + t0;
+            const float* U = ws.U + hc * CK * DV + n0 + col;
+            op.u.x = U[(2 * p) * DV];
+            op.u.y = U[(2 * p + 1) * DV];
+            // rows past the end of a partial chunk read a valid row (the value is not used): no branch
+            op.o.x = a.o[((row0 + min(2 * p, len - 1)) * Hv + h) * DV + n0 + col];
+            op.o.y = a.o[((row0 + min(2 * p + 1, len - 1)) * Hv + h) * DV + n0 + col];
         }
-        op.glast = ws.G[hc * CK + CK - 1];
-        op.u = *reinterpret_cast<const float2*>(ws.Ut + hc * DV * CK + (size_t)(n0 + col) * CK + 2 * p);
-        // rows past the end of a partial chunk read a valid row (the value is not used): no branch
-        op.o.x = a.o[((row0 + min(2 * p, len - 1)) * Hv + h) * DV + n0 + col];
-        op.o.y = a.o[((row0 + min(2 * p + 1, len - 1)) * Hv + h) * DV + n0 + col];
+    };
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    using P2 = std::integral_constant<int, 2>;
+    using P3 = std::integral_constant<int, 3>;
+    auto load_ops = [&](int c, StateOps& op) {
+        load_part(c, op, P0{});
+        load_part(c, op, P1{});
+        load_part(c, op, P2{});
+        load_part(c, op, P3{});
+    };
+    // part P of the loads into `nxt` (when LD), fenced so that the scheduler keeps it at this point
+    auto issue = [&](int cn, StateOps& nxt, auto ld, auto part) {
+        if constexpr (decltype(ld)::value) {
+            __builtin_amdgcn_sched_barrier(0);
+            load_part(cn, nxt, part);
+            __builtin_amdgcn_sched_barrier(0);
+        }
     };
 
     // FULL: the chunk has CK tokens (no per-token bounds test)
-    auto step = [&](int c, const StateOps& cur, auto full) {
+    // LD: load chunk cn into nxt along the way
+    auto step = [&](int c, const StateOps& cur, auto full, int cn, StateOps& nxt, auto ld) {
         constexpr bool FULL = decltype(full)::value;
         const int t0 = c * CK, len = FULL ? CK : min(CK, T - t0);
         const size_t row0 = (size_t)b * T + t0;
+        issue(cn, nxt, ld, P0{});
 
         // W S and Q' S over this wave's 16 state rows
         const Split4 Sb = split4(st);
@@ -620,6 +652,7 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
             *reinterpret_cast<f32x4*>(&red[wave][0][m][16 * rt + 4 * grp]) = pw;
             *reinterpret_cast<f32x4*>(&red[wave][1][m][16 * rt + 4 * grp]) = pq;
         }
+        issue(cn, nxt, ld, P1{});
         lds_barrier();
 
         // Vn = U - W S and O += Q' S for tokens 2p, 2p + 1 of column n0 + col
@@ -642,6 +675,7 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
             if (FULL || t < len) op[0] = cur.o.x + sq.x;
             if (FULL || t + 1 < len) op[(size_t)Hv * DV] = cur.o.y + sq.y;
         }
+        issue(cn, nxt, ld, P2{});
         lds_barrier();
 
         // S <- e^{G_last} S + (K e^{G_last - G})^T Vn
@@ -656,6 +690,7 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
             const Split8 vs{__builtin_bit_cast(bf16x8, vh), __builtin_bit_cast(bf16x8, vl)};
             st = mfma3(kt, vs, st);
         }
+        issue(cn, nxt, ld, P3{});
     };
 
     // Operands two chunks ahead: a 3-slot ring, unrolled so that every slot is a fixed set of registers.
@@ -664,25 +699,23 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
     // the remaining (at most 3, the last possibly partial) chunks follow.
     using Full = std::integral_constant<bool, true>;
     using Part = std::integral_constant<bool, false>;
+    using Yes = std::integral_constant<bool, true>;
+    using No = std::integral_constant<bool, false>;
     const int NCF = T / CK;  // full chunks
     StateOps A, B, C;
     load_ops(0, A);
     load_ops(min(1, NC - 1), B);
     int c = 0;
     for (; c + 3 <= NCF; c += 3) {
-        load_ops(min(c + 2, NC - 1), C);
-        step(c, A, Full{});
-        load_ops(min(c + 3, NC - 1), A);
-        step(c + 1, B, Full{});
-        load_ops(min(c + 4, NC - 1), B);
-        step(c + 2, C, Full{});
+        step(c, A, Full{}, min(c + 2, NC - 1), C, Yes{});
+        step(c + 1, B, Full{}, min(c + 3, NC - 1), A, Yes{});
+        step(c + 2, C, Full{}, min(c + 4, NC - 1), B, Yes{});
     }
     if (c < NC) {
-        load_ops(min(c + 2, NC - 1), C);
-        step(c, A, Part{});
+        step(c, A, Part{}, min(c + 2, NC - 1), C, Yes{});
         if (c + 1 < NC) {
-            step(c + 1, B, Part{});
-            if (c + 2 < NC) step(c + 2, C, Part{});
+            step(c + 1, B, Part{}, 0, A, No{});
+            if (c + 2 < NC) step(c + 2, C, Part{}, 0, A, No{});
         }
     }
 
@@ -703,7 +736,7 @@ static ChunkWs chunk_ws(const DeltaArgs& a, void* workspace) {
     ws.Qf = p, p += n * CK * D * 2;
     ws.Kf = p, p += n * CK * D * 2;
     float* f = reinterpret_cast<float*>(p);
-    ws.Ut = f, f += n * CK * D;
+    ws.U = f, f += n * CK * D;
     ws.G = f;
     return ws;
 }
