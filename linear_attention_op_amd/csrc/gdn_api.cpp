@@ -163,6 +163,8 @@ hipError_t in_proj_rows(const gdn_layer* L, const void* x, int xl, int M, float*
     hipError_t e = fp8(L) ? gdn::launch_linear(x, xl, L->w_in8, gdn::W_F8, L->s_in, M, N1, H, P, L->NP, gdn::OUT_F32, st)
                           : gdn::launch_linear(x, xl, L->w_in, gdn::W_FRAG, nullptr, M, N1, H, P, L->NP, gdn::OUT_F32, st);
     if (e != hipSuccess) return e;
+    // the a | b rows: for prefills the GEMV with the roles swapped (the activations streamed once)
+    if (M > 64) return gdn::launch_linear_rows_t(x, L->w_ab, nab, M, H, P + N1, L->NP, st);
     return gdn::launch_linear(x, xl, L->w_ab, gdn::W_FRAG, nullptr, M, nab, H, P + N1, L->NP, gdn::OUT_F32, st);
 }
 

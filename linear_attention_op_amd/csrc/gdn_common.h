@@ -120,7 +120,8 @@ __device__ __forceinline__ float softplusf_(float x) { return x > 20.0f ? x : lo
 // ------------------------------------------------------------------------------------------------
 namespace gdn {
 
-enum OutKind { OUT_F32 = 0, OUT_BF16 = 1 };
+// OUT_F32_T: fp32, element (m, n) stored at n * ldy + m (the transposed GEMV below)
+enum OutKind { OUT_F32 = 0, OUT_BF16 = 1, OUT_F32_T = 2 };
 // Weight layouts: W_ROW = row-major bf16 [N, K]; W_FRAG = bf16 MFMA-fragment blocks; W_F8 = E4M3 fragment
 // blocks with one fp32 scale per row (see gdn_linear.hip).
 enum WLayout { W_ROW = 0, W_FRAG = 1, W_F8 = 2 };
@@ -130,6 +131,11 @@ enum WLayout { W_ROW = 0, W_FRAG = 1, W_F8 = 2 };
 // activations only for M <= 64).
 hipError_t launch_linear(const void* x, int xlayout, const void* w, int wlayout, const float* w_scale, int M, int N,
                          int K, void* y, int ldy, int out_kind, hipStream_t stream);
+// y[n * ldy + m] = sum_k w[m][k] x[n][k] for a few weight rows (M <= 64, w in W_FRAG layout) against many
+// row-major activation rows x [N, K] (K % 32 == 0): the GEMV with the roles swapped, so that a skinny
+// projection of a long prefill (the a | b rows) streams the activations once over every CU.
+hipError_t launch_linear_rows_t(const void* x, const void* w, int M, int N, int K, float* y, int ldy,
+                                hipStream_t stream);
 // Decode in_proj (M <= 64; activations in W_FRAG layout, or row-major W_ROW for M <= 16): rows [0, N1) of w
 // (W_FRAG, or W_F8 with w_scale) into P (fp32, row stride ldp) with the workgroups balanced over the CUs;
 // the N2 rows of w2 (W_FRAG) as ab_splits partial sums over k ranges into Pab [ab_splits][M][N2] (the

@@ -31,7 +31,7 @@ namespace {
 
 template <int OUT>
 __device__ __forceinline__ void store_out(void* y, size_t idx, float v) {
-    if (OUT == OUT_F32)
+    if (OUT == OUT_F32 || OUT == OUT_F32_T)
         reinterpret_cast<float*>(y)[idx] = v;
     else
         reinterpret_cast<u16*>(y)[idx] = f2bf(v);
@@ -137,14 +137,16 @@ __device__ __forceinline__ void gemv_finish(f32x4 (&acc)[NTS][MT], float* red_ld
                 for (int i = 0; i < 4; ++i) red[wave][16 * mt + r][16 * t + 4 * g + i] = acc[t][mt][i];
     }
     __syncthreads();
+    // OUT_F32_T: x rows fastest, so that a wave writes whole output rows
+    constexpr bool TR = OUT == OUT_F32_T;
     for (int e = threadIdx.x; e < BM * BN; e += NW * 64) {
-        const int m = e / BN, nl = e % BN, n = n0 + nl;
+        const int m = TR ? e % BM : e / BN, nl = TR ? e / BM : e % BN, n = n0 + nl;
         if (m >= M || n >= N) continue;
         float s = 0.f;
 #pragma unroll
         for (int wv = 0; wv < HALF; ++wv) s += red[wv][m][nl];
         if (scale) s *= scale[n];
-        store_out<OUT>(y, (size_t)m * ldy + n, s);
+        store_out<OUT>(y, TR ? (size_t)n * ldy + m : (size_t)m * ldy + n, s);
     }
 }
 
@@ -715,7 +717,10 @@ hipError_t gemv(const LinArgs& a, hipStream_t stream) {
     constexpr int PD = WL == W_F8 ? 2 : 4;  // an E4M3 ring slot covers two k-steps
     const dim3 grid((a.N + NTS * 16 - 1) / (NTS * 16));
     const dim3 block(NW * 64);
-    if (a.out_kind == OUT_F32)
+    if (a.out_kind == OUT_F32_T)
+        hipLaunchKernelGGL((gemv_kernel<NTS, MT, NW, PD, OUT_F32_T, WL, XL>), grid, block, 0, stream, (const u16*)a.x,
+                           a.w, a.scale, a.M, a.N, a.K, a.y, a.ldy);
+    else if (a.out_kind == OUT_F32)
         hipLaunchKernelGGL((gemv_kernel<NTS, MT, NW, PD, OUT_F32, WL, XL>), grid, block, 0, stream, (const u16*)a.x,
                            a.w, a.scale, a.M, a.N, a.K, a.y, a.ldy);
     else
@@ -864,6 +869,15 @@ hipError_t launch_in_proj_decode(const void* x, int xlayout, const void* w, int 
     const DecodeArgs a{(const u16*)x, w, w_scale, (const u16*)w2, M, N1, N2, K, 0, ab_splits, P, ldp, Pab};
     if (wlayout == W_F8) return in_proj_decode_wl<W_F8>(a, xlayout, stream);
     return in_proj_decode_wl<W_FRAG>(a, xlayout, stream);
+}
+
+hipError_t launch_linear_rows_t(const void* x, const void* w, int M, int N, int K, float* y, int ldy,
+                                hipStream_t stream) {
+    if (M <= 0 || N <= 0) return hipSuccess;
+    if (M > 64 || K % 32 || ldy < M) return hipErrorInvalidValue;
+    // the GEMV's activations are the W_FRAG rows w, its streamed weights the row-major rows x
+    const LinArgs a{w, x, nullptr, M, N, K, y, ldy, OUT_F32_T};
+    return gemv_m<W_ROW, W_FRAG>(a, stream);
 }
 
 hipError_t launch_linear(const void* x, int xlayout, const void* w, int wlayout, const float* w_scale, int M, int N,
