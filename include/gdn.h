@@ -65,11 +65,15 @@ typedef struct gdn_weights {
 } gdn_weights;
 
 /* Weight storage of a layer: the reference's weight_dtype argument (9B/gdn_layer.py:55, 115-120: w_in and
- * w_out in ttnn.bfloat16 or ttnn.bfloat8_b, w_ab always bfloat16; 0.8B/gdn_l1.py:79-80). */
+ * w_out in ttnn.bfloat16, ttnn.bfloat8_b or ttnn.bfloat4_b, w_ab always bfloat16; 0.8B/gdn_l1.py:79-80). */
 typedef enum gdn_weight_format {
     GDN_WEIGHTS_BF16 = 0,      /* the bf16 weights as given */
     GDN_WEIGHTS_FP8_E4M3 = 1,  /* in_proj q|k|v|z rows and out_proj as OCP E4M3 codes with one fp32 scale per
                                 * output row (absmax / 448, see gdn_quantize_fp8); the a|b rows stay bf16.
+                                * Activations and accumulation are unchanged (bf16 x bf16 MFMA, fp32). */
+    GDN_WEIGHTS_MXFP4 = 2,     /* the counterpart of bfloat4_b: the same matrices as OCP MXFP4, E2M1 codes with
+                                * one E8M0 scale per row and 32 columns (see gdn_quantize_mxfp4); the a|b
+                                * rows stay bf16.
                                 * Activations and accumulation are unchanged (bf16 x bf16 MFMA, fp32). */
 } gdn_weight_format;
 
@@ -214,6 +218,15 @@ int gdn_linear_bf16(const void* x, const void* w, int M, int N, int K, void* y, 
  * (1 for an all-zero row) and q[n, k] = round-to-nearest-even(w[n, k] / scale[n]), saturating at +-448.
  * Row n of the dequantized matrix is decode(q[n, :]) * scale[n]. */
 int gdn_quantize_fp8(const void* w, int N, int K, void* q, float* scale, void* stream);
+
+/* The MXFP4 weight quantizer of GDN_WEIGHTS_MXFP4 (the reference's conversion to bfloat4_b, ttnn.from_torch(...,
+ * dtype=weight_dtype) at 0.8B/gdn_l1.py:79-80, re-specified for OCP MXFP4): w bf16 [N, K] (device, K % 32 ==
+ * 0) -> q uint8 [N, K / 2] E2M1 codes, two per byte (column 2i in the low nibble), and scale uint8 [N, K / 32]
+ * E8M0 codes, block j of row n (columns 32 j .. 32 j + 31) scaled by X = 2^(floor(log2 max |w|) - 2)
+ * (exponent clamped to [-127, 127], code = exponent + 127; 0 for an all-zero block) and each value coded as
+ * round-to-nearest-even(w / X) on the E2M1 grid {0, 0.5, 1, 1.5, 2, 3, 4, 6}, saturating at +-6.  The
+ * dequantized value is decode(code) * 2^(scale code - 127). */
+int gdn_quantize_mxfp4(const void* w, int N, int K, void* q, void* scale, void* stream);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* gdn_last_error(void);

@@ -64,6 +64,10 @@ struct gdn_layer {
     float* s_in = nullptr;    // fp8: per-row scales of w_in8
     u8* w_out8 = nullptr;     // fp8: [H, Vd] W_F8 layout
     float* s_out = nullptr;   // fp8: per-row scales of w_out8
+    u8* w_in4 = nullptr;      // mxfp4: [CD + Vd, H] rows q | k | v | z, W_F4 layout
+    u8* s_in4 = nullptr;      // mxfp4: E8M0 scale codes of w_in4 (f4_scale_offset order)
+    u8* w_out4 = nullptr;     // mxfp4: [H, Vd] W_F4 layout
+    u8* s_out4 = nullptr;     // mxfp4: scale codes of w_out4
     float4* conv_w = nullptr; // [CD] taps
     float* neg_A = nullptr;   // [nv]
     float* dt_bias = nullptr; // [nv]
@@ -150,6 +154,23 @@ hipError_t run_delta(gdn_layer* L, const gdn::DeltaArgs& r, hipStream_t st) {
 }
 
 bool fp8(const gdn_layer* L) { return L->wfmt == GDN_WEIGHTS_FP8_E4M3; }
+bool fp4(const gdn_layer* L) { return L->wfmt == GDN_WEIGHTS_MXFP4; }
+// the q | k | v | z rows of in_proj, and out_proj, as stored: (weights, layout, scales)
+struct QW {
+    const void* w;
+    int layout;
+    const float* scale;
+};
+QW w_in_q(const gdn_layer* L) {
+    if (fp8(L)) return {L->w_in8, gdn::W_F8, L->s_in};
+    if (fp4(L)) return {L->w_in4, gdn::W_F4, reinterpret_cast<const float*>(L->s_in4)};
+    return {L->w_in, gdn::W_FRAG, nullptr};
+}
+QW w_out_q(const gdn_layer* L) {
+    if (fp8(L)) return {L->w_out8, gdn::W_F8, L->s_out};
+    if (fp4(L)) return {L->w_out4, gdn::W_F4, reinterpret_cast<const float*>(L->s_out4)};
+    return {L->w_out, gdn::W_FRAG, nullptr};
+}
 
 // in_proj of M rows (x row-major, or W_FRAG for M <= 64) into P [M, NP] (9B/gdn_layer.py:255-259).  FP8
 // layers run the q | k | v | z rows on E4M3 weights and the a | b rows on bf16 ones.
@@ -158,10 +179,10 @@ bool fp8(const gdn_layer* L) { return L->wfmt == GDN_WEIGHTS_FP8_E4M3; }
 // full round of workgroups for 64 useful columns.
 hipError_t in_proj_rows(const gdn_layer* L, const void* x, int xl, int M, float* P, hipStream_t st) {
     const int H = L->d.hidden, N1 = L->CD + L->Vd, nab = 2 * L->d.num_v_heads;
-    if (!fp8(L) && M <= 64)
+    if (L->wfmt == GDN_WEIGHTS_BF16 && M <= 64)
         return gdn::launch_linear(x, xl, L->w_in, gdn::W_FRAG, nullptr, M, L->NP, H, P, L->NP, gdn::OUT_F32, st);
-    hipError_t e = fp8(L) ? gdn::launch_linear(x, xl, L->w_in8, gdn::W_F8, L->s_in, M, N1, H, P, L->NP, gdn::OUT_F32, st)
-                          : gdn::launch_linear(x, xl, L->w_in, gdn::W_FRAG, nullptr, M, N1, H, P, L->NP, gdn::OUT_F32, st);
+    const QW q = w_in_q(L);
+    hipError_t e = gdn::launch_linear(x, xl, q.w, q.layout, q.scale, M, N1, H, P, L->NP, gdn::OUT_F32, st);
     if (e != hipSuccess) return e;
     // the a | b rows: for prefills the GEMV with the roles swapped (the activations streamed once)
     if (M > 64) return gdn::launch_linear_rows_t(x, L->w_ab, nab, M, H, P + N1, L->NP, st);
@@ -171,8 +192,8 @@ hipError_t in_proj_rows(const gdn_layer* L, const void* x, int xl, int M, float*
 // out_proj of M rows of y (row-major, or W_FRAG for M <= 64) into out bf16 [M, H] (9B/gdn_layer.py:272-276).
 hipError_t out_proj_rows(const gdn_layer* L, const void* y, int yl, int M, void* out, hipStream_t st) {
     const int H = L->d.hidden;
-    if (fp8(L)) return gdn::launch_linear(y, yl, L->w_out8, gdn::W_F8, L->s_out, M, H, L->Vd, out, H, gdn::OUT_BF16, st);
-    return gdn::launch_linear(y, yl, L->w_out, gdn::W_FRAG, nullptr, M, H, L->Vd, out, H, gdn::OUT_BF16, st);
+    const QW q = w_out_q(L);
+    return gdn::launch_linear(y, yl, q.w, q.layout, q.scale, M, H, L->Vd, out, H, gdn::OUT_BF16, st);
 }
 
 // A group of sequences of one launch with the same length: rows [row0, row0 + B T) of the launch,
@@ -205,12 +226,12 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, u16* o
     // up to 16 rows the decode in_proj reads the activations row-major: re-tiling them would cost a launch
     const bool x_rows = ab_split && M <= 16;
     if (frag && !x_rows) HIP_OK(gdn::launch_frag_tile(x, M, d.hidden, L->x_frag, st));
-    if (ab_split)
+    if (ab_split) {
+        const QW q = w_in_q(L);
         HIP_OK(gdn::launch_in_proj_decode(x_rows ? (const void*)x : L->x_frag, x_rows ? gdn::W_ROW : gdn::W_FRAG,
-                                          fp8(L) ? (const void*)L->w_in8 : L->w_in, fp8(L) ? gdn::W_F8 : gdn::W_FRAG,
-                                          L->s_in, L->w_ab, M, L->CD + Vd, 2 * nv, d.hidden, L->P, L->NP, L->ab,
-                                          kAbSplits, st));
-    else
+                                          q.w, q.layout, q.scale, L->w_ab, M, L->CD + Vd, 2 * nv, d.hidden, L->P,
+                                          L->NP, L->ab, kAbSplits, st));
+    } else
         HIP_OK(in_proj_rows(L, frag ? L->x_frag : x, frag ? gdn::W_FRAG : gdn::W_ROW, M, L->P, st));
     if (ev[1]) HIP_OK(hipEventRecord(ev[1], st));
     for (int gi = 0; gi < ng; ++gi) {
@@ -332,7 +353,7 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
     *out = nullptr;
     int rc = check_dims(dims);
     if (rc) return rc;
-    if (wfmt != GDN_WEIGHTS_BF16 && wfmt != GDN_WEIGHTS_FP8_E4M3)
+    if (wfmt != GDN_WEIGHTS_BF16 && wfmt != GDN_WEIGHTS_FP8_E4M3 && wfmt != GDN_WEIGHTS_MXFP4)
         return fail(GDN_ERR_INVALID_ARG, "unknown weight format %d", wfmt);
     if (!w || !w->in_proj_qkv || !w->in_proj_z || !w->in_proj_a || !w->in_proj_b || !w->conv1d || !w->A_log ||
         !w->dt_bias || !w->norm_weight || !w->out_proj)
@@ -360,6 +381,13 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
         take(L->alloc(&L->w_ab, gdn::frag_elems(2 * nv, H)));
         take(L->alloc(&L->w_out8, gdn::frag_elems(H, L->Vd)));
         take(L->alloc(&L->s_out, (size_t)H));
+    } else if (wfmt == GDN_WEIGHTS_MXFP4) {
+        // codes: half a byte per weight; scales: a byte per 32 (rows padded to 16)
+        take(L->alloc(&L->w_in4, gdn::frag_elems(N1, H) / 2));
+        take(L->alloc(&L->s_in4, gdn::frag_elems(N1, H) / 32));
+        take(L->alloc(&L->w_ab, gdn::frag_elems(2 * nv, H)));
+        take(L->alloc(&L->w_out4, gdn::frag_elems(H, L->Vd) / 2));
+        take(L->alloc(&L->s_out4, gdn::frag_elems(H, L->Vd) / 32));
     } else {
         take(L->alloc(&L->w_in, gdn::frag_elems(L->NP, H)));
         take(L->alloc(&L->w_out, gdn::frag_elems(H, L->Vd)));
@@ -409,8 +437,8 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
 
     // fused in_proj rows: q | k | v (in_proj_qkv), z, a, b -- one weight stream per token.  The HF
     // row-major weights are staged in a temporary device buffer and re-laid out into fragment blocks
-    // (FP8: the q | k | v | z rows and out_proj quantized to E4M3 with per-row scales, as the reference
-    // converts w_in and w_out to its weight_dtype and keeps w_ab bf16, 9B/gdn_layer.py:115-120).
+    // (FP8 / MXFP4: the q | k | v | z rows and out_proj quantized to E4M3 with per-row scales or to MXFP4, as
+    // the reference converts w_in and w_out to its weight_dtype and keeps w_ab bf16, 9B/gdn_layer.py:115-120).
     const size_t row = (size_t)H * sizeof(u16);
     u16* stage = nullptr;
     e = hipMalloc(&stage, std::max((size_t)L->NP * H, (size_t)H * L->Vd) * sizeof(u16));
@@ -423,6 +451,9 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
         if (wfmt == GDN_WEIGHTS_FP8_E4M3) {
             e = gdn::launch_quantize_e4m3(stage, N1, H, L->w_in8, L->s_in, 1, nullptr);
             if (e == hipSuccess) e = gdn::launch_frag_tile(stage + (size_t)N1 * H, 2 * nv, H, L->w_ab, nullptr);
+        } else if (wfmt == GDN_WEIGHTS_MXFP4) {
+            e = gdn::launch_quantize_mxfp4(stage, N1, H, L->w_in4, L->s_in4, 1, nullptr);
+            if (e == hipSuccess) e = gdn::launch_frag_tile(stage + (size_t)N1 * H, 2 * nv, H, L->w_ab, nullptr);
         } else {
             e = gdn::launch_frag_tile(stage, L->NP, H, L->w_in, nullptr);
         }
@@ -433,6 +464,8 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
     if (e == hipSuccess) {
         if (wfmt == GDN_WEIGHTS_FP8_E4M3)
             e = gdn::launch_quantize_e4m3(stage, H, L->Vd, L->w_out8, L->s_out, 1, nullptr);
+        else if (wfmt == GDN_WEIGHTS_MXFP4)
+            e = gdn::launch_quantize_mxfp4(stage, H, L->Vd, L->w_out4, L->s_out4, 1, nullptr);
         else
             e = gdn::launch_frag_tile(stage, H, L->Vd, L->w_out, nullptr);
     }
@@ -654,6 +687,14 @@ int gdn_quantize_fp8(const void* w, int N, int K, void* q, float* scale, void* s
     if (!w || !q || !scale) return fail(GDN_ERR_INVALID_ARG, "gdn_quantize_fp8: NULL argument");
     if (N <= 0 || K <= 0) return fail(GDN_ERR_SHAPE, "N=%d K=%d", N, K);
     HIP_OK(gdn::launch_quantize_e4m3(w, N, K, (u8*)q, scale, 0, as_stream(stream)));
+    return GDN_OK;
+}
+
+int gdn_quantize_mxfp4(const void* w, int N, int K, void* q, void* scale, void* stream) {
+    if (!w || !q || !scale) return fail(GDN_ERR_INVALID_ARG, "gdn_quantize_mxfp4: NULL argument");
+    if (N <= 0 || K <= 0) return fail(GDN_ERR_SHAPE, "N=%d K=%d", N, K);
+    if (K % 32) return fail(GDN_ERR_UNSUPPORTED, "K=%d is not a multiple of 32", K);
+    HIP_OK(gdn::launch_quantize_mxfp4(w, N, K, (u8*)q, (u8*)scale, 0, as_stream(stream)));
     return GDN_OK;
 }
 

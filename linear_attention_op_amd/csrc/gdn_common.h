@@ -103,6 +103,38 @@ __device__ __forceinline__ void e4m3x16_to_bf16(const u32x4 q, bf16x8& lo, bf16x
     hi = bf16x8{p[4][0], p[4][1], p[5][0], p[5][1], p[6][0], p[6][1], p[7][0], p[7][1]};
 }
 
+// ---- MXFP4 (OCP Microscaling: E2M1 values 0, 0.5, 1, 1.5, 2, 3, 4, 6 with one E8M0 scale per 32) -------
+// E2M1 code of one value already divided by its block scale: nearest, ties to the even mantissa,
+// saturating to +-6 (the decision thresholds of that rounding on the E2M1 grid).
+__host__ __device__ __forceinline__ uint32_t e2m1_code(float v) {
+    const float a = fabsf(v);
+    const uint32_t c = a <= 0.25f ? 0u : a < 0.75f ? 1u : a <= 1.25f ? 2u : a < 1.75f ? 3u
+                     : a <= 2.5f ? 4u : a < 3.5f ? 5u : a <= 5.0f ? 6u : 7u;
+    return (signbit(v) ? 8u : 0u) | c;
+}
+// E8M0 exponent byte of the block scale 2^(floor(log2 amax) - 2), clamped to [-127, 127]; 0 for amax 0.
+__host__ __device__ __forceinline__ uint32_t mx_scale_code(float amax) {
+    if (!(amax > 0.f)) return 0u;
+    union { float f; uint32_t u; } b{amax};
+    int e = (int)((b.u >> 23) & 0xffu) - 127;  // floor(log2 amax) for a normal amax
+    if (((b.u >> 23) & 0xffu) == 0u) e = -127;  // subnormal amax: below 2^-126, the clamp applies
+    int x = e - 2;
+    x = x < -127 ? -127 : (x > 127 ? 127 : x);
+    return (uint32_t)(x + 127);
+}
+// The scale of an E8M0 byte as a float (2^-127 for code 0, a subnormal).
+__device__ __forceinline__ float e8m0_value(uint32_t e) { return __uint_as_float(e ? e << 23 : 0x00400000u); }
+// 8 E2M1 codes (4 bytes, two per byte, low nibble first, in k order) times `scale` -> 8 bf16, exact for
+// scales of at least 2^-126 (every such product is a bf16 value).
+__device__ __forceinline__ bf16x8 e2m1x8_to_bf16(uint32_t q, float scale) {
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    const bf16x2 p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, scale, 0);
+    const bf16x2 p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, scale, 1);
+    const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, scale, 2);
+    const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, scale, 3);
+    return bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
 // Workgroup barrier for LDS traffic only: unlike __syncthreads() it does not wait for outstanding
 // global loads, so loads issued for the next step stay in flight across it.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
@@ -123,11 +155,13 @@ namespace gdn {
 // OUT_F32_T: fp32, element (m, n) stored at n * ldy + m (the transposed GEMV below)
 enum OutKind { OUT_F32 = 0, OUT_BF16 = 1, OUT_F32_T = 2 };
 // Weight layouts: W_ROW = row-major bf16 [N, K]; W_FRAG = bf16 MFMA-fragment blocks; W_F8 = E4M3 fragment
-// blocks with one fp32 scale per row (see gdn_linear.hip).
-enum WLayout { W_ROW = 0, W_FRAG = 1, W_F8 = 2 };
+// blocks with one fp32 scale per row; W_F4 = MXFP4 fragment blocks with one E8M0 scale per row and 32
+// columns (see gdn_linear.hip).
+enum WLayout { W_ROW = 0, W_FRAG = 1, W_F8 = 2, W_F4 = 3 };
 
 // y[M, N] (row stride ldy) = x[M, K] . w[N, K]^T ; bf16 activations, fp32 accumulation; K % 128 == 0.
-// w in layout `wlayout` (W_F8: w = E4M3 codes, row n scaled by w_scale[n]); x in `xlayout` (W_FRAG
+// w in layout `wlayout` (W_F8: w = E4M3 codes, row n scaled by w_scale[n]; W_F4: w = E2M1 codes, w_scale
+// the E8M0 scale codes in f4_scale_offset order, passed through this pointer); x in `xlayout` (W_FRAG
 // activations only for M <= 64).
 hipError_t launch_linear(const void* x, int xlayout, const void* w, int wlayout, const float* w_scale, int M, int N,
                          int K, void* y, int ldy, int out_kind, hipStream_t stream);
@@ -137,7 +171,7 @@ hipError_t launch_linear(const void* x, int xlayout, const void* w, int wlayout,
 hipError_t launch_linear_rows_t(const void* x, const void* w, int M, int N, int K, float* y, int ldy,
                                 hipStream_t stream);
 // Decode in_proj (M <= 64; activations in W_FRAG layout, or row-major W_ROW for M <= 16): rows [0, N1) of w
-// (W_FRAG, or W_F8 with w_scale) into P (fp32, row stride ldp) with the workgroups balanced over the CUs;
+// (W_FRAG, or W_F8 / W_F4 with w_scale) into P (fp32, row stride ldp) with the workgroups balanced over the CUs;
 // the N2 rows of w2 (W_FRAG) as ab_splits partial sums over k ranges into Pab [ab_splits][M][N2] (the
 // consumer adds the slices).  N1 % 16 == 0.
 hipError_t launch_in_proj_decode(const void* x, int xlayout, const void* w, int wlayout, const float* w_scale,
@@ -155,6 +189,22 @@ hipError_t launch_quantize_e4m3(const void* w, int N, int K, u8* q, float* scale
 __host__ __device__ __forceinline__ size_t f8_offset(int n, int k, int K) {
     return ((size_t)(n >> 4) * (K >> 6) + (k >> 6)) * 1024 + ((((k >> 3) & 3) << 4) + (n & 15)) * 16 +
            ((k >> 5) & 1) * 8 + (k & 7);
+}
+// MXFP4 weights: codes in W_F4 layout (to_frag != 0; rows padded to 16 with zero codes and scale code 0,
+// K % 128 == 0) or row-major [N, K / 2] bytes (low nibble = even column), with their E8M0 scale codes in
+// the matching order (f4_scale_offset, or row-major [N, K / 32]).
+hipError_t launch_quantize_mxfp4(const void* w, int N, int K, u8* q, u8* scale, int to_frag, hipStream_t stream);
+// W_F4 layout: blocks of 16 rows x 128 columns (1 KB), lane l = 16 g + r of block holding the 32 codes
+// W[16 nt + r][128 kb + 32 h + 8 g + j] (h, j < 4, 8) in its 16 bytes at byte 4 h + j / 2, nibble j % 2 --
+// four consecutive MFMA A operands per 16-byte load.  Byte offset of (row n, column k):
+__host__ __device__ __forceinline__ size_t f4_offset(int n, int k, int K) {
+    return ((size_t)(n >> 4) * (K >> 7) + (k >> 7)) * 1024 + ((((k >> 3) & 3) << 4) + (n & 15)) * 16 +
+           ((k >> 5) & 3) * 4 + ((k & 7) >> 1);
+}
+// Scale codes of W_F4: [N / 16][K / 128][16 rows][4 k-steps] bytes, so the lane of row r reads the scales of
+// its four k-steps as one 32-bit word.  Byte offset of the scale of (row n, 32-column block kq):
+__host__ __device__ __forceinline__ size_t f4_scale_offset(int n, int kq, int K) {
+    return (((size_t)(n >> 4) * (K >> 7) + (kq >> 2)) * 16 + (n & 15)) * 4 + (kq & 3);
 }
 // Convert a row-major device matrix [N, K] into W_FRAG layout (frag_elems(N, K) elements).
 hipError_t launch_frag_tile(const void* w, int N, int K, void* wf, hipStream_t stream);

@@ -11,6 +11,11 @@
 // W[16 nt + r][64 kp + 32 h + 8 g + j] (h = 0, 1), i.e. the A operands of two consecutive k-steps, plus one
 // fp32 scale per row applied to the finished dot product.  Codes are widened to bf16 in registers
 // (v_cvt_scalef32_pk_bf16_fp8, exact), so the MFMA work is unchanged and the weight stream halves.
+// W_F4 holds MXFP4 weights (the counterpart of the reference's bfloat4_b, 0.8B/gdn_l1.py:79-80): E2M1 codes
+// in blocks of 16 rows x 128 columns, lane l = 16 g + r holding the 32 codes W[16 nt + r][128 kb + 32 h +
+// 8 g + j] (four consecutive k-steps), and one E8M0 scale per row and 32 columns, four to a 32-bit word per
+// lane; codes are widened to bf16 times their scale in registers (v_cvt_scalef32_pk_bf16_fp4, exact), so
+// the weight stream is a quarter of bf16's plus 1/32 for the scales.
 //
 // Kernels (bf16 MFMA, fp32 accumulation):
 //  * gemv_kernel (M <= 64, decode): HBM-bound weight streaming.  A workgroup owns 16 NTS rows of w; its
@@ -76,6 +81,41 @@ __global__ __launch_bounds__(256) void quantize_e4m3_kernel(const u16* __restric
     for (int k = threadIdx.x; k < K; k += 256) {
         const u8 c = real ? (u8)e4m3_code(bf2f(w[(size_t)n * K + k]) / sc) : (u8)0;
         q[FRAG ? f8_offset(n, k, K) : (size_t)n * K + k] = c;
+    }
+}
+
+// MXFP4 quantizer: one workgroup per (padded) row, a thread per 32-column block: scale code from the
+// block's largest magnitude, E2M1 codes of w / 2^(code - 127) (the division is exact: a power of two).
+template <bool FRAG>
+__global__ __launch_bounds__(256) void quantize_mxfp4_kernel(const u16* __restrict__ w, int N, int K,
+                                                             u8* __restrict__ q, u8* __restrict__ scale) {
+    const int n = blockIdx.x;
+    const bool real = n < N;
+    for (int kq = threadIdx.x; kq < (K >> 5); kq += 256) {
+        float v[32];
+        float m = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u16x8 x = real ? *reinterpret_cast<const u16x8*>(w + (size_t)n * K + 32 * kq + 8 * i) : u16x8{};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[8 * i + j] = bf2f(x[j]), m = fmaxf(m, fabsf(v[8 * i + j]));
+        }
+        const uint32_t e = mx_scale_code(m);
+        uint32_t wd[4];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            wd[g] = 0;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) wd[g] |= e2m1_code(ldexpf(v[8 * g + j], 127 - (int)e)) << (4 * j);
+        }
+        if (FRAG) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) *reinterpret_cast<uint32_t*>(q + f4_offset(n, 32 * kq + 8 * g, K)) = wd[g];
+            scale[f4_scale_offset(n, kq, K)] = (u8)e;
+        } else {
+            *reinterpret_cast<u32x4*>(q + (size_t)n * (K >> 1) + 16 * kq) = u32x4{wd[0], wd[1], wd[2], wd[3]};
+            scale[(size_t)n * (K >> 5) + kq] = (u8)e;
+        }
     }
 }
 
@@ -314,6 +354,88 @@ __device__ __forceinline__ void gemv_block_f8(const u16* __restrict__ x, const u
     gemv_finish<NTS, MT, NW, OUT>(acc, red, M, N, y, ldy, n0, scale);
 }
 
+// The same on W_F4 weights: one 16-byte load per row tile covers a k-quad (4 k-steps, 128 columns) and its
+// four scales one 32-bit load; weights two quads ahead, x fragments one quad (4 k-steps) ahead.  K % 128
+// == 0; the k range is [kbb, kbb + kbn) in k-quads.
+template <int NTS, int MT, int NW, int OUT, int XL>
+__device__ __forceinline__ void gemv_block_f4(const u16* __restrict__ x, const u8* __restrict__ w,
+                                              const uint32_t* __restrict__ sw, int M, int N, int K,
+                                              void* __restrict__ y, int ldy, int n0, int kbb, int kbn, float* red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int KQ = K >> 5, KB = K >> 7;
+    const int kb_per = (kbn + NW - 1) / NW;
+    const int kb0 = kbb + min(kbn, wave * kb_per);
+    const int nq = kbb + min(kbn, (wave + 1) * kb_per) - kb0;
+    const int NT = (N + 15) >> 4;
+
+    const u8* wp[NTS];
+    const uint32_t* sp[NTS];
+#pragma unroll
+    for (int t = 0; t < NTS; ++t) {
+        const size_t blk = (size_t)min((n0 >> 4) + t, NT - 1) * KB + kb0;
+        wp[t] = w + blk * 1024 + lane * 16;
+        sp[t] = sw + blk * 16 + r;
+    }
+    const u16* xp[MT];
+    bool xv[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        if (XL == W_FRAG) {
+            xv[mt] = true;
+            xp[mt] = x + ((size_t)mt * KQ + 4 * kb0) * 512 + lane * 8;
+        } else {
+            xv[mt] = 16 * mt + r < M;
+            xp[mt] = x + (size_t)min(16 * mt + r, M - 1) * K + 128 * kb0 + 8 * g;
+        }
+    }
+    constexpr size_t XSTEP = XL == W_FRAG ? 512 : 32;
+
+    u32x4 wq[2][NTS];
+    uint32_t ws[2][NTS];
+    bf16x8 xb[4][MT];
+    const bf16x8 zero8 = {};
+    auto wload = [&](int slot, int qd) {
+#pragma unroll
+        for (int t = 0; t < NTS; ++t) {
+            wq[slot][t] = ldw8(wp[t] + (size_t)qd * 1024);
+            ws[slot][t] = sp[t][(size_t)qd * 16];
+        }
+    };
+    auto xload = [&](int h, int s) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+            xb[h][mt] = xv[mt] ? *reinterpret_cast<const bf16x8*>(xp[mt] + (size_t)s * XSTEP) : zero8;
+    };
+    if (nq > 0) wload(0, 0);
+    if (nq > 1) wload(1, 1);
+    if (nq > 0) {
+#pragma unroll
+        for (int h = 0; h < 4; ++h) xload(h, h);
+    }
+    f32x4 acc[NTS][MT];
+#pragma unroll
+    for (int t = 0; t < NTS; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    for (int qd = 0; qd < nq; ++qd) {
+        const int slot = qd & 1;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+#pragma unroll
+            for (int t = 0; t < NTS; ++t) {
+                const bf16x8 a = e2m1x8_to_bf16(wq[slot][t][h], e8m0_value((ws[slot][t] >> (8 * h)) & 0xffu));
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) acc[t][mt] = mfma16(a, xb[h][mt], acc[t][mt]);
+            }
+            if (qd + 1 < nq) xload(h, 4 * (qd + 1) + h);
+        }
+        if (qd + 2 < nq) wload(slot, qd + 2);
+    }
+    gemv_finish<NTS, MT, NW, OUT>(acc, red, M, N, y, ldy, n0, nullptr);
+}
+
 template <int NTS, int MT, int NW, int PD, int OUT, int WL, int XL>
 __global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x, const void* __restrict__ w,
                                                       const float* __restrict__ scale, int M, int N, int K,
@@ -322,6 +444,9 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x
     if constexpr (WL == W_F8)
         gemv_block_f8<NTS, MT, NW, PD, OUT, XL>(x, (const u8*)w, scale, M, N, K, y, ldy, blockIdx.x * NTS * 16, 0,
                                                 K >> 6, red);
+    else if constexpr (WL == W_F4)
+        gemv_block_f4<NTS, MT, NW, OUT, XL>(x, (const u8*)w, reinterpret_cast<const uint32_t*>(scale), M, N, K, y,
+                                            ldy, blockIdx.x * NTS * 16, 0, K >> 7, red);
     else
         gemv_block<NTS, MT, NW, PD, OUT, WL, XL>(x, (const u16*)w, M, N, K, y, ldy, blockIdx.x * NTS * 16, 0,
                                                  K >> 5, red);
@@ -347,6 +472,9 @@ __global__ __launch_bounds__(NW * 64) void in_proj_decode_kernel(const u16* __re
         if constexpr (WL == W_F8)
             gemv_block_f8<NTS, MT, NW, PD, OUT_F32, XL>(x, (const u8*)w, scale, M, N1, K, P, ldp, bid * NTS * 16, 0,
                                                        K >> 6, red);
+        else if constexpr (WL == W_F4)
+            gemv_block_f4<NTS, MT, NW, OUT_F32, XL>(x, (const u8*)w, reinterpret_cast<const uint32_t*>(scale), M, N1,
+                                                   K, P, ldp, bid * NTS * 16, 0, K >> 7, red);
         else
             gemv_block<NTS, MT, NW, PD, OUT_F32, W_FRAG, XL>(x, (const u16*)w, M, N1, K, P, ldp, bid * NTS * 16, 0,
                                                             K >> 5, red);
@@ -405,7 +533,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
 
     // global -> register staging: 1024 16-byte pieces per operand tile, 4 per thread (W_F8: 512 B pieces,
     // 2 per thread, each widened to two 16-byte bf16 pieces on the way to LDS)
-    constexpr int NB = WL == W_F8 ? 2 : 4;
+    constexpr int NB = WL == W_F8 || WL == W_F4 ? 2 : 4;
     const u16* w = (const u16*)wv;
     const u8* w8 = (const u8*)wv;
     u16x8 ra[4], rb[4];
@@ -413,6 +541,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
     const u16* ag[4];
     const u16* bg[4];
     const u8* bq[2];
+    const uint32_t* bs4[2];
     int soffa[4], soffb[4];
     const int NT = (N + 15) >> 4;
 #pragma unroll
@@ -427,6 +556,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
             if (j < NB) {
                 const int ntl = c >> 6, l = c & 63;
                 bq[j] = w8 + (size_t)min((n0 >> 4) + ntl, NT - 1) * (K >> 6) * 1024 + l * 16;
+                soffb[2 * j] = (16 * ntl + (l & 15)) * TLD + 8 * (l >> 4);
+                soffb[2 * j + 1] = soffb[2 * j] + 32;
+            }
+        } else if (WL == W_F4) {
+            // piece c (< 512) of the 8 W_F4 blocks (8 n-tiles x 1 k-quad) holding this k-tile: 8 bytes of lane
+            // l, the two k-steps of the tile, into the same places as a W_F8 piece; its row's scale word
+            if (j < NB) {
+                const int ntl = c >> 6, l = c & 63;
+                const size_t blk = (size_t)min((n0 >> 4) + ntl, NT - 1) * (K >> 7);
+                bq[j] = w8 + blk * 1024 + l * 16;
+                bs4[j] = reinterpret_cast<const uint32_t*>(scale) + blk * 16 + (l & 15);
                 soffb[2 * j] = (16 * ntl + (l & 15)) * TLD + 8 * (l >> 4);
                 soffb[2 * j + 1] = soffb[2 * j] + 32;
             }
@@ -447,6 +587,13 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
         if constexpr (WL == W_F8) {
 #pragma unroll
             for (int j = 0; j < NB; ++j) rq[j] = *reinterpret_cast<const u32x4*>(bq[j] + (size_t)kt * BSTEP);
+        } else if constexpr (WL == W_F4) {
+            // codes, and the scale word shifted so that its bytes 0, 1 belong to this k-tile's k-steps
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const uint2 c = *reinterpret_cast<const uint2*>(bq[j] + (size_t)(kt >> 1) * 1024 + (kt & 1) * 8);
+                rq[j] = u32x4{c.x, c.y, bs4[j][(size_t)(kt >> 1) * 16] >> (16 * (kt & 1)), 0u};
+            }
         } else {
 #pragma unroll
             for (int j = 0; j < 4; ++j) rb[j] = *reinterpret_cast<const u16x8*>(bg[j] + (size_t)kt * BSTEP);
@@ -460,6 +607,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
                 e4m3x16_to_bf16(rq[j], lo, hi);
                 *reinterpret_cast<bf16x8*>(&Bs[buf][soffb[2 * j]]) = lo;
                 *reinterpret_cast<bf16x8*>(&Bs[buf][soffb[2 * j + 1]]) = hi;
+            }
+        } else if constexpr (WL == W_F4) {
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                *reinterpret_cast<bf16x8*>(&Bs[buf][soffb[2 * j]]) =
+                    e2m1x8_to_bf16(rq[j][0], e8m0_value(rq[j][2] & 0xffu));
+                *reinterpret_cast<bf16x8*>(&Bs[buf][soffb[2 * j + 1]]) =
+                    e2m1x8_to_bf16(rq[j][1], e8m0_value((rq[j][2] >> 8) & 0xffu));
             }
         } else {
 #pragma unroll
@@ -564,12 +719,13 @@ __global__ __launch_bounds__(512, 1) void gemm256_kernel(const u16* __restrict__
 
     // staging: 4 A and 4 B pieces of 16 bytes per thread and k-tile (W_F8: 2 B pieces of 16 codes, each
     // widened to two bf16 pieces on the way to LDS)
-    constexpr int NB = WL == W_F8 ? 2 : 4;
+    constexpr int NB = WL == W_F8 || WL == W_F4 ? 2 : 4;
     const u16* w = (const u16*)wv;
     const u8* w8 = (const u8*)wv;
     const u16* ag[4];
     const u16* bg[4];
     const u8* bq[2];
+    const uint32_t* bs4[2];
     int sa[4], sb[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -581,6 +737,15 @@ __global__ __launch_bounds__(512, 1) void gemm256_kernel(const u16* __restrict__
             if (j < NB) {
                 const int ntl = c >> 6, l = c & 63;
                 bq[j] = w8 + (size_t)min((n0 >> 4) + ntl, NT - 1) * (K >> 6) * 1024 + l * 16;
+                sb[2 * j] = lds_off(16 * ntl + (l & 15), l >> 4);
+                sb[2 * j + 1] = lds_off(16 * ntl + (l & 15), 4 + (l >> 4));
+            }
+        } else if (WL == W_F4) {  // piece c (< 1024) of the 16 W_F4 blocks (16 n-tiles x 1 k-quad): 8 bytes
+            if (j < NB) {
+                const int ntl = c >> 6, l = c & 63;
+                const size_t blk = (size_t)min((n0 >> 4) + ntl, NT - 1) * (K >> 7);
+                bq[j] = w8 + blk * 1024 + l * 16;
+                bs4[j] = reinterpret_cast<const uint32_t*>(scale) + blk * 16 + (l & 15);
                 sb[2 * j] = lds_off(16 * ntl + (l & 15), l >> 4);
                 sb[2 * j + 1] = lds_off(16 * ntl + (l & 15), 4 + (l >> 4));
             }
@@ -606,9 +771,13 @@ __global__ __launch_bounds__(512, 1) void gemm256_kernel(const u16* __restrict__
         for (int j = 0; j < 4; ++j) ra[j] = *reinterpret_cast<const u16x8*>(ag[j] + (size_t)k * LBK);
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            if constexpr (WL == W_F8)
+            if constexpr (WL == W_F8) {
                 rb[j] = __builtin_bit_cast(u16x8, *reinterpret_cast<const u32x4*>(bq[j] + (size_t)k * BSTEP));
-            else
+            } else if constexpr (WL == W_F4) {
+                // codes, and the scale word shifted so that its bytes 0, 1 belong to this k-tile's k-steps
+                const uint2 c = *reinterpret_cast<const uint2*>(bq[j] + (size_t)(k >> 1) * 1024 + (k & 1) * 8);
+                rb[j] = __builtin_bit_cast(u16x8, u32x4{c.x, c.y, bs4[j][(size_t)(k >> 1) * 16] >> (16 * (k & 1)), 0u});
+            } else
                 rb[j] = *reinterpret_cast<const u16x8*>(bg[j] + (size_t)k * BSTEP);
         }
     };
@@ -622,6 +791,11 @@ __global__ __launch_bounds__(512, 1) void gemm256_kernel(const u16* __restrict__
                 e4m3x16_to_bf16(__builtin_bit_cast(u32x4, rb[j]), lo, hi);
                 *reinterpret_cast<bf16x8*>(&Bs[buf][sb[2 * j]]) = lo;
                 *reinterpret_cast<bf16x8*>(&Bs[buf][sb[2 * j + 1]]) = hi;
+            } else if constexpr (WL == W_F4) {
+                const u32x4 v = __builtin_bit_cast(u32x4, rb[j]);
+                *reinterpret_cast<bf16x8*>(&Bs[buf][sb[2 * j]]) = e2m1x8_to_bf16(v[0], e8m0_value(v[2] & 0xffu));
+                *reinterpret_cast<bf16x8*>(&Bs[buf][sb[2 * j + 1]]) =
+                    e2m1x8_to_bf16(v[1], e8m0_value((v[2] >> 8) & 0xffu));
             } else {
                 *reinterpret_cast<u16x8*>(&Bs[buf][sb[j]]) = rb[j];
             }
@@ -800,6 +974,17 @@ hipError_t launch_quantize_e4m3(const void* w, int N, int K, u8* q, float* scale
     return hipGetLastError();
 }
 
+hipError_t launch_quantize_mxfp4(const void* w, int N, int K, u8* q, u8* scale, int to_frag, hipStream_t stream) {
+    if (N <= 0 || K <= 0) return hipSuccess;
+    if (K % (to_frag ? 128 : 32)) return hipErrorInvalidValue;
+    const int rows = to_frag ? (N + 15) / 16 * 16 : N;
+    if (to_frag)
+        hipLaunchKernelGGL(quantize_mxfp4_kernel<true>, dim3(rows), dim3(256), 0, stream, (const u16*)w, N, K, q, scale);
+    else
+        hipLaunchKernelGGL(quantize_mxfp4_kernel<false>, dim3(rows), dim3(256), 0, stream, (const u16*)w, N, K, q, scale);
+    return hipGetLastError();
+}
+
 hipError_t launch_frag_tile(const void* w, int N, int K, void* wf, hipStream_t stream) {
     const size_t pieces = frag_elems(N, K) / 8;
     hipLaunchKernelGGL(frag_tile_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, stream, (const u16*)w,
@@ -863,11 +1048,13 @@ hipError_t launch_in_proj_decode(const void* x, int xlayout, const void* w, int 
                                  int ab_splits, hipStream_t stream) {
     if (M <= 0) return hipSuccess;
     if (M > 64 || N1 % 16 || ab_splits <= 0 || K % 32) return hipErrorInvalidValue;
-    if (wlayout != W_FRAG && wlayout != W_F8) return hipErrorInvalidValue;
+    if (wlayout != W_FRAG && wlayout != W_F8 && wlayout != W_F4) return hipErrorInvalidValue;
     if (wlayout == W_F8 && (K % 64 || !w_scale)) return hipErrorInvalidValue;
+    if (wlayout == W_F4 && (K % 128 || !w_scale)) return hipErrorInvalidValue;
     if (xlayout != W_FRAG && (xlayout != W_ROW || M > 16)) return hipErrorInvalidValue;
     const DecodeArgs a{(const u16*)x, w, w_scale, (const u16*)w2, M, N1, N2, K, 0, ab_splits, P, ldp, Pab};
     if (wlayout == W_F8) return in_proj_decode_wl<W_F8>(a, xlayout, stream);
+    if (wlayout == W_F4) return in_proj_decode_wl<W_F4>(a, xlayout, stream);
     return in_proj_decode_wl<W_FRAG>(a, xlayout, stream);
 }
 
@@ -888,6 +1075,10 @@ hipError_t launch_linear(const void* x, int xlayout, const void* w, int wlayout,
     if (wlayout == W_F8) {
         if (K % 64 || !w_scale) return hipErrorInvalidValue;
         return linear_wl<W_F8>(a, xlayout, stream);
+    }
+    if (wlayout == W_F4) {
+        if (K % 128 || !w_scale) return hipErrorInvalidValue;
+        return linear_wl<W_F4>(a, xlayout, stream);
     }
     if (wlayout == W_FRAG) return linear_wl<W_FRAG>(a, xlayout, stream);
     return linear_wl<W_ROW>(a, xlayout, stream);

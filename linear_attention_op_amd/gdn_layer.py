@@ -86,8 +86,9 @@ class Qwen35GatedDeltaNetHIP:
     """One GDN layer.  `weights` is an HF Qwen3_5GatedDeltaNet or a dict with keys
     w_qkv [conv_dim, H], w_z [Vd, H], w_a, w_b [nv, H], conv_w [conv_dim, 4], A_log, dt_bias [nv],
     norm_w [dv], w_out [H, Vd] (projection weights are used as bf16, the rest as fp32).
-    `weight_dtype` ("bf16" or "fp8") mirrors the reference's weight_dtype (9B/gdn_layer.py:55): "fp8" keeps the
-    q|k|v|z and out projections as E4M3 with per-row scales (see quantize_fp8); a|b stay bf16."""
+    `weight_dtype` ("bf16", "fp8" or "mxfp4") mirrors the reference's weight_dtype (9B/gdn_layer.py:55;
+    bfloat8_b / bfloat4_b, 0.8B/gdn_l1.py:79-80): "fp8" keeps the q|k|v|z and out projections as E4M3 with
+    per-row scales (see quantize_fp8), "mxfp4" as MXFP4 with a scale per 32 (see quantize_mxfp4); a|b stay bf16."""
 
     def __init__(self, weights, dims=None, batch=1, max_slots=None, max_tokens=16384, device="cuda", _handle=None,
                  weight_dtype="bf16"):
@@ -112,7 +113,7 @@ class Qwen35GatedDeltaNetHIP:
         self.conv_dim = 2 * self.nk * self.dk + self.nv * self.dv
         self.proj_width = _lib.lib().gdn_layer_proj_width(self._h)
         fmt = _lib.lib().gdn_layer_weight_format(self._h)
-        self.weight_dtype = "fp8" if fmt == _lib.GDN_WEIGHTS_FP8_E4M3 else "bf16"
+        self.weight_dtype = _lib.WEIGHT_NAMES[fmt]
 
     @classmethod
     def from_checkpoint(cls, path, layer_idx, prefix=None, **kwargs):
@@ -274,4 +275,16 @@ def quantize_fp8(w):
     q = torch.empty(w.shape, device=w.device, dtype=torch.uint8)
     s = torch.empty(w.shape[0], device=w.device, dtype=torch.float32)
     _lib.check(_lib.lib().gdn_quantize_fp8(_ptr(w), w.shape[0], w.shape[1], _ptr(q), _ptr(s), _stream()))
+    return q, s
+
+
+def quantize_mxfp4(w):
+    """The library's MXFP4 weight quantizer (gdn_quantize_mxfp4) on a CUDA matrix w [N, K] (K % 32 == 0): ->
+    (codes uint8 [N, K / 2], two E2M1 codes per byte, column 2i in the low nibble; scale codes uint8 [N, K / 32],
+    E8M0).  Block j of row n dequantizes to e2m1_value(codes) * 2^(scale[n, j] - 127)."""
+    w = w.to(torch.bfloat16).contiguous()
+    N, K = w.shape
+    q = torch.empty((N, K // 2), device=w.device, dtype=torch.uint8)
+    s = torch.empty((N, K // 32), device=w.device, dtype=torch.uint8)
+    _lib.check(_lib.lib().gdn_quantize_mxfp4(_ptr(w), N, K, _ptr(q), _ptr(s), _stream()))
     return q, s

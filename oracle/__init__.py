@@ -65,6 +65,13 @@ def _declare(L):
     L.orc_e4m3_encode.argtypes = [ctypes.c_float]
     L.orc_e4m3_encode.restype = _I
     L.orc_quantize_e4m3.argtypes = [_P, _I, _I, ctypes.c_void_p, _P]
+    L.orc_e2m1_value.argtypes = [_I]
+    L.orc_e2m1_value.restype = ctypes.c_double
+    L.orc_e2m1_encode.argtypes = [ctypes.c_float]
+    L.orc_e2m1_encode.restype = _I
+    L.orc_mx_scale_code.argtypes = [ctypes.c_float]
+    L.orc_mx_scale_code.restype = _I
+    L.orc_quantize_mxfp4.argtypes = [_P, _I, _I, ctypes.c_void_p, ctypes.c_void_p]
 
 
 def _f(a):
@@ -245,3 +252,37 @@ def quantize_e4m3(w):
 def dequantize_e4m3(q, scale):
     """codes [N, K], scale [N] -> float32 [N, K] = value(code) * scale (the weights the FP8 path multiplies by)."""
     return e4m3_table()[np.asarray(q)] * np.asarray(scale, np.float32)[:, None]
+
+
+# ---- low-precision weights (MXFP4: E2M1 values, one E8M0 scale per 32 along K) ------------------------
+def e2m1_table():
+    """float32 [16]: the value of every E2M1 code."""
+    return np.array([lib().orc_e2m1_value(c) for c in range(16)], np.float32)
+
+
+def e2m1_encode(v):
+    """E2M1 code of one float (nearest, ties to even, saturating at +-6)."""
+    return lib().orc_e2m1_encode(float(v))
+
+
+def mx_scale_code(amax):
+    """E8M0 exponent byte of the scale 2^(floor(log2 amax) - 2) of a block with largest magnitude amax."""
+    return lib().orc_mx_scale_code(float(amax))
+
+
+def quantize_mxfp4(w):
+    """w [N, K] (K % 32 == 0) -> (codes uint8 [N, K], one E2M1 code per byte; scale codes uint8 [N, K / 32])."""
+    w, pw = _f(w)
+    N, K = w.shape
+    if K % 32:
+        raise ValueError("K must be a multiple of 32")
+    q = np.empty((N, K), np.uint8)
+    sc = np.empty((N, K // 32), np.uint8)
+    lib().orc_quantize_mxfp4(pw, N, K, q.ctypes.data_as(ctypes.c_void_p), sc.ctypes.data_as(ctypes.c_void_p))
+    return q, sc
+
+
+def dequantize_mxfp4(q, sc):
+    """codes [N, K], scale codes [N, K / 32] -> float32 [N, K] = value(code) * 2^(scale code - 127)."""
+    scale = np.ldexp(np.float32(1.0), np.asarray(sc, np.int32) - 127).astype(np.float32)
+    return e2m1_table()[np.asarray(q)] * np.repeat(scale, 32, axis=1)

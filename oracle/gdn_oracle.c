@@ -595,3 +595,56 @@ EXPORT void orc_quantize_e4m3(const float* w, int N, int K, uint8_t* q, float* s
         for (int k = 0; k < K; ++k) q[(size_t)n * K + k] = (uint8_t)orc_e4m3_encode(w[(size_t)n * K + k] / s);
     }
 }
+
+/* ---- low-precision weights: MXFP4 (E2M1 elements, one E8M0 scale per 32 along K) ----------------------
+ * The reference's other weight_dtype, ttnn.bfloat4_b (0.8B/gdn_l1.py:79-80; 0.8B/test_gdn_l1.py:88-92 runs
+ * six resident layers in it), is a shared-exponent tile format with no MI355X counterpart; the HIP path
+ * stores w_in (q|k|v|z rows) and w_out as OCP MXFP4 (OCP Microscaling Formats Specification v1.0, 2023):
+ * blocks of 32 consecutive values of a row share the scale X = 2^(floor(log2(amax)) - 2) (emax of E2M1 is
+ * 2; X stored as its E8M0 exponent byte, bias 127, the exponent clamped to [-127, 127]; an all-zero block
+ * takes code 0), and each value is the FP4 E2M1 code nearest to w / X (1 sign bit, 2 exponent bits with
+ * bias 1, 1 mantissa bit: 0, 0.5, 1, 1.5, 2, 3, 4, 6), ties to the even mantissa, saturating at +-6.
+ * Dequantized weight = value(code) * X.  Restated from the specification: decode by the closed form,
+ * encode by exhaustive nearest search over the eight magnitudes, the exponent by frexp. */
+EXPORT double orc_e2m1_value(int code) {
+    const int s = (code >> 3) & 1, e = (code >> 1) & 3, m = code & 1;
+    const double mag = e == 0 ? 0.5 * m : ldexp(1.0 + 0.5 * m, e - 1);
+    return s ? -mag : mag;
+}
+
+EXPORT int orc_e2m1_encode(float v) {
+    const double a = fmin(fabs((double)v), 6.0);
+    int best = 0;
+    double dbest = INFINITY;
+    for (int c = 0; c < 8; ++c) {  /* codes 0..7 are the non-negative values, ascending */
+        const double d = fabs(orc_e2m1_value(c) - a);
+        if (d < dbest || (d == dbest && (c & 1) == 0)) best = c, dbest = d;
+    }
+    return (signbit(v) ? 8 : 0) | best;
+}
+
+/* E8M0 exponent byte of the block scale for a block whose largest magnitude is amax */
+EXPORT int orc_mx_scale_code(float amax) {
+    if (!(amax > 0.f)) return 0;
+    int e2;
+    frexp((double)amax, &e2);   /* amax = f 2^e2, f in [0.5, 1): floor(log2 amax) = e2 - 1 */
+    int x = e2 - 1 - 2;
+    if (x < -127) x = -127;
+    if (x > 127) x = 127;
+    return x + 127;
+}
+
+/* w [N, K] (K % 32 == 0) -> codes [N, K] (one E2M1 code per byte, unpacked) and scale codes [N, K / 32] */
+EXPORT void orc_quantize_mxfp4(const float* w, int N, int K, uint8_t* q, uint8_t* sc) {
+#pragma omp parallel for schedule(static)
+    for (int n = 0; n < N; ++n)
+        for (int kb = 0; kb < K / 32; ++kb) {
+            const float* b = w + (size_t)n * K + 32 * kb;
+            float m = 0.f;
+            for (int j = 0; j < 32; ++j) m = fmaxf(m, fabsf(b[j]));
+            const int code = orc_mx_scale_code(m);
+            sc[(size_t)n * (K / 32) + kb] = (uint8_t)code;
+            const double X = ldexp(1.0, code - 127);
+            for (int j = 0; j < 32; ++j) q[(size_t)n * K + 32 * kb + j] = (uint8_t)orc_e2m1_encode((float)(b[j] / X));
+        }
+}

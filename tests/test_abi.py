@@ -89,5 +89,10 @@ def test_weight_format_checks():
     assert L.gdn_quantize_fp8(p, 0, 64, p, p, None) == _lib.GDN_ERR_SHAPE
     assert _lib.weight_format("fp8") == _lib.GDN_WEIGHTS_FP8_E4M3 == _lib.weight_format("FP8_E4M3")
     assert _lib.weight_format("bf16") == _lib.GDN_WEIGHTS_BF16
+    assert _lib.weight_format("mxfp4") == _lib.GDN_WEIGHTS_MXFP4 == _lib.weight_format("FP4")
     with pytest.raises(ValueError):
         _lib.weight_format("bfp4")
+    # MXFP4: K a multiple of 32 for the quantizer
+    assert L.gdn_quantize_mxfp4(None, 4, 64, p, p, None) == _lib.GDN_ERR_INVALID_ARG
+    assert L.gdn_quantize_mxfp4(p, 0, 64, p, p, None) == _lib.GDN_ERR_SHAPE
+    assert L.gdn_quantize_mxfp4(p, 4, 48, p, p, None) == _lib.GDN_ERR_UNSUPPORTED
