@@ -27,15 +27,18 @@ HBM_PEAK = 8.0e12        # B/s, MI355X HBM3E
 BF16_PEAK = 2.5e15       # FLOP/s, MI355X dense bf16 MFMA
 
 
-def decode_bytes(d, B, fp8=False):
+def decode_bytes(d, B, fp8=False, fp4=False):
     """Algorithmic HBM bytes of one decode layer step: weights once plus per-sequence state and I/O.
     W = bf16 projections (qkv, z, a, b, out) + bf16 conv taps (fp8: qkv, z and out as 1-byte codes plus an
-    fp32 scale per row, a and b bf16); s = fp32 state read + write, fp32 conv history (3 reads + 1 write per
-    channel), bf16 x in and out."""
+    fp32 scale per row; fp4: the same as half-byte codes plus a 1-byte scale per 32; a and b bf16); s = fp32
+    state read + write, fp32 conv history (3 reads + 1 write per channel), bf16 x in and out."""
     H, nk, nv, dk, dv = d["hidden"], d["num_k_heads"], d["num_v_heads"], d["head_k_dim"], d["head_v_dim"]
     C, Vd = 2 * nk * dk + nv * dv, nv * dv
+    q = C * H + Vd * H + H * Vd  # quantized weights
     if fp8:
-        W = (C * H + Vd * H + H * Vd) + 4 * (C + Vd + H) + 2 * 2 * nv * H + 2 * C * 4
+        W = q + 4 * (C + Vd + H) + 2 * 2 * nv * H + 2 * C * 4
+    elif fp4:
+        W = q // 2 + q // 32 + 2 * 2 * nv * H + 2 * C * 4
     else:
         W = 2 * (C * H + Vd * H + 2 * nv * H + H * Vd) + 2 * C * 4
     s = nv * dk * dv * 4 * 2 + C * 4 * 4 + 2 * H * 2
@@ -210,7 +213,7 @@ def stream_ceiling(nbytes, copies=4, reps=40):
             "bytes": 2 * nbytes, "us": sec * 1e6, "GBps": 2 * nbytes / sec / 1e9, "frac": 2 * nbytes / sec / HBM_PEAK}
 
 
-def small_batch_decode(shape, B, copies=8, steps=400, warmup=40):
+def small_batch_decode(shape, B, copies=8, steps=400, warmup=40, weight_dtype="bf16"):
     """Decode latency of one layer at a small batch, one HIP graph per layer copy (launch overhead is most
     of such a step), rotating over `copies` layers so that the weights come from HBM."""
     import torch
@@ -226,7 +229,7 @@ def small_batch_decode(shape, B, copies=8, steps=400, warmup=40):
         gg = torch.Generator(device=dev).manual_seed(200 + i)
         w = {k: (torch.randn(v.shape, generator=gg, device=dev) * v.float().std()).to(v.dtype)
              if k.startswith("w_") or k == "conv_w" else v for k, v in w0.items()}
-        lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B, max_tokens=64)
+        lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B, max_tokens=64, weight_dtype=weight_dtype)
         lay.set_state(rec=torch.randn(B, d["num_v_heads"], d["head_k_dim"], d["head_v_dim"], device=dev) * 0.01)
         layers.append(lay)
         xin.append(torch.randn(B, 1, d["hidden"], device=dev).to(torch.bfloat16))
@@ -250,8 +253,8 @@ def small_batch_decode(shape, B, copies=8, steps=400, warmup=40):
         graphs[i % copies].replay()
     torch.cuda.synchronize()
     us = (time.perf_counter() - t0) / steps * 1e6
-    W, s = decode_bytes(d, B)
-    out = {"shape": shape, "batch": B, "us_per_step": us, "tok_per_s": B / (us * 1e-6),
+    W, s = decode_bytes(d, B, fp8=weight_dtype == "fp8", fp4=weight_dtype == "mxfp4")
+    out = {"shape": shape, "batch": B, "weights": weight_dtype, "us_per_step": us, "tok_per_s": B / (us * 1e-6),
            "hbm_frac": (W + B * s) / (us * 1e-6) / HBM_PEAK, "mode": "HIP graph per step"}
     for lay in layers:
         lay.close()
@@ -332,7 +335,7 @@ def main():
     ap.add_argument("--graph", type=int, default=0,
                     help="1: replay the decode step from HIP graphs; 0: launch eagerly (faster here: 104 vs 112 us)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-fp8", action="store_true", help="skip the FP8-weight decode measurement")
+    ap.add_argument("--no-fp8", action="store_true", help="skip the FP8- and MXFP4-weight decode measurements")
     ap.add_argument("--no-small", action="store_true", help="skip the batch-1/8 decode latencies")
     ap.add_argument("--stack", action="store_true",
                     help="also run the 24-layer continuous-batching stack (8 x 2048 prefill + 56 decode per step)")
@@ -485,6 +488,29 @@ def main():
             lay.close()
         del lays8
 
+    # the same decode step on MXFP4 weights (q|k|v|z and out_proj half a byte per weight, a scale per 32)
+    fp4 = None
+    if not args.no_fp8:
+        print(f"[bench] MXFP4-weight decode, {L} copies", file=sys.stderr, flush=True)
+        lays4 = []
+        for i in range(L):
+            lay = Qwen35GatedDeltaNetHIP(copy_weights(i), dims=d, batch=B, max_tokens=max(B, 64),
+                                         weight_dtype="mxfp4")
+            lay.set_state(rec=torch.randn(B, d["num_v_heads"], 128, 128, device=dev) * 0.01)
+            lays4.append(lay)
+        wall4, st4 = eager_decode(lays4, xs, args.steps, args.warmup)
+        W4, s4 = decode_bytes(d, B, fp4=True)
+        b4 = W4 + B * s4
+        fp4 = {"ms_per_step": wall4, "tok_per_s": B / (wall4 / 1e3), "bytes_per_step": b4,
+               "frac": b4 / (wall4 / 1e3) / HBM_PEAK, "event_step_us": st4["total"] * 1e3,
+               "stage_us": {k: v * 1e3 for k, v in st4.items()},
+               "weights": "MXFP4 (E2M1, one E8M0 scale per 32; a|b rows bf16)"}
+        print(f"[bench] mxfp4 decode B={B}: {wall4 * 1e3:.1f} us/step wall, stages (us) "
+              f"{ {k: round(v * 1e3, 1) for k, v in st4.items()} }", file=sys.stderr, flush=True)
+        for lay in lays4:
+            lay.close()
+        del lays4
+
     prefill = None
     if not args.no_prefill:
         T = args.prefill_len
@@ -514,8 +540,10 @@ def main():
     small = None
     if not args.no_small:
         small = [small_batch_decode("0.8b", 1), small_batch_decode("9b", 1), small_batch_decode("9b", 8)]
+        if not args.no_fp8:
+            small += [small_batch_decode("9b", 1, weight_dtype="fp8"), small_batch_decode("9b", 1, weight_dtype="mxfp4")]
         for r in small:
-            print(f"[bench] decode {r['shape']} B={r['batch']}: {r['us_per_step']:.1f} us/step (graph), "
+            print(f"[bench] decode {r['shape']} B={r['batch']} {r['weights']}: {r['us_per_step']:.1f} us/step (graph), "
                   f"{r['hbm_frac'] * 100:.0f}% of HBM roofline", file=sys.stderr, flush=True)
 
     stack = None
@@ -539,7 +567,7 @@ def main():
                    "hidden": d["hidden"], "num_k_heads": d["num_k_heads"], "num_v_heads": d["num_v_heads"],
                    "head_dim": 128, "batch": B, "state_dtype": "fp32", "weights": "bf16 N(0,0.02) seed 2"},
         "roofline": roofline, "layer_roofline": layer_roof, "stream_ceiling": ceiling, "prefill": prefill,
-        "stack": stack, "fp8_decode": fp8, "small_batch_decode": small,
+        "stack": stack, "fp8_decode": fp8, "mxfp4_decode": fp4, "small_batch_decode": small,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

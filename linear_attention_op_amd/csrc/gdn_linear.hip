@@ -355,8 +355,10 @@ __device__ __forceinline__ void gemv_block_f8(const u16* __restrict__ x, const u
 }
 
 // The same on W_F4 weights: one 16-byte load per row tile covers a k-quad (4 k-steps, 128 columns) and its
-// four scales one 32-bit load; weights two quads ahead, x fragments one quad (4 k-steps) ahead.  K % 128
-// == 0; the k range is [kbb, kbb + kbn) in k-quads.
+// four scales one 32-bit load; x fragments one quad (4 k-steps) ahead, weights four quads ahead for small
+// tiles (a wave's whole share at the 9B shape and batch <= 16, so its weight loads are all in flight at
+// once) and two for the large ones (register budget).  K % 128 == 0; the k range is [kbb, kbb + kbn) in
+// k-quads.
 template <int NTS, int MT, int NW, int OUT, int XL>
 __device__ __forceinline__ void gemv_block_f4(const u16* __restrict__ x, const u8* __restrict__ w,
                                               const uint32_t* __restrict__ sw, int M, int N, int K,
@@ -391,8 +393,9 @@ __device__ __forceinline__ void gemv_block_f4(const u16* __restrict__ x, const u
     }
     constexpr size_t XSTEP = XL == W_FRAG ? 512 : 32;
 
-    u32x4 wq[2][NTS];
-    uint32_t ws[2][NTS];
+    constexpr int PQ = NTS * MT <= 4 ? 4 : 2;  // quads in flight
+    u32x4 wq[PQ][NTS];
+    uint32_t ws[PQ][NTS];
     bf16x8 xb[4][MT];
     const bf16x8 zero8 = {};
     auto wload = [&](int slot, int qd) {
@@ -407,8 +410,9 @@ __device__ __forceinline__ void gemv_block_f4(const u16* __restrict__ x, const u
         for (int mt = 0; mt < MT; ++mt)
             xb[h][mt] = xv[mt] ? *reinterpret_cast<const bf16x8*>(xp[mt] + (size_t)s * XSTEP) : zero8;
     };
-    if (nq > 0) wload(0, 0);
-    if (nq > 1) wload(1, 1);
+#pragma unroll
+    for (int j = 0; j < PQ; ++j)
+        if (j < nq) wload(j, j);
     if (nq > 0) {
 #pragma unroll
         for (int h = 0; h < 4; ++h) xload(h, h);
@@ -419,19 +423,25 @@ __device__ __forceinline__ void gemv_block_f4(const u16* __restrict__ x, const u
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    for (int qd = 0; qd < nq; ++qd) {
-        const int slot = qd & 1;
+    for (int q0 = 0; q0 < nq; q0 += PQ) {
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
+        for (int slot = 0; slot < PQ; ++slot) {
+            const int qd = q0 + slot;
+            if (qd < nq) {
 #pragma unroll
-            for (int t = 0; t < NTS; ++t) {
-                const bf16x8 a = e2m1x8_to_bf16(wq[slot][t][h], e8m0_value((ws[slot][t] >> (8 * h)) & 0xffu));
+                for (int h = 0; h < 4; ++h) {
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt) acc[t][mt] = mfma16(a, xb[h][mt], acc[t][mt]);
+                    for (int t = 0; t < NTS; ++t) {
+                        const bf16x8 a =
+                            e2m1x8_to_bf16(wq[slot][t][h], e8m0_value((ws[slot][t] >> (8 * h)) & 0xffu));
+#pragma unroll
+                        for (int mt = 0; mt < MT; ++mt) acc[t][mt] = mfma16(a, xb[h][mt], acc[t][mt]);
+                    }
+                    if (qd + 1 < nq) xload(h, 4 * (qd + 1) + h);
+                }
+                if (qd + PQ < nq) wload(slot, qd + PQ);
             }
-            if (qd + 1 < nq) xload(h, 4 * (qd + 1) + h);
         }
-        if (qd + 2 < nq) wload(slot, qd + 2);
     }
     gemv_finish<NTS, MT, NW, OUT>(acc, red, M, N, y, ldy, n0, nullptr);
 }
