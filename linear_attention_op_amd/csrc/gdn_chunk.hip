@@ -51,7 +51,8 @@ struct ChunkWs {
     u16* Wf;    // [B, Hv, NC][4 rt][8 w][64 lane][8]: W[16 rt + m][16 w + 4 grp + j], hi j < 4, then lo
     u16* Qf;    // the same for Q'
     u16* Kf;    // [B, Hv, NC][8 w][2 s][2 plane][64 lane][8]: Kt[16 w + m][32 s + 8 grp + j], plane 0 hi, 1 lo
-    float* U;   // [B, Hv, NC][CK][DV]   U
+    float* U;   // [B, Hv, NC][4 mi][DV / 16 n][64 lane][4]: U[16 mi + 4 grp + i][16 n + m] (the prep pass's
+                //   MFMA C order: one 16-byte store per lane; the state pass reads 8 contiguous bytes)
     float* G;   // [B, Hv, NC, CK]       G (in-chunk cumulative log decay)
     int NC;     // chunks per sequence
 };
@@ -491,7 +492,7 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
     float* U = ws.U + hc * CK * DV;
 #pragma unroll
     for (int nn = 0; nn < 4; ++nn) {
-        const int col = 16 * (4 * hf + nn) + m;
+        const int n = 4 * hf + nn, col = 16 * n + m;
         f32x4 accT = {0.f, 0.f, 0.f, 0.f}, accM = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
@@ -500,10 +501,10 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
             accT = mfma3(At[s], V, accT);
             accM = mfma3(Am[s], V, accM);
         }
+        *reinterpret_cast<f32x4*>(U + ((size_t)(mi * (DV / 16) + n) * 64 + lane) * 4) = accT;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int r = 16 * mi + 4 * grp + i;
-            U[r * DV + col] = accT[i];
             if (r < len) a.o[((row0 + r) * Hv + h) * DV + col] = accM[i];
         }
     }
@@ -607,9 +608,10 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
         } else {
             const int t0 = c * CK, len = min(CK, T - t0);
             const size_t row0 = (size_t)b * T + t0;
-            const float* U = ws.U + hc * CK * DV + n0 + col;
-            op.u.x = U[(2 * p) * DV];
-            op.u.y = U[(2 * p + 1) * DV];
+            // tokens 2p, 2p + 1 of column n0 + col: token tile p / 8, lane 16 ((p / 2) % 4) + col, slots 2 (p % 2) + e
+            op.u = *reinterpret_cast<const float2*>(
+                ws.U + hc * CK * DV + ((size_t)((p >> 3) * (DV / 16) + cb) * 64 + 16 * ((p >> 1) & 3) + col) * 4 +
+                2 * (p & 1));
             // rows past the end of a partial chunk read a valid row (the value is not used): no branch
             op.o.x = a.o[((row0 + min(2 * p, len - 1)) * Hv + h) * DV + n0 + col];
             op.o.y = a.o[((row0 + min(2 * p + 1, len - 1)) * Hv + h) * DV + n0 + col];
