@@ -208,6 +208,22 @@ int gdn_delta_rule_fla(const float* q, const float* k, const float* v, const flo
                        int T, int Hk, int Hv, int dk, int dv, float* state, int use_qk_l2norm, float scale,
                        float* o, void* stream);
 
+/* Bytes of device workspace that gdn_delta_rule_fla_ws needs to run this launch in the chunk-64 form (the
+ * counterpart of HF's torch_chunk_gated_delta_rule, HF:248-328, which the reference's prefill of a whole
+ * prompt evaluates); 0 when the launch runs the token loop anyway (T <= 64, head dims other than 128 x 128,
+ * or a bad shape). */
+size_t gdn_delta_rule_fla_workspace_size(int B, int T, int Hv, int dk, int dv);
+
+/* gdn_delta_rule_fla with a caller-owned device workspace (nothing is allocated).  When
+ * gdn_delta_rule_fla_workspace_size(B, T, Hv, dk, dv) > 0 and workspace_bytes is at least that, the launch
+ * runs the chunk-64 form: a parallel pass per (sequence, v-head, 64-token chunk), then one sequential pass
+ * over the chunks.  Same arguments, layouts and results (within fp32 rounding) as gdn_delta_rule_fla.
+ * workspace NULL: the token loop, exactly gdn_delta_rule_fla.  A non-NULL workspace smaller than the size
+ * above is GDN_ERR_SHAPE.  Calls that share one workspace must not overlap. */
+int gdn_delta_rule_fla_ws(const float* q, const float* k, const float* v, const float* g, const float* beta,
+                          int B, int T, int Hk, int Hv, int dk, int dv, float* state, int use_qk_l2norm,
+                          float scale, float* o, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Projection y[M, N] = x[M, K] . w[N, K]^T, bf16 inputs, fp32 accumulation (the ttnn.linear call sites
  * 9B/gdn_layer.py:255, 259, 272).  out_fp32 != 0: y is fp32, else bf16.  K % 128 == 0. */
 int gdn_linear_bf16(const void* x, const void* w, int M, int N, int K, void* y, int out_fp32, void* stream);

@@ -63,6 +63,7 @@ class GdnWeights(ctypes.Structure):
 _V = ctypes.c_void_p
 _I = ctypes.c_int
 _F = ctypes.c_float
+_Z = ctypes.c_size_t
 
 # name -> (restype, argtypes)
 SIGNATURES = {
@@ -94,6 +95,8 @@ SIGNATURES = {
     "gdn_gated_rmsnorm": (_I, [_V, _V, _V, _I, _I, _V, _V]),
     "gdn_out_proj": (_I, [_V, _V, _I, _V, _V]),
     "gdn_delta_rule_fla": (_I, [_V, _V, _V, _V, _V, _I, _I, _I, _I, _I, _I, _V, _I, _F, _V, _V]),
+    "gdn_delta_rule_fla_workspace_size": (_Z, [_I, _I, _I, _I, _I]),
+    "gdn_delta_rule_fla_ws": (_I, [_V, _V, _V, _V, _V, _I, _I, _I, _I, _I, _I, _V, _I, _F, _V, _V, _Z, _V]),
     "gdn_linear_bf16": (_I, [_V, _V, _I, _I, _I, _V, _I, _V]),
     "gdn_quantize_fp8": (_I, [_V, _I, _I, _V, _V, _V]),
     "gdn_quantize_mxfp4": (_I, [_V, _I, _I, _V, _V, _V]),
@@ -108,7 +111,7 @@ def header_symbols():
     """Function names declared in include/gdn.h."""
     with open(HEADER) as f:
         text = f.read()
-    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(gdn_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(gdn_\w+)\s*\(", text, re.M)))
 
 
 def lib():

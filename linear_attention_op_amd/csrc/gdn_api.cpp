@@ -660,17 +660,35 @@ int gdn_out_proj(gdn_layer* L, const void* y, int M, void* out, void* stream) {
 int gdn_delta_rule_fla(const float* q, const float* k, const float* v, const float* g, const float* beta, int B,
                        int T, int Hk, int Hv, int dk, int dv, float* state, int use_qk_l2norm, float scale, float* o,
                        void* stream) {
+    return gdn_delta_rule_fla_ws(q, k, v, g, beta, B, T, Hk, Hv, dk, dv, state, use_qk_l2norm, scale, o, nullptr, 0,
+                                 stream);
+}
+
+size_t gdn_delta_rule_fla_workspace_size(int B, int T, int Hv, int dk, int dv) {
+    if (B <= 0 || T <= kFusedMaxT || Hv <= 0 || !gdn::delta_chunked_supported(dk, dv)) return 0;
+    return gdn::delta_chunked_workspace(B, T, Hv, dk, dv);
+}
+
+int gdn_delta_rule_fla_ws(const float* q, const float* k, const float* v, const float* g, const float* beta, int B,
+                          int T, int Hk, int Hv, int dk, int dv, float* state, int use_qk_l2norm, float scale,
+                          float* o, void* workspace, size_t workspace_bytes, void* stream) {
     if (!q || !k || !v || !g || !beta || !state || !o) return fail(GDN_ERR_INVALID_ARG, "gdn_delta_rule_fla: NULL argument");
     if (B <= 0 || T <= 0 || Hk <= 0 || Hv <= 0) return fail(GDN_ERR_SHAPE, "B=%d T=%d Hk=%d Hv=%d", B, T, Hk, Hv);
     if (Hv % Hk) return fail(GDN_ERR_UNSUPPORTED, "Hv=%d is not a multiple of Hk=%d", Hv, Hk);
     if (dk != dv || !supported_head_dim(dk))
         return fail(GDN_ERR_UNSUPPORTED, "head dims %d x %d: need dk == dv in {32, 64, 128}", dk, dv);
+    const size_t need = gdn_delta_rule_fla_workspace_size(B, T, Hv, dk, dv);
+    if (workspace && workspace_bytes < need)
+        return fail(GDN_ERR_SHAPE, "workspace of %zu bytes, this launch needs %zu", workspace_bytes, need);
     gdn::DeltaArgs r{};
     r.q = q, r.k = k, r.v = v, r.g = g, r.beta = beta;
     r.B = B, r.T = T, r.Hk = Hk, r.Hv = Hv, r.slot_ids = nullptr;
     r.state = state, r.o = o, r.normalize = use_qk_l2norm ? 1 : 0;
     r.scale = scale > 0.f ? scale : 1.f / std::sqrt((float)dk);
-    HIP_OK(gdn::launch_delta_seq(r, dk, dv, as_stream(stream)));
+    if (workspace && need > 0)
+        HIP_OK(gdn::launch_delta_chunked(r, dk, dv, workspace, workspace_bytes, as_stream(stream)));
+    else
+        HIP_OK(gdn::launch_delta_seq(r, dk, dv, as_stream(stream)));
     return GDN_OK;
 }
 

@@ -7,6 +7,10 @@ sequences (decode never moves the state to the host).  Inputs use the fla / HF l
 q, k [B, T, Hk, dk], v [B, T, Hv, dv], g (log decay) and beta [B, T, Hv]; v-head h reads k-head
 h // (Hv / Hk).  Per token (reference.py:28-34):  S = exp(g) S;  u = v - k^T S;  S = S + beta k u^T;
 o = q^T S, with q, k L2-normalised and q scaled by dk ** -0.5.
+
+Launches of more than 64 tokens with 128 x 128 heads run the chunk-64 form (HF's torch_chunk_gated_delta_rule,
+HF:248-328: a parallel pass per 64-token chunk, then one sequential pass over the chunks) in a workspace the
+object keeps on the device; `chunked=False` keeps every launch on the token loop.
 """
 
 import ctypes
@@ -17,11 +21,13 @@ from . import _lib
 
 
 class GatedDeltaRuleHIP:
-    def __init__(self, num_heads, head_k_dim=128, head_v_dim=128, initial_state=None, device="cuda"):
+    def __init__(self, num_heads, head_k_dim=128, head_v_dim=128, initial_state=None, device="cuda", chunked=True):
         """num_heads = B * Hv state tiles, as the reference's constructor takes them."""
         self.device = torch.device(device)
         self.num_heads = num_heads
         self.dk, self.dv = head_k_dim, head_v_dim
+        self.chunked = chunked
+        self.workspace = None  # uint8 device buffer of the chunked form, grown on demand
         self.state = torch.zeros(num_heads, head_k_dim, head_v_dim, device=self.device)
         self.reset_state(initial_state)
 
@@ -47,8 +53,14 @@ class GatedDeltaRuleHIP:
         dev = self.device
         t = [x.to(device=dev, dtype=torch.float32).contiguous() for x in (q, k, v, g, beta)]
         o = torch.empty(B, T, Hv, dv, device=dev)
-        _lib.check(_lib.lib().gdn_delta_rule_fla(
+        L = _lib.lib()
+        need = L.gdn_delta_rule_fla_workspace_size(B, T, Hv, dk, dv) if self.chunked else 0
+        if need and (self.workspace is None or self.workspace.numel() < need):
+            self.workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        ws = self.workspace if need else None
+        _lib.check(L.gdn_delta_rule_fla_ws(
             *[ctypes.c_void_p(x.data_ptr()) for x in t], B, T, Hk, Hv, dk, dv, ctypes.c_void_p(self.state.data_ptr()),
             int(bool(use_qk_l2norm)), float(scale or 0.0), ctypes.c_void_p(o.data_ptr()),
+            ctypes.c_void_p(ws.data_ptr() if ws is not None else None), ws.numel() if ws is not None else 0,
             ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)))
         return o

@@ -67,6 +67,21 @@ def test_linear_and_recurrence_shape_checks():
     assert L.gdn_delta_rule_fla(*args, 1, 0, 2, 4, 128, 128, p, 1, 0.0, p, None) == _lib.GDN_ERR_SHAPE
 
 
+def test_chunked_recurrence_workspace_checks():
+    L = _lib.lib()
+    need = L.gdn_delta_rule_fla_workspace_size(2, 200, 32, 128, 128)
+    # W, Q', keys (bf16 hi + lo) and U, G (fp32) for 4 chunks of 64 tokens per (sequence, v-head)
+    assert need == 2 * 32 * 4 * (64 * 128 * 3 + 64 * 128 + 64) * 4
+    assert L.gdn_delta_rule_fla_workspace_size(2, 64, 32, 128, 128) == 0  # one chunk: the token loop
+    assert L.gdn_delta_rule_fla_workspace_size(2, 200, 32, 64, 64) == 0   # chunked form is for 128 x 128
+    assert L.gdn_delta_rule_fla_workspace_size(0, 200, 32, 128, 128) == 0
+    p = ctypes.c_void_p(16)  # non-null, never dereferenced: the size is checked before any launch
+    args = [p] * 5
+    assert L.gdn_delta_rule_fla_ws(*args, 2, 200, 16, 32, 128, 128, p, 1, 0.0, p, p, need - 1, None) == \
+        _lib.GDN_ERR_SHAPE
+    assert b"workspace" in L.gdn_last_error()
+
+
 def test_errors_raise_value_error_in_python():
     with pytest.raises(ValueError):
         _lib.check(_lib.GDN_ERR_SHAPE)

@@ -111,7 +111,7 @@ def test_chunked_recurrence_full_size(layer9b_long, T):
     o_chunk = layer.delta_rule(qn, kn, v, g, beta, 1, T)
     s_chunk = layer.get_recurrent_state()
     nk, nv = d["num_k_heads"], d["num_v_heads"]
-    seq = GatedDeltaRuleHIP(nv, 128, 128)
+    seq = GatedDeltaRuleHIP(nv, 128, 128, chunked=False)
     o_seq = seq(qn.reshape(1, T, nk, 128), kn.reshape(1, T, nk, 128), v.reshape(1, T, nv, 128),
                 g.reshape(1, T, nv), beta.reshape(1, T, nv), use_qk_l2norm=False, scale=1.0)
     torch.cuda.synchronize()
@@ -141,7 +141,7 @@ def test_chunked_layer_full_size_16k(layer9b_long):
     P = layer.in_proj(x.reshape(T, -1))
     qn, kn, v, g, beta = layer.conv_front(P, 1, T)
     nk, nv = d["num_k_heads"], d["num_v_heads"]
-    seq = GatedDeltaRuleHIP(nv, 128, 128)
+    seq = GatedDeltaRuleHIP(nv, 128, 128, chunked=False)
     o_seq = seq(qn.reshape(1, T, nk, 128), kn.reshape(1, T, nk, 128), v.reshape(1, T, nv, 128),
                 g.reshape(1, T, nv), beta.reshape(1, T, nv), use_qk_l2norm=False, scale=1.0)
     Cd, Vd = syn.conv_dim(d), nv * 128

@@ -110,6 +110,48 @@ def test_recurrence_matches_hf_golden(name):
     assert rel(op.get_state(), f["state"].reshape(B * Hv, dk, dv)) < STATE_TOL
 
 
+@pytest.mark.parametrize("B, Hk, Hv, T, l2", [(1, 16, 32, 65, True), (2, 4, 8, 200, True), (3, 2, 2, 130, False)])
+def test_chunked_recurrence_matches_oracle(B, Hk, Hv, T, l2):
+    """Launches of more than 64 tokens run the chunk-64 form: ragged tail chunks (65 = 64 + 1, 200, 130), two
+    v-heads per k-head, a nonzero initial state, with the op's l2norm and without it (unit q, k and scale 1,
+    as the layer hands them over)."""
+    print(f"chunked recurrence B={B} Hk={Hk} Hv={Hv} T={T} l2={l2}", flush=True)
+    dk = dv = 128
+    q, k, v, g, beta = make_rec_inputs(B, T, Hk, Hv, dk, dv, seed=T)
+    scale = None
+    if not l2:
+        q, k, scale = q / q.norm(dim=-1, keepdim=True), k / k.norm(dim=-1, keepdim=True), 1.0
+    init = torch.randn(B, Hv, dk, dv, generator=torch.Generator().manual_seed(1)) * 0.1
+    want_o, want_s = oracle.recurrent_gated_delta_rule(q.numpy(), k.numpy(), v.numpy(), g.numpy(), beta.numpy(),
+                                                       init.numpy(), use_qk_l2norm=l2, scale=scale)
+    op = GatedDeltaRuleHIP(B * Hv, dk, dv, initial_state=init.reshape(B * Hv, dk, dv).cuda())
+    got_o = op(q, k, v, g, beta, use_qk_l2norm=l2, scale=scale)
+    torch.cuda.synchronize()
+    assert op.workspace is not None  # the chunked form ran
+    assert rel(got_o, want_o) < STATE_TOL
+    assert rel(op.get_state(), want_s.reshape(B * Hv, dk, dv)) < STATE_TOL
+
+
+def test_chunked_recurrence_matches_token_loop():
+    """9B heads, T = 2048 then T = 100 on the same object (the workspace is kept, the state carried): the
+    chunked form against the token loop on the same inputs."""
+    B, Hk, Hv, dk, dv = 2, 16, 32, 128, 128
+    chunked = GatedDeltaRuleHIP(B * Hv, dk, dv)
+    loop = GatedDeltaRuleHIP(B * Hv, dk, dv, chunked=False)
+    addr = None
+    for T, seed in ((2048, 5), (100, 6)):
+        print(f"chunked vs token loop T={T}", flush=True)
+        q, k, v, g, beta = make_rec_inputs(B, T, Hk, Hv, dk, dv, seed=seed)
+        o_c = chunked(q, k, v, g, beta)
+        o_l = loop(q, k, v, g, beta)
+        torch.cuda.synchronize()
+        assert loop.workspace is None
+        addr = addr or chunked.workspace.data_ptr()
+        assert chunked.workspace.data_ptr() == addr
+        assert rel(o_c, o_l) < STATE_TOL
+        assert rel(chunked.get_state(), loop.get_state()) < STATE_TOL
+
+
 def test_unsupported_head_dims_raise():
     f = dict(np.load(os.path.join(G, "rec_chunk_edge.npz")))  # dk = 16, dv = 24
     B, T, Hk, dk = f["q"].shape
