@@ -213,6 +213,40 @@ def stream_ceiling(nbytes, copies=4, reps=40):
             "bytes": 2 * nbytes, "us": sec * 1e6, "GBps": 2 * nbytes / sec / 1e9, "frac": 2 * nbytes / sec / HBM_PEAK}
 
 
+def prefill_bench(w, d, T, steps, weight_dtype="bf16"):
+    """One sequence of T tokens through one layer from a zero state (in_proj GEMM, chunked mixer, out_proj
+    GEMM), `steps` times: the HIP-event layer time per prefill and its bf16-MFMA roofline fraction (E4M3 and
+    MXFP4 weights are widened to bf16 on the way into LDS, so the MFMA work is the same)."""
+    import torch
+
+    from linear_attention_op_amd import Qwen35GatedDeltaNetHIP
+
+    dev = torch.device("cuda", 0)
+    lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=1, max_tokens=T, weight_dtype=weight_dtype)
+    x = torch.randn(1, T, d["hidden"], device=dev).to(torch.bfloat16)
+    lay.reset_state()
+    lay(x)
+    torch.cuda.synchronize()
+    lay.profile(steps)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        lay.reset_state()
+        lay(x)
+    torch.cuda.synchronize()
+    pe = (time.perf_counter() - t0) / steps
+    ms, n = lay.profile_read()
+    ev = ms["total"] / max(n, 1) / 1e3
+    flops = prefill_flops_per_token(d) * T
+    out = {"tokens": T, "weights": weight_dtype, "tok_per_s": T / ev, "ms": ev * 1e3, "wall_ms": pe * 1e3,
+           "stage_ms": {k: v / max(n, 1) for k, v in ms.items()},
+           "roofline": {"bound": "mfma", "achieved": flops / ev / 1e12, "peak": BF16_PEAK / 1e12,
+                        "unit": "TFLOP/s", "frac": flops / ev / BF16_PEAK, "flops": flops}}
+    print(f"[bench] prefill T={T} {weight_dtype}: {ev * 1e3:.2f} ms, {T / ev:.0f} tok/s, stages (ms) "
+          f"{ {k: round(v / max(n, 1), 3) for k, v in ms.items()} }", file=sys.stderr, flush=True)
+    lay.close()
+    return out
+
+
 def small_batch_decode(shape, B, copies=8, steps=400, warmup=40, weight_dtype="bf16"):
     """Decode latency of one layer at a small batch, one HIP graph per layer copy (launch overhead is most
     of such a step), rotating over `copies` layers so that the weights come from HBM."""
@@ -335,7 +369,7 @@ def main():
     ap.add_argument("--graph", type=int, default=0,
                     help="1: replay the decode step from HIP graphs; 0: launch eagerly (faster here: 104 vs 112 us)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-fp8", action="store_true", help="skip the FP8- and MXFP4-weight decode measurements")
+    ap.add_argument("--no-fp8", action="store_true", help="skip the FP8- and MXFP4-weight decode and prefill measurements")
     ap.add_argument("--no-small", action="store_true", help="skip the batch-1/8 decode latencies")
     ap.add_argument("--stack", action="store_true",
                     help="also run the 24-layer continuous-batching stack (8 x 2048 prefill + 56 decode per step)")
@@ -512,29 +546,11 @@ def main():
         del lays4
 
     prefill = None
+    prefill_lowp = None
     if not args.no_prefill:
-        T = args.prefill_len
-        lay = Qwen35GatedDeltaNetHIP(w0, dims=d, batch=1, max_tokens=T)
-        x = torch.randn(1, T, d["hidden"], device=dev).to(torch.bfloat16)
-        lay.reset_state()
-        lay(x)
-        torch.cuda.synchronize()
-        lay.profile(args.prefill_steps)
-        t0 = time.perf_counter()
-        for _ in range(args.prefill_steps):
-            lay.reset_state()
-            lay(x)
-        torch.cuda.synchronize()
-        pe = (time.perf_counter() - t0) / args.prefill_steps
-        ms, n = lay.profile_read()
-        ev = ms["total"] / max(n, 1) / 1e3
-        flops = prefill_flops_per_token(d) * T
-        prefill = {"tokens": T, "tok_per_s": T / ev, "ms": ev * 1e3, "wall_ms": pe * 1e3,
-                   "stage_ms": {k: v / max(n, 1) for k, v in ms.items()},
-                   "roofline": {"bound": "mfma", "achieved": flops / ev / 1e12, "peak": BF16_PEAK / 1e12,
-                                "unit": "TFLOP/s", "frac": flops / ev / BF16_PEAK, "flops": flops}}
-        print(f"[bench] prefill T={T}: {ev * 1e3:.2f} ms, {T / ev:.0f} tok/s", file=sys.stderr, flush=True)
-        lay.close()
+        prefill = prefill_bench(w0, d, args.prefill_len, args.prefill_steps)
+        if not args.no_fp8:
+            prefill_lowp = [prefill_bench(w0, d, args.prefill_len, args.prefill_steps, wd) for wd in ("fp8", "mxfp4")]
 
     # small-batch decode latency (the reference's headline configurations are batch 1)
     small = None
@@ -567,7 +583,8 @@ def main():
                    "hidden": d["hidden"], "num_k_heads": d["num_k_heads"], "num_v_heads": d["num_v_heads"],
                    "head_dim": 128, "batch": B, "state_dtype": "fp32", "weights": "bf16 N(0,0.02) seed 2"},
         "roofline": roofline, "layer_roofline": layer_roof, "stream_ceiling": ceiling, "prefill": prefill,
-        "stack": stack, "fp8_decode": fp8, "mxfp4_decode": fp4, "small_batch_decode": small,
+        "prefill_lowp_weights": prefill_lowp, "stack": stack, "fp8_decode": fp8, "mxfp4_decode": fp4,
+        "small_batch_decode": small,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
