@@ -93,30 +93,97 @@ def prefill_flops_per_token(d, chunk=64):
     return proj + rec
 
 
-def cpu_baseline(d, w_np, B, seconds, gen_seed=2):
-    """Time the CPU oracle (fp64 C restatement, OpenMP over the host cores) on decode steps of the same
-    workload until about `seconds` have passed (at least one step)."""
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_time(fn, warmup=10, reps=20):
+    """Median wall seconds of `reps` calls after `warmup` untimed ones (the reference's bench protocol,
+    wormhole_n150/qwen3.5_0.8B/bench_decode.py:29-41)."""
+    import statistics
+
+    for _ in range(warmup):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def cpu_baseline(w9, prefill_prefix=256, oracle_seconds=2.0):
+    """The reference's CPU path timed on this host: an fp32 torch restatement of it (oracle/torch_ref.py:
+    ATen GEMMs, the per-token recurrence for decode, the chunk-64 form for prefill), with all the host threads
+    the process may use, 10 warm-ups and the median of 20 runs per row.  Rows: 9B decode at batch 64 (the
+    headline workload), 0.8B decode at batch 1, and the 9B 16k prefill extrapolated from a prefix.  The fp64
+    oracle's rate on the headline workload is kept as a side figure."""
     import numpy as np
+    import torch
 
     import oracle
+    from linear_attention_op_amd import synthetic as syn
+    from oracle.torch_ref import GDNLayerTorchCPU
 
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    gen = torch.Generator().manual_seed(2)
+    rows = {}
+    t_start = time.perf_counter()
+
+    d9 = syn.SHAPES["9b"]
+    lay = GDNLayerTorchCPU(w9, d9)
+    B = 64
+    x = torch.randn(B, d9["hidden"], generator=gen).bfloat16().float()
+    rec = torch.randn(B, d9["num_v_heads"], 128, 128, generator=gen) * 0.01
+    conv = torch.zeros(B, syn.conv_dim(d9), 3)
+    t = _median_time(lambda: lay.decode(x, rec, conv))
+    rows["9b_decode_b64"] = {"tok_per_s": B / t, "ms_per_step": t * 1e3}
+
+    xp = torch.randn(prefill_prefix, d9["hidden"], generator=gen).bfloat16().float()
+
+    def prefill():
+        lay.prefill(xp, torch.zeros(d9["num_v_heads"], 128, 128), torch.zeros(syn.conv_dim(d9), 3))
+
+    t = _median_time(prefill)
+    rows["9b_prefill_16k"] = {"tok_per_s": prefill_prefix / t, "ms_16k_extrapolated": t * 16384 / prefill_prefix * 1e3,
+                              "note": f"extrapolated from a {prefill_prefix}-token prefix (time is linear in T)"}
+    del lay
+
+    d8 = syn.SHAPES["0.8b"]
+    w8, g8 = syn.make_weights(d8, seed=0)
+    lay8 = GDNLayerTorchCPU(w8, d8)
+    x8, s8 = syn.make_inputs(d8, 1, 1, g8, state_std=0.01)
+    conv8 = torch.zeros(1, syn.conv_dim(d8), 3)
+    t = _median_time(lambda: lay8.decode(x8[:, 0], s8, conv8))
+    rows["0.8b_decode_b1"] = {"tok_per_s": 1 / t, "us_per_step": t * 1e6}
+
+    # side figure: the fp64 C oracle (naive loops, OpenMP) on the headline workload
     oracle.set_threads(threads)
-    rng = np.random.default_rng(gen_seed)
-    dm = oracle.dims(d["hidden"], d["num_k_heads"], d["num_v_heads"], d["head_k_dim"], d["head_v_dim"])
-    rec = (rng.standard_normal((B, d["num_v_heads"], d["head_k_dim"], d["head_v_dim"])) * 0.01).astype(np.float32)
-    conv = np.zeros((B, 2 * d["num_k_heads"] * d["head_k_dim"] + d["num_v_heads"] * d["head_v_dim"], 3), np.float32)
-    x = rng.standard_normal((B, 1, d["hidden"])).astype(np.float32)
-    oracle.layer_forward(dm, w_np, x, rec, conv)  # warm-up (page-in, thread pool)
-    steps, t0 = 0, time.perf_counter()
-    while True:
-        oracle.layer_forward(dm, w_np, x, rec, conv)
-        steps += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or steps >= 50:
-            break
-    return {"value": B * steps / el, "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"{steps} decode steps of the 9B layer at batch {B} (fp64 oracle, {el:.1f} s)"}
+    dm = oracle.dims(d9["hidden"], d9["num_k_heads"], d9["num_v_heads"], 128, 128)
+    wn = {k: v.float().numpy() for k, v in w9.items()}
+    rec_o = rec.numpy().copy()
+    conv_o = np.zeros((B, syn.conv_dim(d9), 3), np.float32)
+    xo = x.numpy()[:, None]
+    oracle.layer_forward(dm, wn, xo, rec_o, conv_o)
+    n, t0 = 0, time.perf_counter()
+    while n < 1 or time.perf_counter() - t0 < oracle_seconds:
+        oracle.layer_forward(dm, wn, xo, rec_o, conv_o)
+        n += 1
+    rows["9b_decode_b64_fp64_oracle"] = {"tok_per_s": B * n / (time.perf_counter() - t0),
+                                         "note": "fp64 naive-loop oracle, side figure only"}
+    head = rows["9b_decode_b64"]
+    return {"value": head["tok_per_s"], "unit": "tok/s", "cores": threads, "kind": "port",
+            "sample": "fp32 torch restatement of the reference's CPU path (oracle/torch_ref.py), 9B decode at "
+                      "batch 64: median of 20 steps after 10 warm-ups",
+            "cpu_model": _cpu_model(), "rows": rows, "seconds": time.perf_counter() - t_start}
 
 
 CAL_BYTES = 1 << 30      # the calibration copy in the counter passes
@@ -146,6 +213,40 @@ def pmc_child(steps=4):
         lay(x)
     torch.cuda.synchronize()
     lay.close()
+
+
+def profile_child(which):
+    """Workload for an external profiler (rocprofv3 --kernel-trace / --pmc put this process after `--`):
+    `decode`: 9B decode at batch 64, 4 layer copies rotated as in the benchmark, 3 warm-up + 12 steps;
+    `prefill`: one 16384-token prefill of a 9B layer, 1 warm-up + 3 runs."""
+    import torch
+
+    from linear_attention_op_amd import Qwen35GatedDeltaNetHIP
+    from linear_attention_op_amd import synthetic as syn
+
+    dev = torch.device("cuda", 0)
+    d = syn.SHAPES["9b"]
+    w, _ = syn.make_weights(d, seed=2)
+    if which == "decode":
+        layers = []
+        for i in range(4):
+            gg = torch.Generator(device=dev).manual_seed(100 + i)
+            wi = w if i == 0 else {k: (torch.randn(v.shape, generator=gg, device=dev) * v.float().std()).to(v.dtype)
+                                   if k.startswith("w_") or k == "conv_w" else v for k, v in w.items()}
+            lay = Qwen35GatedDeltaNetHIP(wi, dims=d, batch=64, max_tokens=64)
+            lay.set_state(rec=torch.randn(64, d["num_v_heads"], 128, 128, device=dev) * 0.01)
+            layers.append(lay)
+        x = torch.randn(64, 1, d["hidden"], device=dev).to(torch.bfloat16)
+        for i in range(15):
+            layers[i % 4](x)
+    else:
+        lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=1, max_tokens=16384)
+        x = torch.randn(1, 16384, d["hidden"], device=dev).to(torch.bfloat16)
+        for _ in range(4):
+            lay.reset_state()
+            lay(x)
+    torch.cuda.synchronize()
+    print(f"profile child {which}: done", flush=True)
 
 
 def measure_traffic(kernel="mixer_kernel", timeout=180):
@@ -191,26 +292,63 @@ def measure_traffic(kernel="mixer_kernel", timeout=180):
     return {"bytes": out["FETCH_SIZE"]["bytes"] + out["WRITE_SIZE"]["bytes"], "passes": out}, None
 
 
-def stream_ceiling(nbytes, copies=4, reps=40):
-    """In-place read + write of `nbytes` (torch's elementwise scale) over `copies` rotating buffers, so that the
-    256 MB last-level cache cannot hold them: the HBM rate a plain streaming kernel with the decode state's
-    access pattern (read once, write once) reaches on this device."""
+STREAM_MODES = {0: "read", 1: "write", 2: "copy", 3: "in_place"}
+
+
+def hbm_ceiling(buf_bytes=512 << 20, copies=4, reps=4, sweep_log=None):
+    """The HBM rate a purpose-built stream kernel reaches on this device (csrc/hbm_stream.hip): read-only,
+    write-only, copy and in-place read + write, each over `copies` rotating buffers of `buf_bytes` (more than
+    the 256 MB Infinity Cache in all), swept over 16-byte accesses in flight per thread (1-16), non-temporal
+    accesses off / on and the grid size.  Returns {mode: best row} (GB/s, the fraction of 8 TB/s and the
+    configuration); every row goes to `sweep_log` if given."""
+    import ctypes
+
     import torch
 
-    bufs = [torch.ones(nbytes // 4, device="cuda") for _ in range(copies)]
-    for b in bufs:
-        b.mul_(1.0000001)
+    lib = ctypes.CDLL(os.path.join(ROOT, "linear_attention_op_amd", "libgdn_stream.so"))
+    fn = lib.gdn_stream_run
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                   ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    src = [torch.ones(buf_bytes // 4, device="cuda") for _ in range(copies)]
+    dst = [torch.zeros(buf_bytes // 4, device="cuda") for _ in range(copies)]
+    sink = torch.zeros(256, device="cuda")
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    n4 = buf_bytes // 16
+    best = {}
+    rows = []
+    for mode in (0, 1, 2, 3):
+        moved = buf_bytes * (2 if mode in (2, 3) else 1)
+        for unroll in (1, 2, 4, 8, 16):
+            for nt in (0, 1):
+                for blocks in (1024, 2048, 4096, 8192, -1):
+                    nb = blocks if blocks > 0 else (n4 + 256 * unroll - 1) // (256 * unroll)
+
+                    def run(i):
+                        rc = fn(mode, unroll, nt, ctypes.c_void_p(src[i].data_ptr()),
+                                ctypes.c_void_p(dst[i].data_ptr()), buf_bytes, nb, ctypes.c_void_p(sink.data_ptr()), st)
+                        if rc:
+                            raise RuntimeError(f"gdn_stream_run returned {rc}")
+
+                    for i in range(copies):
+                        run(i)
+                    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    for r in range(reps * copies):
+                        run(r % copies)
+                    e1.record()
+                    torch.cuda.synchronize()
+                    sec = e0.elapsed_time(e1) / 1e3 / (reps * copies)
+                    row = {"mode": STREAM_MODES[mode], "unroll": unroll, "nontemporal": nt, "blocks": nb,
+                           "GBps": moved / sec / 1e9, "frac": moved / sec / HBM_PEAK}
+                    rows.append(row)
+                    if sweep_log:
+                        print(json.dumps(row), file=sweep_log, flush=True)
+                    if row["GBps"] > best.get(row["mode"], {"GBps": 0})["GBps"]:
+                        best[row["mode"]] = row
+    del src, dst
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(reps):
-        bufs[i % copies].mul_(1.0000001)
-    e1.record()
-    torch.cuda.synchronize()
-    sec = e0.elapsed_time(e1) / 1e3 / reps
-    del bufs
-    return {"op": f"torch in-place fp32 scale, {copies} rotating buffers of {nbytes / 1e6:.1f} MB",
-            "bytes": 2 * nbytes, "us": sec * 1e6, "GBps": 2 * nbytes / sec / 1e9, "frac": 2 * nbytes / sec / HBM_PEAK}
+    return best
 
 
 def prefill_bench(w, d, T, steps, weight_dtype="bf16"):
@@ -296,45 +434,26 @@ def small_batch_decode(shape, B, copies=8, steps=400, warmup=40, weight_dtype="b
 
 
 def stack_bench(d, n_layers=24, n_prefill=8, prefill_len=2048, n_decode=56, steps=3, warmup=1, seed=4):
-    """Continuous batching through a stack of 9B-shape layers with the decoder RMSNorm between layers:
-    every step carries the next prefill_len tokens of n_prefill prompts (chunked prefill, states carried)
-    and one token for each of n_decode streams, in one variable-length launch per layer.  The decode
-    streams start from 0.01 randn states (a GDN state has constant size, so a long context only changes
-    its values).  Weights: projections N(0, 0.02) in bf16 drawn on the GPU, the rest as synthetic.py."""
+    """Continuous batching through a stack of 9B-shape layers with the decoder RMSNorm between layers
+    (synthetic.continuous_batch, seed 4): every step carries the next prefill_len tokens of n_prefill prompts
+    (chunked prefill, states carried) and one token for each of n_decode streams, in one variable-length
+    launch per layer.  The decode streams start from 0.01 randn states (a GDN state has constant size, so a
+    long context only changes its values)."""
     import torch
 
     from linear_attention_op_amd import Qwen35GDNStackHIP
     from linear_attention_op_amd import synthetic as syn
 
-    dev = torch.device("cuda", 0)
-    gg = torch.Generator(device=dev).manual_seed(seed)
-    _, gen = syn.make_weights(syn.SHAPES["tiny"], seed=seed)
-    H, nv, dv, C = d["hidden"], d["num_v_heads"], d["head_v_dim"], syn.conv_dim(d)
-    Vd = nv * dv
-
-    def n(*shape):
-        return (torch.randn(*shape, generator=gg, device=dev) * 0.02).to(torch.bfloat16)
-
-    layers = []
-    for _ in range(n_layers):
-        layers.append({"w_qkv": n(C, H), "w_z": n(Vd, H), "w_a": n(nv, H), "w_b": n(nv, H),
-                       "conv_w": n(C, 4).float(), "w_out": n(H, Vd),
-                       "norm_w": torch.rand(dv, generator=gen) + 0.5,
-                       "dt_bias": torch.rand(nv, generator=gen) * 2.0 - 1.0,
-                       "A_log": torch.log(torch.rand(nv, generator=gen) * 16.0).clamp_min(-20.0)})
-    n_seq = n_prefill + n_decode
-    rows = n_prefill * prefill_len + n_decode
+    layers, cu, x, s0 = syn.continuous_batch(d, n_layers=n_layers, n_prefill=n_prefill, prefill_len=prefill_len,
+                                             n_decode=n_decode, seed=seed)
+    n_seq, rows = n_prefill + n_decode, cu[-1]
     stack = Qwen35GDNStackHIP(layers, dims=d, batch=n_seq, max_slots=n_seq, max_tokens=rows, inter_norm=True)
     del layers
-    dec_slots = torch.arange(n_prefill, n_seq, dtype=torch.int32, device=dev)
-    for L in stack.layers:
-        L.set_state(rec=torch.randn(n_decode, nv, d["head_k_dim"], dv, generator=gg, device=dev) * 0.01,
-                    slot_ids=dec_slots)
-    cu = [0]
-    for i in range(n_seq):
-        cu.append(cu[-1] + (prefill_len if i < n_prefill else 1))
-    slots = torch.arange(n_seq, dtype=torch.int32, device=dev)
-    xs = [torch.randn(rows, H, generator=gg, device=dev).to(torch.bfloat16) for _ in range(2)]
+    slots = torch.arange(n_seq, dtype=torch.int32, device="cuda")
+    for L, s in zip(stack.layers, s0):
+        L.set_state(rec=s, slot_ids=slots[n_prefill:])
+    del s0
+    xs = [x, torch.roll(x, 1, 0)]
     for i in range(warmup):
         stack.forward_varlen(xs[i % 2], cu, slots)
     torch.cuda.synchronize()
@@ -356,6 +475,9 @@ def main():
     if "--pmc-child" in sys.argv:
         pmc_child()
         return
+    if "--profile-child" in sys.argv:
+        profile_child(sys.argv[sys.argv.index("--profile-child") + 1])
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
@@ -365,14 +487,14 @@ def main():
     ap.add_argument("--prefill-len", type=int, default=16384)
     ap.add_argument("--prefill-steps", type=int, default=3)
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--graph", type=int, default=0,
                     help="1: replay the decode step from HIP graphs; 0: launch eagerly (faster here: 104 vs 112 us)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-fp8", action="store_true", help="skip the FP8- and MXFP4-weight decode and prefill measurements")
     ap.add_argument("--no-small", action="store_true", help="skip the batch-1/8 decode latencies")
-    ap.add_argument("--stack", action="store_true",
-                    help="also run the 24-layer continuous-batching stack (8 x 2048 prefill + 56 decode per step)")
+    ap.add_argument("--no-stack", action="store_true",
+                    help="skip the 24-layer continuous-batching stack (8 x 2048 prefill + 56 decode per step)")
+    ap.add_argument("--stream-log", default=None, help="write every row of the HBM stream sweep to this file")
     ap.add_argument("--no-traffic", action="store_true",
                     help="skip the two rocprofv3 counter passes (required when bench.py itself runs under rocprofv3)")
     args = ap.parse_args()
@@ -484,11 +606,13 @@ def main():
                   "event_step_us": stage_avg_ms["total"] * 1e3,
                   "event_frac": step_bytes / (stage_avg_ms["total"] / 1e3) / HBM_PEAK,
                   "stage_us": {k: v * 1e3 for k, v in stage_avg_ms.items()}}
-    # the practical ceiling for the mixer's traffic: a plain stream over the same state bytes
-    ceiling = stream_ceiling(B * d["num_v_heads"] * 128 * 128 * 4)
-    roofline["frac_of_stream"] = roofline["achieved"] / ceiling["GBps"]
-    print(f"[bench] stream ceiling: {ceiling['GBps']:.0f} GB/s ({ceiling['frac'] * 100:.0f}% of peak); mixer "
-          f"{roofline['achieved']:.0f} GB/s", file=sys.stderr, flush=True)
+    # the practical ceiling for the mixer's traffic: the best in-place read + write stream (the state's access
+    # pattern) a purpose-built kernel reaches here, and the best read-only, write-only and copy streams
+    ceiling = hbm_ceiling(sweep_log=open(args.stream_log, "w") if args.stream_log else None)
+    roofline["frac_of_stream"] = roofline["achieved"] / ceiling["in_place"]["GBps"]
+    print(f"[bench] stream ceiling: " + ", ".join(f"{k} {v['GBps']:.0f} GB/s ({v['frac'] * 100:.0f}%)"
+                                                   for k, v in ceiling.items()) +
+          f"; mixer {roofline['achieved']:.0f} GB/s", file=sys.stderr, flush=True)
     print(f"[bench] decode B={B}: {ms_per_step * 1e3:.1f} us/step wall ({'graph' if args.graph else 'eager'}), "
           f"eager stages (us) "
           f"{ {k: round(v * 1e3, 1) for k, v in stage_avg_ms.items()} }", file=sys.stderr, flush=True)
@@ -563,7 +687,7 @@ def main():
                   f"{r['hbm_frac'] * 100:.0f}% of HBM roofline", file=sys.stderr, flush=True)
 
     stack = None
-    if args.stack:
+    if not args.no_stack:
         print("[bench] 24-layer continuous-batching stack", file=sys.stderr, flush=True)
         stack = stack_bench(d)
         print(f"[bench] stack: {stack['ms_per_step']:.1f} ms/step, {stack['tok_per_s']:.0f} tok/s", file=sys.stderr,
@@ -571,8 +695,12 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        print("[bench] timing the CPU oracle", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(d, syn.to_numpy(w0), B, args.cpu_seconds)
+        print("[bench] timing the reference's CPU path (fp32 torch restatement) on the host", file=sys.stderr,
+              flush=True)
+        cpu = cpu_baseline({k: v.float().cpu() for k, v in w0.items()})
+        print(f"[bench] CPU baseline ({cpu['cores']} threads, {cpu['cpu_model']}): "
+              f"{ {k: round(v['tok_per_s'], 1) for k, v in cpu['rows'].items()} } tok/s", file=sys.stderr,
+              flush=True)
 
     line = {
         "metric": METRIC, "value": value, "unit": "tok/s", "n_gpus": 1, "steps": args.steps,

@@ -14,6 +14,11 @@
  *   - `stream` is a hipStream_t (NULL = the default stream).  Calls are asynchronous on that stream
  *     except gdn_layer_create/destroy, which synchronise the device.
  *   - A gdn_layer handle is not thread-safe.  Two sequences of one launch must not share a state slot.
+ *   - Slot ids are device int32 arrays with values in [0, max_slots).  The library cannot read them on the
+ *     host without a synchronisation, so the kernels check them: a sequence (or state-call entry) whose id
+ *     is outside that range is skipped -- its states are not touched and its output rows are left
+ *     unwritten.  Callers that hold the ids on the host check them first (the Python mirror raises
+ *     GdnValueError before any launch).
  */
 #ifndef GDN_H
 #define GDN_H
@@ -39,7 +44,9 @@ typedef enum gdn_status {
 } gdn_status;
 
 /* Layer geometry (HF Qwen3_5TextConfig fields; 9B/gdn_layer.py:58-64).  Supported: head_k_dim ==
- * head_v_dim in {32, 64, 128}, num_v_heads % num_k_heads == 0, conv_kernel == 4, hidden % 128 == 0. */
+ * head_v_dim in {32, 64, 128}, num_v_heads % num_k_heads == 0 with num_v_heads / num_k_heads <= 4,
+ * conv_kernel == 4, hidden % 128 == 0, num_v_heads * head_v_dim % 128 == 0.  Other geometries are
+ * GDN_ERR_UNSUPPORTED at create time. */
 typedef struct gdn_dims {
     int hidden;        /* H: 4096 (9B), 1024 (0.8B) */
     int num_k_heads;   /* nk: 16 */
@@ -125,16 +132,23 @@ int gdn_state_get(gdn_layer* layer, const int* slot_ids, int n, float* rec, floa
 int gdn_state_set(gdn_layer* layer, const int* slot_ids, int n, const float* rec, const float* conv, void* stream);
 
 /* Device addresses of the resident state buffers (for address-stability checks,
- * 9B/test_gated_delta_l1.py:81-92).  rec: [max_slots, nv, dk, dv] fp32; conv: [max_slots, nv, 3, 2dk + dv]
- * fp32, the last 3 pre-conv inputs of each v-head's channels in time order (entry 2 = newest). */
-int gdn_layer_state_buffers(gdn_layer* layer, void** rec, void** conv);
+ * 9B/test_gated_delta_l1.py:81-92); any output may be NULL.  rec: [max_slots, nv, dk, dv] fp32.
+ * conv: the conv history rings, [max_slots, nk, 4, 2 dk + R dv] fp32 with R = nv / nk: per slot and k-head
+ * group kh the pre-conv inputs of the group's channels (q and k of kh, then v of the v-heads R kh ..
+ * R kh + R - 1), the input of token time tau at entry tau % 4.  conv_pos: int32 [max_slots, nv], pos = tokens
+ * seen % 4 per v-head (equal for all v-heads of a slot); the window of the next token, time order j = 0
+ * (oldest) .. 2, is entry (pos + 1 + j) % 4.  A launch of T tokens writes only its last min(T, 3) inputs, one
+ * entry per token, and advances pos by T. */
+int gdn_layer_state_buffers(gdn_layer* layer, void** rec, void** conv, void** conv_pos);
 
-/* Stage timing with HIP events recorded on the launch stream at the stage boundaries of every
- * gdn_layer_forward call (no counterpart in the reference, whose benches read the tt-metal device
- * profiler, wormhole_n150/qwen3.5_0.8B/bench_decode.py:35-37).  gdn_layer_profile(layer, n) starts
- * recording for up to n calls (n = 0 stops); gdn_layer_profile_read synchronises on the last event and
+/* Stage timing with HIP events recorded on the launch stream at the stage boundaries of every launch of
+ * the layer (no counterpart in the reference, whose benches read the tt-metal device profiler,
+ * wormhole_n150/qwen3.5_0.8B/bench_decode.py:35-37).  A launch is one gdn_layer_forward or
+ * gdn_layer_forward_varlen call of at most max_tokens rows; a longer gdn_layer_forward call is split into
+ * launches of at most max_tokens rows and records one set per launch.  gdn_layer_profile(layer, n) starts
+ * recording for up to n launches (n = 0 stops); gdn_layer_profile_read synchronises on the last event and
  * writes the summed milliseconds per stage: ms[0] in_proj, ms[1] mixer (conv .. gated RMSNorm),
- * ms[2] out_proj, ms[3] whole call; *calls = number of calls recorded. */
+ * ms[2] out_proj, ms[3] whole launch; *calls = number of launches recorded. */
 int gdn_layer_profile(gdn_layer* layer, int max_calls);
 int gdn_layer_profile_read(gdn_layer* layer, double* ms, int* calls);
 
@@ -189,11 +203,12 @@ int gdn_stack_destroy(gdn_stack* stack);
 int gdn_stack_layer(gdn_stack* stack, int i, gdn_layer** layer);
 
 /* gdn_l1.py:294-341 (forward_device / __call__(hidden_states, layers)): layers [first, first + count) on
- * x bf16 [B*T, H] -> out bf16 [B*T, H], B*T <= max_tokens; slot_ids as in gdn_layer_forward. */
+ * x bf16 [B*T, H] -> out bf16 [B*T, H]; slot_ids as in gdn_layer_forward.  Launches of more than max_tokens
+ * rows run token blocks of at most max_tokens rows through all the layers in turn (B <= max_tokens). */
 int gdn_stack_forward(gdn_stack* stack, const void* x, int B, int T, const int* slot_ids, int first, int count,
                       void* out, void* stream);
 
-/* The same over a variable-length launch (see gdn_layer_forward_varlen). */
+/* The same over a variable-length launch (see gdn_layer_forward_varlen; at most max_tokens rows). */
 int gdn_stack_forward_varlen(gdn_stack* stack, const void* x, int n_seqs, const int* cu_seqlens,
                              const int* slot_ids, int first, int count, void* out, void* stream);
 

@@ -85,7 +85,7 @@ SIGNATURES = {
     "gdn_state_reset": (_I, [_V, _V, _I, _V]),
     "gdn_state_get": (_I, [_V, _V, _I, _V, _V, _V]),
     "gdn_state_set": (_I, [_V, _V, _I, _V, _V, _V]),
-    "gdn_layer_state_buffers": (_I, [_V, ctypes.POINTER(_V), ctypes.POINTER(_V)]),
+    "gdn_layer_state_buffers": (_I, [_V, ctypes.POINTER(_V), ctypes.POINTER(_V), ctypes.POINTER(_V)]),
     "gdn_layer_proj_width": (_I, [_V]),
     "gdn_layer_profile": (_I, [_V, _I]),
     "gdn_layer_profile_read": (_I, [_V, ctypes.POINTER(ctypes.c_double), ctypes.POINTER(_I)]),

@@ -2,7 +2,8 @@
 
     python -m linear_attention_op_amd.build        # or __graft_entry__.build()
 
-Objects go to linear_attention_op_amd/_build/, the library to linear_attention_op_amd/libgdn_hip.so.
+Objects go to linear_attention_op_amd/_build/, the library to linear_attention_op_amd/libgdn_hip.so.  The HBM
+stream probe (csrc/hbm_stream.hip), a measurement yardstick that only bench.py loads, becomes libgdn_stream.so.
 """
 
 import os
@@ -18,6 +19,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 
 SOURCES = ["gdn_linear.hip", "gdn_mixer.hip", "gdn_delta.hip", "gdn_chunk.hip", "gdn_api.cpp"]
+STREAM_SOURCES = ["hbm_stream.hip"]
+STREAM_LIB = os.path.join(HERE, "libgdn_stream.so")
 
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-result",
@@ -41,18 +44,24 @@ def _compile(src):
     return obj
 
 
-def build(verbose=True):
-    os.makedirs(BUILD, exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 4)) as ex:
-        objs = list(ex.map(_compile, SOURCES))
-    tmp = LIB + ".tmp"
+def _link(objs, lib, verbose):
+    tmp = lib + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
     if verbose:
-        print(f"built {LIB}", file=sys.stderr)
+        print(f"built {lib}", file=sys.stderr)
+
+
+def build(verbose=True):
+    os.makedirs(BUILD, exist_ok=True)
+    srcs = SOURCES + STREAM_SOURCES
+    with ThreadPoolExecutor(max_workers=min(len(srcs), os.cpu_count() or 4)) as ex:
+        objs = list(ex.map(_compile, srcs))
+    _link(objs[:len(SOURCES)], LIB, verbose)
+    _link(objs[len(SOURCES):], STREAM_LIB, verbose)
     return LIB
 
 

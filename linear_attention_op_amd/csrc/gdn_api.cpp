@@ -73,7 +73,8 @@ struct gdn_layer {
     float* dt_bias = nullptr; // [nv]
     float* norm_w = nullptr;  // [dv]
     float* rec = nullptr;     // [slots, nv, dk, dv]
-    float* conv = nullptr;    // [slots, nv, 3, CH] conv history, time order
+    float* conv = nullptr;    // [slots, nk, 4, CH] conv history rings, one per k-head group
+    int* conv_pos = nullptr;  // [slots, nv] ring positions, one per v-head
 
     int* iota = nullptr;      // [max_slots] identity slot ids (slot offsets of varlen groups)
 
@@ -138,6 +139,9 @@ int check_dims(const gdn_dims* d) {
     if (d->hidden % 128) return fail(GDN_ERR_UNSUPPORTED, "hidden %d is not a multiple of 128", d->hidden);
     if ((d->num_v_heads * d->head_v_dim) % 128)
         return fail(GDN_ERR_UNSUPPORTED, "value dim %d is not a multiple of 128", d->num_v_heads * d->head_v_dim);
+    // the fused mixer runs a k-head group (k-head and its v-heads, 256 threads each) in one workgroup
+    if (d->num_v_heads / d->num_k_heads > 4)
+        return fail(GDN_ERR_UNSUPPORTED, "num_v_heads / num_k_heads = %d (at most 4)", d->num_v_heads / d->num_k_heads);
     return GDN_OK;
 }
 
@@ -185,7 +189,8 @@ hipError_t in_proj_rows(const gdn_layer* L, const void* x, int xl, int M, float*
     hipError_t e = gdn::launch_linear(x, xl, q.w, q.layout, q.scale, M, N1, H, P, L->NP, gdn::OUT_F32, st);
     if (e != hipSuccess) return e;
     // the a | b rows: for prefills the GEMV with the roles swapped (the activations streamed once)
-    if (M > 64) return gdn::launch_linear_rows_t(x, L->w_ab, nab, M, H, P + N1, L->NP, st);
+    // (at most 64 weight rows; wider a | b blocks run as an ordinary projection)
+    if (M > 64 && nab <= 64) return gdn::launch_linear_rows_t(x, L->w_ab, nab, M, H, P + N1, L->NP, st);
     return gdn::launch_linear(x, xl, L->w_ab, gdn::W_FRAG, nullptr, M, nab, H, P + N1, L->NP, gdn::OUT_F32, st);
 }
 
@@ -216,7 +221,7 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, u16* o
     // the fused mixer writes y straight into W_FRAG layout when it produces every row
     const bool y_frag = frag && ng == 1 && grp[0].T <= kFusedMaxT;
     // decode: q | k | v | z over workgroups balanced on the CUs, a | b as partial sums for the mixer
-    const bool split_ab = frag && L->CD + Vd == L->NP - 2 * nv;
+    const bool split_ab = frag && gdn::in_proj_decode_supported(L->CD + Vd, L->d.hidden);
     bool ab_split = false;
     if (frag) {
         bool mixer_only = true;
@@ -241,10 +246,10 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, u16* o
         if (g.T <= kFusedMaxT) {
             gdn::MixerArgs a{};
             a.P = L->P + r0 * L->NP, a.NP = L->NP, a.B = g.B, a.T = g.T, a.slot_ids = g.slots;
-            a.nk = d.num_k_heads, a.nv = nv;
+            a.max_slots = L->max_slots, a.nk = d.num_k_heads, a.nv = nv;
             a.conv_w = L->conv_w, a.neg_A = L->neg_A, a.dt_bias = L->dt_bias, a.norm_w = L->norm_w;
             a.eps = d.rms_norm_eps;
-            a.rec_state = L->rec, a.conv_state = L->conv;
+            a.rec_state = L->rec, a.conv_state = L->conv, a.conv_pos = L->conv_pos;
             a.y = y_frag ? L->y : L->y + r0 * Vd, a.y_frag = y_frag ? 1 : 0, a.o_tap = nullptr;
             a.ab = ab_split ? L->ab + r0 * 2 * nv : nullptr, a.ab_splits = kAbSplits;
             a.ab_stride = (size_t)M * 2 * nv;
@@ -252,24 +257,24 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, u16* o
         } else {
             float* P = L->P + r0 * L->NP;
             gdn::FrontArgs f{};
-            f.P = P, f.NP = L->NP, f.B = g.B, f.T = g.T, f.slot_ids = g.slots;
+            f.P = P, f.NP = L->NP, f.B = g.B, f.T = g.T, f.slot_ids = g.slots, f.max_slots = L->max_slots;
             f.nk = d.num_k_heads, f.nv = nv, f.dk = d.head_k_dim, f.dv = d.head_v_dim;
             f.conv_w = L->conv_w, f.neg_A = L->neg_A, f.dt_bias = L->dt_bias;
-            f.conv_state = L->conv;
+            f.conv_state = L->conv, f.conv_pos = L->conv_pos;
             f.qn = L->qn + r0 * Kd, f.kn = L->kn + r0 * Kd, f.v = L->v + r0 * Vd;
             f.g = L->g + r0 * nv, f.beta = L->beta + r0 * nv;
             gdn::DeltaArgs r{};
             r.q = f.qn, r.k = f.kn, r.v = f.v, r.g = f.g, r.beta = f.beta;
             r.B = g.B, r.T = g.T, r.Hk = d.num_k_heads, r.Hv = nv, r.slot_ids = g.slots;
-            r.state = L->rec, r.o = L->o + r0 * Vd, r.normalize = 0, r.scale = 1.f;
+            r.max_slots = L->max_slots, r.state = L->rec, r.o = L->o + r0 * Vd, r.normalize = 0, r.scale = 1.f;
             if (L->chunk_ws && gdn::delta_chunked_supported(d.head_k_dim, d.head_v_dim) &&
                 gdn::delta_chunked_workspace(g.B, g.T, nv, d.head_k_dim, d.head_v_dim) <= L->chunk_ws_bytes) {
                 // chunked recurrence with the front end computed inside its chunk preparation
-                HIP_OK(gdn::launch_front_chunked(f, L->conv, r, L->chunk_ws, L->chunk_ws_bytes, st));
+                HIP_OK(gdn::launch_front_chunked(f, L->conv, L->conv_pos, r, L->chunk_ws, L->chunk_ws_bytes, st));
             } else {
                 HIP_OK(gdn::launch_conv_front(f, st));
-                HIP_OK(gdn::launch_conv_commit(P, L->NP, g.B, g.T, g.slots, d.num_k_heads, nv, d.head_k_dim,
-                                               d.head_v_dim, L->conv, st));
+                HIP_OK(gdn::launch_conv_commit(P, L->NP, g.B, g.T, g.slots, L->max_slots, d.num_k_heads, nv,
+                                               d.head_k_dim, d.head_v_dim, L->conv, L->conv_pos, st));
                 HIP_OK(run_delta(L, r, st));
             }
             HIP_OK(gdn::launch_gated_rmsnorm(r.o, Mg, nv, d.head_v_dim, P + L->CD, L->NP, L->norm_w,
@@ -365,7 +370,7 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
     const gdn_dims& d = L->d;
     const int H = d.hidden, nk = d.num_k_heads, nv = d.num_v_heads, dk = d.head_k_dim, dv = d.head_v_dim;
     L->Kd = nk * dk, L->Vd = nv * dv, L->CD = 2 * L->Kd + L->Vd, L->NP = L->CD + L->Vd + 2 * nv;
-    L->CH = 2 * dk + dv;
+    L->CH = gdn::conv_group_width(dk, dv, nv / nk);
     L->max_slots = max_slots, L->max_tokens = max_tokens;
     L->wfmt = wfmt;
     const size_t MT = (size_t)max_tokens;
@@ -398,7 +403,8 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
     take(L->alloc(&L->dt_bias, (size_t)nv));
     take(L->alloc(&L->norm_w, (size_t)dv));
     take(L->alloc(&L->rec, (size_t)max_slots * nv * dk * dv));
-    take(L->alloc(&L->conv, (size_t)max_slots * nv * 3 * L->CH));
+    take(L->alloc(&L->conv, (size_t)max_slots * nk * gdn::CONV_RING * L->CH));
+    take(L->alloc(&L->conv_pos, (size_t)max_slots * nv));
     take(L->alloc(&L->iota, (size_t)max_slots));
     if (share) {
         L->owns_ws = false;
@@ -485,8 +491,8 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
         for (int i = 0; i < max_slots; ++i) ids[i] = i;
         e = hipMemcpy(L->iota, ids.data(), max_slots * sizeof(int), hipMemcpyHostToDevice);
     }
-    if (e == hipSuccess) e = gdn::launch_state_zero(L->rec, L->conv, nullptr, max_slots, nv, dk, dv,
-                                                    L->CH, nullptr);
+    if (e == hipSuccess) e = gdn::launch_state_zero(L->rec, L->conv, L->conv_pos, nullptr, max_slots, max_slots, nk,
+                                                    nv, dk, dv, nullptr);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         delete L;
@@ -540,8 +546,8 @@ int gdn_state_reset(gdn_layer* L, const int* slot_ids, int n, void* stream) {
     if (!L) return fail(GDN_ERR_INVALID_ARG, "layer is NULL");
     if (n < 0 || (!slot_ids && n > L->max_slots)) return fail(GDN_ERR_SLOT, "bad slot count %d", n);
     const gdn_dims& d = L->d;
-    HIP_OK(gdn::launch_state_zero(L->rec, L->conv, slot_ids, n, d.num_v_heads, d.head_k_dim,
-                                  d.head_v_dim, L->CH, as_stream(stream)));
+    HIP_OK(gdn::launch_state_zero(L->rec, L->conv, L->conv_pos, slot_ids, n, L->max_slots, d.num_k_heads,
+                                  d.num_v_heads, d.head_k_dim, d.head_v_dim, as_stream(stream)));
     return GDN_OK;
 }
 
@@ -549,8 +555,8 @@ int gdn_state_get(gdn_layer* L, const int* slot_ids, int n, float* rec, float* c
     if (!L || (!rec && !conv)) return fail(GDN_ERR_INVALID_ARG, "gdn_state_get: NULL argument");
     if (n < 0 || (!slot_ids && n > L->max_slots)) return fail(GDN_ERR_SLOT, "bad slot count %d", n);
     const gdn_dims& d = L->d;
-    HIP_OK(gdn::launch_state_export(L->rec, L->conv, slot_ids, n, d.num_k_heads, d.num_v_heads,
-                                    d.head_k_dim, d.head_v_dim, rec, conv, as_stream(stream)));
+    HIP_OK(gdn::launch_state_export(L->rec, L->conv, L->conv_pos, slot_ids, n, L->max_slots, d.num_k_heads,
+                                    d.num_v_heads, d.head_k_dim, d.head_v_dim, rec, conv, as_stream(stream)));
     return GDN_OK;
 }
 
@@ -558,15 +564,16 @@ int gdn_state_set(gdn_layer* L, const int* slot_ids, int n, const float* rec, co
     if (!L) return fail(GDN_ERR_INVALID_ARG, "layer is NULL");
     if (n < 0 || (!slot_ids && n > L->max_slots)) return fail(GDN_ERR_SLOT, "bad slot count %d", n);
     const gdn_dims& d = L->d;
-    HIP_OK(gdn::launch_state_import(L->rec, L->conv, slot_ids, n, d.num_k_heads, d.num_v_heads,
-                                    d.head_k_dim, d.head_v_dim, rec, conv, as_stream(stream)));
+    HIP_OK(gdn::launch_state_import(L->rec, L->conv, L->conv_pos, slot_ids, n, L->max_slots, d.num_k_heads,
+                                    d.num_v_heads, d.head_k_dim, d.head_v_dim, rec, conv, as_stream(stream)));
     return GDN_OK;
 }
 
-int gdn_layer_state_buffers(gdn_layer* L, void** rec, void** conv) {
+int gdn_layer_state_buffers(gdn_layer* L, void** rec, void** conv, void** conv_pos) {
     if (!L) return fail(GDN_ERR_INVALID_ARG, "layer is NULL");
     if (rec) *rec = L->rec;
     if (conv) *conv = L->conv;
+    if (conv_pos) *conv_pos = L->conv_pos;
     return GDN_OK;
 }
 
@@ -616,14 +623,14 @@ int gdn_conv_front(gdn_layer* L, const float* P, int B, int T, const int* slot_i
     const gdn_dims& d = L->d;
     const hipStream_t st = as_stream(stream);
     gdn::FrontArgs f{};
-    f.P = P, f.NP = L->NP, f.B = B, f.T = T, f.slot_ids = slot_ids;
+    f.P = P, f.NP = L->NP, f.B = B, f.T = T, f.slot_ids = slot_ids, f.max_slots = L->max_slots;
     f.nk = d.num_k_heads, f.nv = d.num_v_heads, f.dk = d.head_k_dim, f.dv = d.head_v_dim;
     f.conv_w = L->conv_w, f.neg_A = L->neg_A, f.dt_bias = L->dt_bias;
-    f.conv_state = L->conv;
+    f.conv_state = L->conv, f.conv_pos = L->conv_pos;
     f.qn = qn, f.kn = kn, f.v = v, f.g = g, f.beta = beta;
     HIP_OK(gdn::launch_conv_front(f, st));
-    HIP_OK(gdn::launch_conv_commit(P, L->NP, B, T, slot_ids, d.num_k_heads, d.num_v_heads, d.head_k_dim,
-                                   d.head_v_dim, L->conv, st));
+    HIP_OK(gdn::launch_conv_commit(P, L->NP, B, T, slot_ids, L->max_slots, d.num_k_heads, d.num_v_heads,
+                                   d.head_k_dim, d.head_v_dim, L->conv, L->conv_pos, st));
     return GDN_OK;
 }
 
@@ -636,7 +643,7 @@ int gdn_delta_rule(gdn_layer* L, const float* qn, const float* kn, const float* 
     gdn::DeltaArgs r{};
     r.q = qn, r.k = kn, r.v = v, r.g = g, r.beta = beta;
     r.B = B, r.T = T, r.Hk = d.num_k_heads, r.Hv = d.num_v_heads, r.slot_ids = slot_ids;
-    r.state = L->rec, r.o = o, r.normalize = 0, r.scale = 1.f;
+    r.max_slots = L->max_slots, r.state = L->rec, r.o = o, r.normalize = 0, r.scale = 1.f;
     HIP_OK(run_delta(L, r, as_stream(stream)));
     return GDN_OK;
 }
@@ -682,7 +689,7 @@ int gdn_delta_rule_fla_ws(const float* q, const float* k, const float* v, const 
         return fail(GDN_ERR_SHAPE, "workspace of %zu bytes, this launch needs %zu", workspace_bytes, need);
     gdn::DeltaArgs r{};
     r.q = q, r.k = k, r.v = v, r.g = g, r.beta = beta;
-    r.B = B, r.T = T, r.Hk = Hk, r.Hv = Hv, r.slot_ids = nullptr;
+    r.B = B, r.T = T, r.Hk = Hk, r.Hv = Hv, r.slot_ids = nullptr, r.max_slots = B;
     r.state = state, r.o = o, r.normalize = use_qk_l2norm ? 1 : 0;
     r.scale = scale > 0.f ? scale : 1.f / std::sqrt((float)dk);
     if (workspace && need > 0)
@@ -772,6 +779,10 @@ int gdn_stack_create_ex(const gdn_dims* dims, const gdn_weights* weights, int n_
     if (!out) return fail(GDN_ERR_INVALID_ARG, "out is NULL");
     *out = nullptr;
     if (!weights || n_layers <= 0) return fail(GDN_ERR_INVALID_ARG, "gdn_stack_create: %d layers", n_layers);
+    int rc0 = check_dims(dims);
+    if (rc0) return rc0;
+    if (inter_norm && dims->hidden > 8192)
+        return fail(GDN_ERR_UNSUPPORTED, "inter-layer RMSNorm over hidden %d (at most 8192)", dims->hidden);
     gdn_stack* S = new gdn_stack();
     for (int i = 0; i < n_layers; ++i) {
         gdn_layer* L = nullptr;
@@ -822,11 +833,40 @@ int gdn_stack_forward(gdn_stack* S, const void* x, int B, int T, const int* slot
     if (!S || !x || !out) return fail(GDN_ERR_INVALID_ARG, "gdn_stack_forward: NULL argument");
     const int n = (int)S->layers.size();
     if (first < 0 || count <= 0 || first + count > n) return fail(GDN_ERR_INVALID_ARG, "layers [%d, %d) of %d", first, first + count, n);
-    if (B <= 0 || T <= 0 || (size_t)B * T > (size_t)S->max_tokens)
-        return fail(GDN_ERR_SHAPE, "gdn_stack_forward: B=%d T=%d (max_tokens %d)", B, T, S->max_tokens);
+    if (B <= 0 || T <= 0) return fail(GDN_ERR_SHAPE, "gdn_stack_forward: B=%d T=%d must be > 0", B, T);
+    if (B > S->max_tokens) return fail(GDN_ERR_SHAPE, "B=%d exceeds max_tokens=%d", B, S->max_tokens);
     if (!slot_ids && B > S->layers[0]->max_slots) return fail(GDN_ERR_SLOT, "B=%d exceeds max_slots", B);
-    const Group g{0, B, T, slot_ids ? slot_ids : S->layers[0]->iota};
-    return stack_run(S, (const u16*)x, B * T, &g, 1, first, count, (u16*)out, as_stream(stream));
+    const int* slots = slot_ids ? slot_ids : S->layers[0]->iota;
+    const hipStream_t st = as_stream(stream);
+    const u16* xin = (const u16*)x;
+    u16* xout = (u16*)out;
+    const int tc_max = S->max_tokens / B;
+    if (T <= tc_max) {
+        const Group g{0, B, T, slots};
+        return stack_run(S, xin, B * T, &g, 1, first, count, xout, st);
+    }
+    // Longer launches run token blocks of at most max_tokens rows through all the layers in turn: every layer
+    // is causal and carries its states, so block by block equals the whole launch (9B/gdn_layer.py:282-292
+    // splits one layer the same way).  Rows of several sequences are gathered into the workspace of layer 0
+    // (not used by the layers' own launches) and scattered back.
+    gdn_layer* L0 = S->layers[0];
+    const size_t rb = (size_t)S->H * sizeof(u16);
+    for (int t0 = 0; t0 < T; t0 += tc_max) {
+        const int tc = T - t0 < tc_max ? T - t0 : tc_max;
+        const Group g{0, B, tc, slots};
+        if (B == 1) {
+            int rc = stack_run(S, xin + (size_t)t0 * S->H, tc, &g, 1, first, count, xout + (size_t)t0 * S->H, st);
+            if (rc) return rc;
+            continue;
+        }
+        HIP_OK(hipMemcpy2DAsync(L0->x_ws, tc * rb, xin + (size_t)t0 * S->H, (size_t)T * rb, tc * rb, B,
+                                hipMemcpyDeviceToDevice, st));
+        int rc = stack_run(S, L0->x_ws, B * tc, &g, 1, first, count, L0->out_ws, st);
+        if (rc) return rc;
+        HIP_OK(hipMemcpy2DAsync(xout + (size_t)t0 * S->H, (size_t)T * rb, L0->out_ws, tc * rb, tc * rb, B,
+                                hipMemcpyDeviceToDevice, st));
+    }
+    return GDN_OK;
 }
 
 int gdn_stack_forward_varlen(gdn_stack* S, const void* x, int n_seqs, const int* cu_seqlens, const int* slot_ids,

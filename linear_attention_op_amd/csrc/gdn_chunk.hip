@@ -110,6 +110,7 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
     const size_t row0 = (size_t)b * T + t0;
     const int m = lane & 15, grp = lane >> 4;
     const size_t hc = ((size_t)b * Hv + h) * ws.NC + c;
+    if (a.slot_ids && (unsigned)a.slot_ids[b] >= (unsigned)a.max_slots) return;
 
     // ---- 0. inputs: thread (prow, pc4) owns tokens 4 prow + j (j < 4), channels pc4 .. pc4 + 3 of q, k, v
     const int prow = tid >> 5, pc4 = (tid & 31) * 4;
@@ -136,15 +137,18 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
         // The front end, from the projection rows: causal conv (4 taps over the inputs at t - 3 .. t, the
         // slot's history before t = 0) + SiLU, as conv_front_kernel (layer_compute.cpp C1, 74-103).  The
         // window of the thread's 4 tokens is 7 input rows, loaded one tensor at a time (register budget).
-        const int Kd = f.nk * DK, Vd = f.nv * DV, CD = 2 * Kd + Vd, CH = 2 * DK + DV;
+        const int R = Hv / Hk;
+        const int Kd = f.nk * DK, Vd = f.nv * DV, CD = 2 * Kd + Vd, CH = conv_group_width(DK, DV, R);
         const int slot = f.slot_ids ? f.slot_ids[b] : b;
-        const float* hq = f.conv_state + ((size_t)slot * f.nv + kh * (Hv / Hk)) * 3 * CH;  // q | k history copy
-        const float* hv = f.conv_state + ((size_t)slot * f.nv + h) * 3 * CH;
+        // the k-head group's history ring (q and k of kh, v of this head at 2 DK + (h % R) DV)
+        const float* hg = f.conv_state + ((size_t)slot * f.nk + kh) * CONV_RING * CH;
+        const int pos = f.conv_pos[(size_t)slot * f.nv + h];
         const int colq = kh * DK + pc4, colk = Kd + kh * DK + pc4, colv = 2 * Kd + h * DV + pc4;
         auto in_row = [&](int tk, int col, const float* hist, int local) -> float4 {
             const int tkc = min(tk, len - 1);  // rows past the end read a valid row, zeroed below
             const int t = t0 + tkc;
-            const float* p = t >= 0 ? f.P + (size_t)((long long)row0 + tkc) * f.NP + col : hist + (3 + t) * CH + local;
+            const float* p = t >= 0 ? f.P + (size_t)((long long)row0 + tkc) * f.NP + col
+                                    : hist + ring_index(pos, 3 + t) * CH + local;
             return keep_if(tk < len, *reinterpret_cast<const float4*>(p));
         };
         if (wave == 0 && lane < len) {
@@ -172,12 +176,12 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
         // one tensor at a time, the queries normalised and stored before the next window is loaded
         {
             float4 qr[4];
-            conv4(colq, hq, pc4, qr);
+            conv4(colq, hg, pc4, qr);
             l2store(qr, a.scale, sQ);
         }
-        conv4(colk, hq, DK + pc4, kr);
+        conv4(colk, hg, DK + pc4, kr);
         l2store(kr, 1.f, sK);
-        conv4(colv, hv, 2 * DK + pc4, vr);
+        conv4(colv, hg, 2 * DK + (h % R) * DV + pc4, vr);
     } else {
         float4 qr[4];
 #pragma unroll
@@ -571,6 +575,7 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
     const int h = blockIdx.x % Hv, cb = blockIdx.x / Hv, b = blockIdx.y;
     const int n0 = 16 * cb;
     const int slot = a.slot_ids ? a.slot_ids[b] : b;
+    if ((unsigned)slot >= (unsigned)a.max_slots) return;
     const int m = lane & 15, grp = lane >> 4;
     const int NC = (T + CK - 1) / CK;
     const int col = tid & 15, p = tid >> 4;  // Vn / output elements of this thread: tokens 2p, 2p + 1
@@ -765,8 +770,8 @@ hipError_t launch_delta_chunked(const DeltaArgs& a, int dk, int dv, void* worksp
     return hipGetLastError();
 }
 
-hipError_t launch_front_chunked(const FrontArgs& f, float* conv_state, const DeltaArgs& r, void* workspace,
-                                size_t ws_bytes, hipStream_t stream) {
+hipError_t launch_front_chunked(const FrontArgs& f, float* conv_state, int* conv_pos, const DeltaArgs& r,
+                                void* workspace, size_t ws_bytes, hipStream_t stream) {
     if (!delta_chunked_supported(f.dk, f.dv) || f.B != r.B || f.T != r.T) return hipErrorInvalidValue;
     if (r.B <= 0 || r.T <= 0) return hipSuccess;
     if (!workspace || ws_bytes < delta_chunked_workspace(r.B, r.T, r.Hv, f.dk, f.dv)) return hipErrorInvalidValue;
@@ -779,7 +784,8 @@ hipError_t launch_front_chunked(const FrontArgs& f, float* conv_state, const Del
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     // the prep pass has read the old history: roll it forward now
-    e = launch_conv_commit(f.P, f.NP, f.B, f.T, f.slot_ids, f.nk, f.nv, f.dk, f.dv, conv_state, stream);
+    e = launch_conv_commit(f.P, f.NP, f.B, f.T, f.slot_ids, f.max_slots, f.nk, f.nv, f.dk, f.dv, conv_state,
+                           conv_pos, stream);
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((chunk_state_kernel<128, 128>), dim3(a.Hv * (128 / 16), a.B), dim3(512), 0, stream, a, ws);
     return hipGetLastError();

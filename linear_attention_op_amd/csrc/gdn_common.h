@@ -177,6 +177,8 @@ hipError_t launch_linear_rows_t(const void* x, const void* w, int M, int N, int 
 hipError_t launch_in_proj_decode(const void* x, int xlayout, const void* w, int wlayout, const float* w_scale,
                                  const void* w2, int M, int N1, int N2, int K, float* P, int ldp, float* Pab,
                                  int ab_splits, hipStream_t stream);
+// Whether launch_in_proj_decode takes N1 rows of K columns (its workgroups tile the rows evenly).
+bool in_proj_decode_supported(int N1, int K);
 // Elements of an [N, K] matrix in W_FRAG layout (rows padded to a multiple of 16); also the bytes of the
 // same matrix in W_F8 layout.
 size_t frag_elems(int N, int K);
@@ -213,11 +215,31 @@ __host__ __device__ __forceinline__ size_t frag_offset(int n, int k, int K) {
     return ((size_t)(n >> 4) * (K >> 5) + (k >> 5)) * 512 + ((((k >> 3) & 3) << 4) + (n & 15)) * 8 + (k & 7);
 }
 
+// Conv history ring of a state slot, one per k-head group (k-head kh with its R = nv / nk v-heads):
+// [4][2 dk + R dv] fp32 entries of the pre-conv inputs of the group's channels -- q and k of kh, then v of the
+// v-heads R kh .. R kh + R - 1.  The input of absolute token time tau sits at entry tau % 4; pos = (tokens seen)
+// % 4 is kept per (slot, v-head) in conv_pos [slots, nv] (every v-head's copy of a slot is equal).  The
+// window of the next token, time order j = 0 (oldest) .. 2 (newest), is entry (pos + 1 + j) % 4, and the
+// launch's input t (0-based) goes to entry (pos + t) % 4; a launch writes only its last min(T, 3) inputs,
+// one entry per token, and entries that stay in the window do not move (the roll of layer_reader.cpp:184-197
+// without the copy).  With four entries a single-token launch writes the one entry no window reads, so the
+// v-heads of a group may run in separate workgroups that all read the group's q and k history while one of
+// them writes it; every workgroup advances only its own v-head's position.
+constexpr int CONV_RING = 4;
+__host__ __device__ __forceinline__ int conv_group_width(int dk, int dv, int R) { return 2 * dk + R * dv; }
+__host__ __device__ __forceinline__ int ring_index(int pos, int j) { return (pos + 1 + j) & 3; }
+__host__ __device__ __forceinline__ int ring_put(int pos, int t) { return (pos + t) & 3; }
+// Column in the fused projection row (q | k | v | z | a | b) of channel c of group kh (Kd = nk dk).
+__host__ __device__ __forceinline__ int group_col(int c, int kh, int dk, int dv, int R, int Kd) {
+    return c < dk ? kh * dk + c : (c < 2 * dk ? Kd + kh * dk + (c - dk) : 2 * Kd + kh * R * dv + (c - 2 * dk));
+}
+
 struct MixerArgs {
     const float* P;         // [M, NP] fused projection rows (q | k | v | z | a | b)
     int NP;                 // row stride of P
     int B, T;               // launch = B sequences x T tokens, rows m = b * T + t
     const int* slot_ids;    // [B] device, or nullptr for identity
+    int max_slots;          // slots of the state buffers; a sequence whose slot id is outside is skipped
     int nk, nv;             // heads
     const float4* conv_w;   // [conv_dim] taps (w0, w1, w2, w3) per channel
     const float* neg_A;     // [nv]  -exp(A_log)
@@ -225,7 +247,8 @@ struct MixerArgs {
     const float* norm_w;    // [dv]
     float eps;              // RMSNorm eps
     float* rec_state;       // [slots, nv, dk, dv]
-    float* conv_state;      // [slots, nv, 3, 2dk + dv] time-ordered history, per v-head copy
+    float* conv_state;      // [slots, nk, 4, 2 dk + R dv] conv history rings
+    int* conv_pos;          // [slots, nv] ring positions
     u16* y;                 // [M, nv * dv] bf16 gated RMSNorm output
     int y_frag;             // 1: y in W_FRAG layout (rows padded to 16; M <= 64), 0: row-major
     float* o_tap;           // optional [M, nv * dv] recurrence output (nullptr: not written)
@@ -235,6 +258,8 @@ struct MixerArgs {
     int ab_splits;
     size_t ab_stride;
 };
+// Fused mixer of a decode-sized launch: single-token launches one workgroup of 256 threads per (sequence,
+// v-head); longer ones one workgroup of 256 R threads per (sequence, k-head group), R = nv / nk <= 4.
 hipError_t launch_mixer(const MixerArgs& a, int dk, int dv, hipStream_t stream);
 
 struct FrontArgs {
@@ -242,11 +267,13 @@ struct FrontArgs {
     int NP;
     int B, T;
     const int* slot_ids;
+    int max_slots;            // sequences with a slot id outside [0, max_slots) are skipped
     int nk, nv, dk, dv;
     const float4* conv_w;
     const float* neg_A;
     const float* dt_bias;
-    const float* conv_state;  // history (read only here)
+    const float* conv_state;  // history rings (read only here)
+    const int* conv_pos;      // ring positions
     float* qn;                // [M, nk, dk]  l2norm(q) * dk^-0.5
     float* kn;                // [M, nk, dk]  l2norm(k)
     float* v;                 // [M, nv, dv]
@@ -254,9 +281,9 @@ struct FrontArgs {
     float* beta;              // [M, nv]
 };
 hipError_t launch_conv_front(const FrontArgs& a, hipStream_t stream);
-// Roll each sequence's conv history forward over the T inputs of this launch.
-hipError_t launch_conv_commit(const float* P, int NP, int B, int T, const int* slot_ids, int nk, int nv, int dk,
-                              int dv, float* conv_state, hipStream_t stream);
+// Roll each sequence's conv history rings forward over the T inputs of this launch.
+hipError_t launch_conv_commit(const float* P, int NP, int B, int T, const int* slot_ids, int max_slots, int nk,
+                              int nv, int dk, int dv, float* conv_state, int* conv_pos, hipStream_t stream);
 
 // Recurrence over T tokens for B sequences from pre-normalised q/k (qn already scaled).
 struct DeltaArgs {
@@ -267,6 +294,7 @@ struct DeltaArgs {
     const float* beta;     // [B*T, Hv]
     int B, T, Hk, Hv;
     const int* slot_ids;   // state slot of sequence b (nullptr: b)
+    int max_slots;         // slots of `state`; a sequence whose slot id is outside [0, max_slots) is skipped
     float* state;          // [slots, Hv, dk, dv]
     float* o;              // [B*T, Hv, dv]
     int normalize;         // 1: apply l2norm to q/k in the kernel
@@ -280,8 +308,8 @@ size_t delta_chunked_workspace(int B, int T, int Hv, int dk, int dv);
 // The same with the front end fused into the chunk preparation: q, k, v, g, beta of each chunk are computed
 // from the projection rows f.P (conv history f.conv_state, then rolled forward in conv_state), so f.qn ..
 // f.beta and r.q .. r.beta are not used; r carries B, T, heads, slots, the state and o.
-hipError_t launch_front_chunked(const FrontArgs& f, float* conv_state, const DeltaArgs& r, void* workspace,
-                                size_t ws_bytes, hipStream_t stream);
+hipError_t launch_front_chunked(const FrontArgs& f, float* conv_state, int* conv_pos, const DeltaArgs& r,
+                                void* workspace, size_t ws_bytes, hipStream_t stream);
 bool delta_chunked_supported(int dk, int dv);
 
 // y = o * rsqrt(mean(o^2) + eps) * w * silu(z), per head of dv; y bf16.
@@ -291,12 +319,16 @@ hipError_t launch_rmsnorm_rows(const u16* x, int M, int H, const float* w, float
 hipError_t launch_gated_rmsnorm(const float* o, int M, int nv, int dv, const float* z, int z_stride,
                                 const float* w, float eps, u16* y, hipStream_t stream);
 
-// State import / export (time-ordered conv history [n, conv_dim, 3]).
-hipError_t launch_state_export(const float* rec_state, const float* conv_state, const int* slots, int n, int nk,
-                               int nv, int dk, int dv, float* rec_out, float* conv_out, hipStream_t stream);
-hipError_t launch_state_import(float* rec_state, float* conv_state, const int* slots, int n, int nk, int nv, int dk,
-                               int dv, const float* rec_in, const float* conv_in, hipStream_t stream);
-hipError_t launch_state_zero(float* rec_state, float* conv_state, const int* slots, int n, int nv, int dk, int dv,
-                             int ch, hipStream_t stream);
+// State import / export / zero of n slots (ids outside [0, max_slots) are skipped): recurrent state
+// [n, nv, dk, dv]; conv history in the reference's time order [n, conv_dim, 3] (entry 2 newest), translated
+// from and to the rings (import and zero set the ring positions to 0).
+hipError_t launch_state_export(const float* rec_state, const float* conv_state, const int* conv_pos, const int* slots,
+                               int n, int max_slots, int nk, int nv, int dk, int dv, float* rec_out, float* conv_out,
+                               hipStream_t stream);
+hipError_t launch_state_import(float* rec_state, float* conv_state, int* conv_pos, const int* slots, int n,
+                               int max_slots, int nk, int nv, int dk, int dv, const float* rec_in,
+                               const float* conv_in, hipStream_t stream);
+hipError_t launch_state_zero(float* rec_state, float* conv_state, int* conv_pos, const int* slots, int n,
+                             int max_slots, int nk, int nv, int dk, int dv, hipStream_t stream);
 
 }  // namespace gdn

@@ -16,6 +16,7 @@ __global__ __launch_bounds__(256) void delta_seq_kernel(DeltaArgs a) {
     const int h = blockIdx.x, b = blockIdx.y;
     const int Hk = a.Hk, Hv = a.Hv, kh = h / (Hv / Hk);
     const int slot = a.slot_ids ? a.slot_ids[b] : b;
+    if ((unsigned)slot >= (unsigned)a.max_slots) return;
     const int T = a.T;
 
     __shared__ float sq[DK], sk[DK], sv[DV];

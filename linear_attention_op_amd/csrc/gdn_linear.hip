@@ -1026,11 +1026,13 @@ void in_proj_decode_launch(const DecodeArgs& a, hipStream_t stream) {
                        a.w2, a.M, a.N1, a.N2, a.K, a.G, a.KS, a.P, a.ldp, a.Pab);
 }
 
+// Row tiles per workgroup of the decode in_proj: the smallest that keeps the main workgroups within one per CU.
+int in_proj_decode_tiles(int NT1) { return NT1 <= 256 ? 1 : (NT1 <= 512 ? 2 : (NT1 <= 768 ? 3 : 4)); }
+
 template <int MT, int WL, int XL = W_FRAG>
 hipError_t in_proj_decode_mt(DecodeArgs a, hipStream_t stream) {
     const int NT1 = a.N1 >> 4;
-    // tiles per workgroup: the smallest that keeps the main workgroups within one per CU
-    const int nts = NT1 <= 256 ? 1 : (NT1 <= 512 ? 2 : (NT1 <= 768 ? 3 : 4));
+    const int nts = in_proj_decode_tiles(NT1);
     if (NT1 % nts) return hipErrorInvalidValue;
     a.G = NT1 / nts;
     switch (nts) {
@@ -1052,6 +1054,10 @@ hipError_t in_proj_decode_wl(const DecodeArgs& a, int xlayout, hipStream_t strea
 }
 
 }  // namespace
+
+bool in_proj_decode_supported(int N1, int K) {
+    return N1 > 0 && N1 % 16 == 0 && K % 128 == 0 && (N1 >> 4) % in_proj_decode_tiles(N1 >> 4) == 0;
+}
 
 hipError_t launch_in_proj_decode(const void* x, int xlayout, const void* w, int wlayout, const float* w_scale,
                                  const void* w2, int M, int N1, int N2, int K, float* P, int ldp, float* Pab,

@@ -1,21 +1,24 @@
 // The Gated DeltaNet mixer between the two projections.
 //
-// mixer_kernel: one workgroup per (sequence, v-head) runs, for each token of the launch, the whole
-// middle of the layer -- causal conv1d (4 taps) + SiLU on the head's 2*dk + dv channels, q/k L2 norm,
-// the gating scalars, the delta-rule update of the fp32 dk x dv state and the gated RMSNorm -- with the
-// state held in VGPRs from the first token to the last.  The state is read from HBM once and written
-// once per launch; nothing else of size dk*dv moves.  This is the decode path (and short prefills).
-// It restates, per token, wormhole_n150/qwen3.5_9B/kernels/layer_compute.cpp C1-C6 (74-395) with
+// mixer_kernel: one workgroup per (sequence, k-head group) -- k-head kh and its R = nv / nk v-heads, 256
+// threads per v-head -- runs, for each token of the launch, the whole middle of the layer: causal conv1d
+// (4 taps) + SiLU on the group's 2 dk + R dv channels (q and k once for the group), q/k L2 norm, the gating
+// scalars, the delta-rule update of each v-head's fp32 dk x dv state and the gated RMSNorm, with the states
+// held in VGPRs from the first token to the last.  A state is read from HBM once and written once per
+// launch; nothing else of size dk*dv moves.  This is the decode path (and short prefills).  It restates,
+// per token, wormhole_n150/qwen3.5_9B/kernels/layer_compute.cpp C1-C6 (74-395) with
 // layer_reader.cpp:103-124,184-197 for the conv history; HF:432-543 for the layer math.
 //
 // Load order matters: vector-memory loads complete in order, so every load the first token's conv,
-// norms and gating need (history, taps, the projection row, z) is issued before the 64 KB state; that
-// front-end work then runs while the state is still arriving.
+// norms and gating need (history, taps, the projection row, z) is issued before the 64 KB states; that
+// front-end work then runs while the states are still arriving.
 //
-// conv history: each (slot, v-head) keeps its 2*dk + dv pre-conv channels for the last 3 tokens in time
-// order, [3][2*dk + dv], entry 0 oldest (the q/k channels of its k-head are kept per v-head, so no two
-// workgroups share a history).  After a launch of T tokens entry j holds the input at time T - 3 + j:
-// the reference's roll (layer_reader.cpp:184-197).
+// The conv history is the k-head group's 4-entry ring (see conv_group_width in gdn_common.h): a workgroup
+// reads the three window entries, slides them through registers over the tokens and writes back only the
+// inputs of the last min(T, 3) tokens and its v-heads' new ring positions.  Single-token launches run one
+// workgroup per v-head (twice the workgroups of a group, so two fit a CU beside each other); the group's q
+// and k channels are then read by all R of its workgroups and written by the first, into the ring entry no
+// window reads.  Longer launches run one workgroup per group, which owns the whole ring.
 //
 // conv_front_kernel / conv_commit_kernel / gated_rmsnorm_kernel: the same front end and norm split into
 // token-parallel kernels for long prefills, where the recurrence runs in the chunked form.
@@ -24,43 +27,50 @@
 
 namespace gdn {
 
-// Map of a head-local conv channel c (q: [0, dk), k: [dk, 2dk), v: [2dk, 2dk + dv)) to its column in
-// the fused projection row (q | k | v | z | a | b).
-__device__ __forceinline__ int conv_col(int c, int kh, int h, int dk, int dv, int Kd) {
-    return c < dk ? kh * dk + c : (c < 2 * dk ? Kd + kh * dk + (c - dk) : 2 * Kd + h * dv + (c - 2 * dk));
-}
-
-template <int DK, int DV>
-__global__ __launch_bounds__(256) void mixer_kernel(MixerArgs a) {
-    constexpr int CH = 2 * DK + DV;
-    constexpr int CPT = (CH + 255) / 256;
+// PER_HEAD: one workgroup of 256 threads per (v-head, sequence), single-token launches only; else one of
+// 256 R threads per (k-head group, sequence).
+template <int DK, int DV, int R, bool PER_HEAD>
+__global__ __launch_bounds__(PER_HEAD ? 256 : 256 * R) void mixer_kernel(MixerArgs a) {
+    constexpr int HW = PER_HEAD ? 1 : R;     // v-heads of the workgroup
+    constexpr int NTH = 256 * HW;
+    constexpr int CHG = 2 * DK + R * DV;     // channels of the group (a ring entry)
+    constexpr int CHW = 2 * DK + HW * DV;    // channels of the workgroup
+    constexpr int CPT = (CHW + NTH - 1) / NTH;
     using Tile = DeltaTile<DK, DV>;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int h = blockIdx.x, b = blockIdx.y;
-    const int nv = a.nv, kh = h / (nv / a.nk);
-    const int Kd = a.nk * DK, Vd = nv * DV, CD = 2 * Kd + Vd;
+    const int sub = PER_HEAD ? 0 : tid >> 8, stid = tid & 255, swave = wave & 3;  // v-head of the workgroup
+    const int h = PER_HEAD ? blockIdx.x : blockIdx.x * R + sub, b = blockIdx.y;
+    const int kh = PER_HEAD ? blockIdx.x / R : blockIdx.x;
+    const int h0 = PER_HEAD ? h : kh * R;    // first v-head of the workgroup
+    const int nv = a.nv, nk = a.nk;
+    const int Kd = nk * DK, Vd = nv * DV, CD = 2 * Kd + Vd;
     const int slot = a.slot_ids ? a.slot_ids[b] : b;
+    if ((unsigned)slot >= (unsigned)a.max_slots) return;
     const int T = a.T;
 
-    __shared__ float sq[DK], sk[DK], sv[DV];
-    __shared__ float red[4][2][DV];
+    __shared__ float sq[DK], sk[DK], sv[HW][DV];
+    __shared__ float red[HW][4][2][DV];
 
     // ---- state-independent loads first: history, taps, the first token's projection values --------
-    float* hist = a.conv_state + ((size_t)slot * nv + h) * 3 * CH;
+    float* hist = a.conv_state + ((size_t)slot * nk + kh) * CONV_RING * CHG;
+    int* posp = a.conv_pos + (size_t)slot * nv + h0;
+    const int pos = *posp;
     float hx[CPT][3], xin[CPT];
     float4 tap[CPT];
-    int pcol[CPT];
+    int pcol[CPT], gch[CPT];
     const float* Prow = a.P + (size_t)b * T * a.NP;
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
-        const int ch = tid + 256 * c;
-        pcol[c] = 0;
-        if (ch < CH) {
-            pcol[c] = conv_col(ch, kh, h, DK, DV, Kd);
+        const int ch = tid + NTH * c;
+        pcol[c] = gch[c] = 0;
+        if (ch < CHW) {
+            // channel of the group: q | k of kh, then the v channels of this workgroup's v-heads
+            gch[c] = ch < 2 * DK ? ch : 2 * DK + (h0 - kh * R) * DV + (ch - 2 * DK);
+            pcol[c] = group_col(gch[c], kh, DK, DV, R, Kd);
             tap[c] = a.conv_w[pcol[c]];
 #pragma unroll
-            for (int j = 0; j < 3; ++j) hx[c][j] = hist[j * CH + ch];
+            for (int j = 0; j < 3; ++j) hx[c][j] = hist[ring_index(pos, j) * CHG + gch[c]];
             xin[c] = Prow[pcol[c]];
         }
     }
@@ -82,16 +92,16 @@ __global__ __launch_bounds__(256) void mixer_kernel(MixerArgs a) {
     float av, bv;
     load_ab((size_t)b * T, av, bv);
     float4 zv = make_float4(0.f, 0.f, 0.f, 0.f), nw = zv;
-    if (tid < Tile::CG) {
-        zv = *reinterpret_cast<const float4*>(Prow + CD + h * DV + 4 * tid);
-        nw = *reinterpret_cast<const float4*>(a.norm_w + 4 * tid);
+    if (stid < Tile::CG) {
+        zv = *reinterpret_cast<const float4*>(Prow + CD + h * DV + 4 * stid);
+        nw = *reinterpret_cast<const float4*>(a.norm_w + 4 * stid);
     }
     const float negA = a.neg_A[h], dtb = a.dt_bias[h];
 
-    // ---- then the state ----------------------------------------------------------------------------
+    // ---- then the states ---------------------------------------------------------------------------
     float* S = a.rec_state + ((size_t)slot * nv + h) * DK * DV;
     Tile st;
-    st.init(tid);
+    st.init(stid);
     st.load(S);
     const float qscale = rsqrtf((float)DK);
 
@@ -99,8 +109,8 @@ __global__ __launch_bounds__(256) void mixer_kernel(MixerArgs a) {
         const size_t m = (size_t)b * T + t;
 #pragma unroll
         for (int c = 0; c < CPT; ++c) {
-            const int ch = tid + 256 * c;
-            if (ch < CH) {
+            const int ch = tid + NTH * c;
+            if (ch < CHW) {
                 const float acc = tap[c].x * hx[c][0] + tap[c].y * hx[c][1] + tap[c].z * hx[c][2] + tap[c].w * xin[c];
                 hx[c][0] = hx[c][1];
                 hx[c][1] = hx[c][2];
@@ -111,7 +121,7 @@ __global__ __launch_bounds__(256) void mixer_kernel(MixerArgs a) {
                 else if (ch < 2 * DK)
                     sk[ch - DK] = out;
                 else
-                    sv[ch - 2 * DK] = out;
+                    (&sv[0][0])[ch - 2 * DK] = out;
             }
         }
         // next token's projection values (issued now, consumed one token later)
@@ -121,9 +131,9 @@ __global__ __launch_bounds__(256) void mixer_kernel(MixerArgs a) {
             const float* Pn = Prow + (size_t)(t + 1) * a.NP;
 #pragma unroll
             for (int c = 0; c < CPT; ++c)
-                if (tid + 256 * c < CH) xin[c] = Pn[pcol[c]];
+                if (tid + NTH * c < CHW) xin[c] = Pn[pcol[c]];
             load_ab(m + 1, av_n, bv_n);
-            if (tid < Tile::CG) zv_n = *reinterpret_cast<const float4*>(Pn + CD + h * DV + 4 * tid);
+            if (stid < Tile::CG) zv_n = *reinterpret_cast<const float4*>(Pn + CD + h * DV + 4 * stid);
         }
         __syncthreads();
 
@@ -139,10 +149,10 @@ __global__ __launch_bounds__(256) void mixer_kernel(MixerArgs a) {
         const float rk = rsqrtf(pkk + 1e-6f);
         const float d = __expf(negA * softplusf_(av + dtb));
         const float beta = sigmoidf_(bv);
-        const float4 o = st.step(sq, sk, sv, red, rq, rk, pqk * rq * rk, d, beta, lane, wave);
+        const float4 o = st.step(sq, sk, sv[sub], red[sub], rq, rk, pqk * rq * rk, d, beta, lane, swave);
 
-        // gated RMSNorm of this head's o on wave 0 (its lanes < CG hold all dv columns)
-        if (wave == 0) {
+        // gated RMSNorm of this head's o on the first wave of its part (lanes < CG hold all dv columns)
+        if (swave == 0) {
             float ss = lane < Tile::CG ? o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w : 0.f;
             ss = warp_sum(ss);
             if (lane < Tile::CG) {
@@ -164,26 +174,50 @@ __global__ __launch_bounds__(256) void mixer_kernel(MixerArgs a) {
     }
 
     st.store(S);
+    // the ring: the window's entry j (the input at launch time T - 3 + j) goes to entry (pos + T - 3 + j) % 4
+    // when it is an input of this launch; older ones are already in place.  Per head, the group's q and k
+    // channels are written by its first v-head's workgroup only.
+    const bool own_qk = !PER_HEAD || h % R == 0;
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
-        const int ch = tid + 256 * c;
-        if (ch < CH)
+        const int ch = tid + NTH * c;
+        if (ch < CHW && (own_qk || ch >= 2 * DK))
 #pragma unroll
-            for (int j = 0; j < 3; ++j) hist[j * CH + ch] = hx[c][j];
+            for (int j = 0; j < 3; ++j)
+                if (T - 3 + j >= 0) hist[ring_put(pos, T - 3 + j) * CHG + gch[c]] = hx[c][j];
     }
+    // every thread read the old position before the step's barriers
+    if (tid < HW) posp[tid] = (pos + T) & 3;
+}
+
+template <int DK, int DV, bool PER_HEAD>
+hipError_t launch_mixer_r(const MixerArgs& a, hipStream_t stream) {
+    const int R = a.nv / a.nk;
+    const dim3 grid(PER_HEAD ? a.nv : a.nk, a.B);
+    const dim3 block(PER_HEAD ? 256 : 256 * R);
+    switch (R) {
+        case 1: hipLaunchKernelGGL((mixer_kernel<DK, DV, 1, PER_HEAD>), grid, block, 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((mixer_kernel<DK, DV, 2, PER_HEAD>), grid, block, 0, stream, a); break;
+        case 3: hipLaunchKernelGGL((mixer_kernel<DK, DV, 3, PER_HEAD>), grid, block, 0, stream, a); break;
+        case 4: hipLaunchKernelGGL((mixer_kernel<DK, DV, 4, PER_HEAD>), grid, block, 0, stream, a); break;
+        default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+}
+
+template <int DK, int DV>
+hipError_t launch_mixer_d(const MixerArgs& a, hipStream_t stream) {
+    // a group's v-heads share a ring: in separate workgroups only when the launch writes the one free entry
+    return a.T == 1 ? launch_mixer_r<DK, DV, true>(a, stream) : launch_mixer_r<DK, DV, false>(a, stream);
 }
 
 hipError_t launch_mixer(const MixerArgs& a, int dk, int dv, hipStream_t stream) {
-    const dim3 grid(a.nv, a.B);
-    if (dk == 128 && dv == 128)
-        hipLaunchKernelGGL((mixer_kernel<128, 128>), grid, dim3(256), 0, stream, a);
-    else if (dk == 64 && dv == 64)
-        hipLaunchKernelGGL((mixer_kernel<64, 64>), grid, dim3(256), 0, stream, a);
-    else if (dk == 32 && dv == 32)
-        hipLaunchKernelGGL((mixer_kernel<32, 32>), grid, dim3(256), 0, stream, a);
-    else
-        return hipErrorInvalidValue;
-    return hipGetLastError();
+    if (a.B <= 0 || a.T <= 0) return hipSuccess;
+    if (a.nk <= 0 || a.nv % a.nk) return hipErrorInvalidValue;
+    if (dk == 128 && dv == 128) return launch_mixer_d<128, 128>(a, stream);
+    if (dk == 64 && dv == 64) return launch_mixer_d<64, 64>(a, stream);
+    if (dk == 32 && dv == 32) return launch_mixer_d<32, 32>(a, stream);
+    return hipErrorInvalidValue;
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -201,9 +235,10 @@ __global__ __launch_bounds__(256) void conv_front_kernel(FrontArgs a) {
     const int T = a.T, b = blockIdx.z, y = blockIdx.y;
     const int t0 = blockIdx.x * FTB, tn = min(FTB, T - t0);
     const int slot = a.slot_ids ? a.slot_ids[b] : b;
+    if ((unsigned)slot >= (unsigned)a.max_slots) return;
     const int nk = a.nk, nv = a.nv, dk = a.dk, dv = a.dv;
     const int ratio = nv / nk;
-    const int Kd = nk * dk, Vd = nv * dv, CD = 2 * Kd + Vd, CH = 2 * dk + dv;
+    const int Kd = nk * dk, Vd = nv * dv, CD = 2 * Kd + Vd, CH = conv_group_width(dk, dv, ratio);
     const size_t row0 = (size_t)b * T + t0;
     const int nvb = (Vd + 255) / 256;
 
@@ -217,21 +252,21 @@ __global__ __launch_bounds__(256) void conv_front_kernel(FrontArgs a) {
         return;
     }
 
-    // this thread's channel: projection column, and where its history lives
+    // this thread's channel: projection column, and where its history lives (group, channel of the group)
     const bool isqk = y < nk;
     bool active;
-    int col = 0, hcopy = 0, local = 0, vc = 0;
+    int col = 0, grp = 0, local = 0, vc = 0;
     if (isqk) {
         const int kh = y, c = tid;  // c < dk: q channel c; dk <= c < 2 dk: k channel c - dk
         active = c < 2 * dk;
         col = c < dk ? kh * dk + c : Kd + kh * dk + (c - dk);
-        hcopy = kh * ratio, local = c;
+        grp = kh, local = c;
     } else {
         vc = (y - nk) * 256 + tid;
         active = vc < Vd;
-        const int hh = vc / dv;
+        const int hh = min(vc, Vd - 1) / dv;
         col = 2 * Kd + vc;
-        hcopy = hh, local = 2 * dk + (vc - hh * dv);
+        grp = hh / ratio, local = 2 * dk + (hh % ratio) * dv + (vc - hh * dv);
     }
     float out[FTB];
 #pragma unroll
@@ -239,12 +274,13 @@ __global__ __launch_bounds__(256) void conv_front_kernel(FrontArgs a) {
     if (active) {
         const float4 w = a.conv_w[col];
         // window: inputs at t0 - 3, t0 - 2, t0 - 1 (history entries for times before 0)
-        const float* hist = a.conv_state + ((size_t)slot * nv + hcopy) * 3 * CH;
+        const float* hist = a.conv_state + ((size_t)slot * nk + grp) * CONV_RING * CH;
+        const int pos = a.conv_pos[(size_t)slot * nv + grp * ratio];
         float xs[3];
 #pragma unroll
         for (int s = 3; s >= 1; --s) {
             const int ts = t0 - s;
-            xs[3 - s] = ts >= 0 ? a.P[(row0 - s) * a.NP + col] : hist[(3 + ts) * CH + local];
+            xs[3 - s] = ts >= 0 ? a.P[(row0 - s) * a.NP + col] : hist[ring_index(pos, 3 + ts) * CH + local];
         }
         float x0 = xs[0], x1 = xs[1], x2 = xs[2];
 #pragma unroll
@@ -296,32 +332,37 @@ hipError_t launch_conv_front(const FrontArgs& a, hipStream_t stream) {
     return hipGetLastError();
 }
 
+// One workgroup per (sequence, k-head group): the inputs of the launch's last min(T, 3) tokens into the
+// group's ring, and the new ring positions of its v-heads (entries from before the launch that stay in the
+// window keep their place).
 __global__ __launch_bounds__(256) void conv_commit_kernel(const float* __restrict__ P, int NP, int T,
-                                                          const int* __restrict__ slot_ids, int nk, int nv, int dk,
-                                                          int dv, float* __restrict__ conv_state) {
-    // new entry j = input at time T - 3 + j: a projection row of this launch, or (T < 3) old entry T + j
-    const int h = blockIdx.x, b = blockIdx.y;
+                                                          const int* __restrict__ slot_ids, int max_slots, int nk,
+                                                          int nv, int dk, int dv, float* __restrict__ conv_state,
+                                                          int* __restrict__ conv_pos) {
+    const int kh = blockIdx.x, b = blockIdx.y;
     const int slot = slot_ids ? slot_ids[b] : b;
-    const int kh = h / (nv / nk), Kd = nk * dk, CH = 2 * dk + dv;
-    float* hist = conv_state + ((size_t)slot * nv + h) * 3 * CH;
+    if ((unsigned)slot >= (unsigned)max_slots) return;
+    const int R = nv / nk, Kd = nk * dk, CH = conv_group_width(dk, dv, R);
+    float* hist = conv_state + ((size_t)slot * nk + kh) * CONV_RING * CH;
+    int* posp = conv_pos + (size_t)slot * nv + kh * R;  // the positions of the group's v-heads
+    const int pos = *posp;
     for (int c = threadIdx.x; c < CH; c += 256) {
-        const int col = conv_col(c, kh, h, dk, dv, Kd);
-        const float old[3] = {hist[c], hist[CH + c], hist[2 * CH + c]};
-        float nw[3];
+        const int col = group_col(c, kh, dk, dv, R, Kd);
 #pragma unroll
         for (int j = 0; j < 3; ++j) {
             const int tj = T - 3 + j;
-            nw[j] = tj >= 0 ? P[((size_t)b * T + tj) * NP + col] : old[T + j];
+            if (tj >= 0) hist[ring_put(pos, tj) * CH + c] = P[((size_t)b * T + tj) * NP + col];
         }
-#pragma unroll
-        for (int j = 0; j < 3; ++j) hist[j * CH + c] = nw[j];
     }
+    __syncthreads();  // every thread has read the old position
+    if (threadIdx.x < R) posp[threadIdx.x] = (pos + T) & 3;
 }
 
-hipError_t launch_conv_commit(const float* P, int NP, int B, int T, const int* slot_ids, int nk, int nv, int dk,
-                              int dv, float* conv_state, hipStream_t stream) {
-    hipLaunchKernelGGL(conv_commit_kernel, dim3(nv, B), dim3(256), 0, stream, P, NP, T, slot_ids, nk, nv, dk, dv,
-                       conv_state);
+hipError_t launch_conv_commit(const float* P, int NP, int B, int T, const int* slot_ids, int max_slots, int nk,
+                              int nv, int dk, int dv, float* conv_state, int* conv_pos, hipStream_t stream) {
+    if (B <= 0 || T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(conv_commit_kernel, dim3(nk, B), dim3(256), 0, stream, P, NP, T, slot_ids, max_slots, nk, nv,
+                       dk, dv, conv_state, conv_pos);
     return hipGetLastError();
 }
 
@@ -442,85 +483,105 @@ hipError_t launch_rmsnorm_rows(const u16* x, int M, int H, const float* w, float
 }
 
 // ------------------------------------------------------------------------------------------------
-// State import / export / zero.  Export gives the conv history in time order [n, conv_dim, 3]
-// (q/k channels from the copy of the first v-head of each k-head group).
+// State import / export / zero.  The conv history crosses the boundary in the reference's layout and time
+// order, [n, conv_dim, 3] with entry 2 the newest (9B/gdn_layer.py:147-151 keeps it per channel): export
+// reads each group's ring from its position, import writes time order at ring position 0.
 // ------------------------------------------------------------------------------------------------
+// Group and channel of the group of HF conv channel `col` (q | k | v order).
+__device__ __forceinline__ void channel_group(int col, int nk, int dk, int dv, int R, int* grp, int* local) {
+    const int Kd = nk * dk;
+    if (col < Kd) {
+        *grp = col / dk, *local = col % dk;
+    } else if (col < 2 * Kd) {
+        *grp = (col - Kd) / dk, *local = dk + (col - Kd) % dk;
+    } else {
+        const int hh = (col - 2 * Kd) / dv;
+        *grp = hh / R, *local = 2 * dk + (hh % R) * dv + (col - 2 * Kd) % dv;
+    }
+}
+
 __global__ void state_export_kernel(const float* __restrict__ rec, const float* __restrict__ conv,
-                                    const int* __restrict__ slots, int nk, int nv, int dk, int dv,
-                                    float* __restrict__ rec_out, float* __restrict__ conv_out) {
+                                    const int* __restrict__ conv_pos, const int* __restrict__ slots, int max_slots,
+                                    int nk, int nv, int dk, int dv, float* __restrict__ rec_out,
+                                    float* __restrict__ conv_out) {
     const int i = blockIdx.y;
     const int slot = slots ? slots[i] : i;
+    if ((unsigned)slot >= (unsigned)max_slots) return;
     const size_t rec_n = (size_t)nv * dk * dv;
     if (rec_out)
         for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < rec_n; e += (size_t)gridDim.x * blockDim.x)
             rec_out[(size_t)i * rec_n + e] = rec[(size_t)slot * rec_n + e];
     if (!conv_out) return;
-    const int Kd = nk * dk, CD = 2 * Kd + nv * dv, CH = 2 * dk + dv, ratio = nv / nk;
+    const int R = nv / nk, CD = 2 * nk * dk + nv * dv, CH = conv_group_width(dk, dv, R);
     for (int col = blockIdx.x * blockDim.x + threadIdx.x; col < CD; col += gridDim.x * blockDim.x) {
-        int hcopy, local;
-        if (col < Kd) {
-            hcopy = (col / dk) * ratio, local = col % dk;
-        } else if (col < 2 * Kd) {
-            hcopy = ((col - Kd) / dk) * ratio, local = dk + (col - Kd) % dk;
-        } else {
-            hcopy = (col - 2 * Kd) / dv, local = 2 * dk + (col - 2 * Kd) % dv;
-        }
-        const float* hist = conv + ((size_t)slot * nv + hcopy) * 3 * CH;
-        for (int j = 0; j < 3; ++j) conv_out[((size_t)i * CD + col) * 3 + j] = hist[j * CH + local];
+        int grp, local;
+        channel_group(col, nk, dk, dv, R, &grp, &local);
+        const float* hist = conv + ((size_t)slot * nk + grp) * CONV_RING * CH;
+        const int pos = conv_pos[(size_t)slot * nv + grp * R];
+        for (int j = 0; j < 3; ++j) conv_out[((size_t)i * CD + col) * 3 + j] = hist[ring_index(pos, j) * CH + local];
     }
 }
 
-__global__ void state_import_kernel(float* __restrict__ rec, float* __restrict__ conv, const int* __restrict__ slots,
-                                    int nk, int nv, int dk, int dv, const float* __restrict__ rec_in,
-                                    const float* __restrict__ conv_in) {
+__global__ void state_import_kernel(float* __restrict__ rec, float* __restrict__ conv, int* __restrict__ conv_pos,
+                                    const int* __restrict__ slots, int max_slots, int nk, int nv, int dk, int dv,
+                                    const float* __restrict__ rec_in, const float* __restrict__ conv_in) {
     const int i = blockIdx.y;
     const int slot = slots ? slots[i] : i;
+    if ((unsigned)slot >= (unsigned)max_slots) return;
     const size_t rec_n = (size_t)nv * dk * dv;
     if (rec_in)
         for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < rec_n; e += (size_t)gridDim.x * blockDim.x)
             rec[(size_t)slot * rec_n + e] = rec_in[(size_t)i * rec_n + e];
-    const int Kd = nk * dk, CD = 2 * Kd + nv * dv, CH = 2 * dk + dv, ratio = nv / nk;
-    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < nv * CH; e += gridDim.x * blockDim.x) {
-        const int h = e / CH, c = e % CH;
-        const int col = conv_col(c, h / ratio, h, dk, dv, Kd);
-        float* hist = conv + ((size_t)slot * nv + h) * 3 * CH;
-        for (int j = 0; j < 3; ++j) hist[j * CH + c] = conv_in ? conv_in[((size_t)i * CD + col) * 3 + j] : 0.f;
+    const int R = nv / nk, CD = 2 * nk * dk + nv * dv, CH = conv_group_width(dk, dv, R);
+    for (int col = blockIdx.x * blockDim.x + threadIdx.x; col < CD; col += gridDim.x * blockDim.x) {
+        int grp, local;
+        channel_group(col, nk, dk, dv, R, &grp, &local);
+        float* hist = conv + ((size_t)slot * nk + grp) * CONV_RING * CH;
+        for (int j = 0; j < 3; ++j)  // time order j at position 0: entry 1 + j
+            hist[ring_index(0, j) * CH + local] = conv_in ? conv_in[((size_t)i * CD + col) * 3 + j] : 0.f;
     }
+    if (blockIdx.x == 0)
+        for (int g = threadIdx.x; g < nv; g += blockDim.x) conv_pos[(size_t)slot * nv + g] = 0;
 }
 
-hipError_t launch_state_export(const float* rec_state, const float* conv_state, const int* slots, int n, int nk,
-                               int nv, int dk, int dv, float* rec_out, float* conv_out, hipStream_t stream) {
+hipError_t launch_state_export(const float* rec_state, const float* conv_state, const int* conv_pos, const int* slots,
+                               int n, int max_slots, int nk, int nv, int dk, int dv, float* rec_out, float* conv_out,
+                               hipStream_t stream) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(state_export_kernel, dim3(64, n), dim3(256), 0, stream, rec_state, conv_state, slots, nk, nv,
-                       dk, dv, rec_out, conv_out);
+    hipLaunchKernelGGL(state_export_kernel, dim3(64, n), dim3(256), 0, stream, rec_state, conv_state, conv_pos, slots,
+                       max_slots, nk, nv, dk, dv, rec_out, conv_out);
     return hipGetLastError();
 }
 
-hipError_t launch_state_import(float* rec_state, float* conv_state, const int* slots, int n, int nk, int nv, int dk,
-                               int dv, const float* rec_in, const float* conv_in, hipStream_t stream) {
+hipError_t launch_state_import(float* rec_state, float* conv_state, int* conv_pos, const int* slots, int n,
+                               int max_slots, int nk, int nv, int dk, int dv, const float* rec_in,
+                               const float* conv_in, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(state_import_kernel, dim3(64, n), dim3(256), 0, stream, rec_state, conv_state, slots, nk, nv,
-                       dk, dv, rec_in, conv_in);
+    hipLaunchKernelGGL(state_import_kernel, dim3(64, n), dim3(256), 0, stream, rec_state, conv_state, conv_pos, slots,
+                       max_slots, nk, nv, dk, dv, rec_in, conv_in);
     return hipGetLastError();
 }
 
-__global__ void state_zero_kernel(float* __restrict__ rec, float* __restrict__ conv, const int* __restrict__ slots,
-                                  int nv, int dk, int dv, int ch) {
+__global__ void state_zero_kernel(float* __restrict__ rec, float* __restrict__ conv, int* __restrict__ conv_pos,
+                                  const int* __restrict__ slots, int max_slots, int nk, int nv, int dk, int dv) {
     const int i = blockIdx.y;
     const int slot = slots ? slots[i] : i;
+    if ((unsigned)slot >= (unsigned)max_slots) return;
     const size_t rec_n = (size_t)nv * dk * dv;
-    const size_t conv_n = (size_t)nv * 3 * ch;
+    const size_t conv_n = (size_t)nk * CONV_RING * conv_group_width(dk, dv, nv / nk);
     for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < rec_n; e += (size_t)gridDim.x * blockDim.x)
         rec[(size_t)slot * rec_n + e] = 0.f;
     for (size_t e = blockIdx.x * (size_t)blockDim.x + threadIdx.x; e < conv_n; e += (size_t)gridDim.x * blockDim.x)
         conv[(size_t)slot * conv_n + e] = 0.f;
+    if (blockIdx.x == 0)
+        for (int g = threadIdx.x; g < nv; g += blockDim.x) conv_pos[(size_t)slot * nv + g] = 0;
 }
 
-hipError_t launch_state_zero(float* rec_state, float* conv_state, const int* slots, int n, int nv, int dk, int dv,
-                             int ch, hipStream_t stream) {
+hipError_t launch_state_zero(float* rec_state, float* conv_state, int* conv_pos, const int* slots, int n,
+                             int max_slots, int nk, int nv, int dk, int dv, hipStream_t stream) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(state_zero_kernel, dim3(64, n), dim3(256), 0, stream, rec_state, conv_state, slots, nv, dk,
-                       dv, ch);
+    hipLaunchKernelGGL(state_zero_kernel, dim3(64, n), dim3(256), 0, stream, rec_state, conv_state, conv_pos, slots,
+                       max_slots, nk, nv, dk, dv);
     return hipGetLastError();
 }
 

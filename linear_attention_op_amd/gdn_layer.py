@@ -38,9 +38,21 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else None
 
 
-def _slots(slot_ids, device):
+def _slots(slot_ids, device, max_slots=None, unique=False):
+    """Slot ids as a device int32 tensor (None stays None).  Ids held on the host (lists, arrays, CPU tensors)
+    are checked against [0, max_slots) -- and, for a launch (`unique`), for repeats -- before the upload; ids
+    already on the device are passed through, and the kernels skip a sequence whose id is out of range
+    (checking them here would synchronise)."""
     if slot_ids is None:
         return None
+    on_device = isinstance(slot_ids, torch.Tensor) and slot_ids.device.type != "cpu"
+    if not on_device and max_slots is not None:
+        host = torch.as_tensor(slot_ids, dtype=torch.int64).reshape(-1)
+        if host.numel() and (int(host.min()) < 0 or int(host.max()) >= max_slots):
+            raise _lib.GdnValueError(_lib.GDN_ERR_SLOT,
+                                     f"slot ids {host.tolist()} outside [0, {max_slots})")
+        if unique and host.unique().numel() != host.numel():
+            raise _lib.GdnValueError(_lib.GDN_ERR_SLOT, f"slot ids {host.tolist()} repeat a slot")
     s = torch.as_tensor(slot_ids, dtype=torch.int32, device=device).contiguous()
     return s
 
@@ -145,7 +157,7 @@ class Qwen35GatedDeltaNetHIP:
             raise ValueError(f"hidden {H} != {self.hidden}")
         x = hidden_states.to(device=self.device, dtype=torch.bfloat16).contiguous()
         out = torch.empty_like(x)
-        s = _slots(slot_ids, self.device)
+        s = _slots(slot_ids, self.device, self.max_slots, unique=True)
         _lib.check(_lib.lib().gdn_layer_forward(self._h, _ptr(x), B, T, _ptr(s), _ptr(out), _stream()))
         return out
 
@@ -155,14 +167,14 @@ class Qwen35GatedDeltaNetHIP:
         n = len(cu_seqlens) - 1
         x = x.to(device=self.device, dtype=torch.bfloat16).reshape(-1, self.hidden).contiguous()
         out = torch.empty_like(x)
-        s = _slots(slot_ids, self.device)
+        s = _slots(slot_ids, self.device, self.max_slots, unique=True)
         _lib.check(_lib.lib().gdn_layer_forward_varlen(self._h, _ptr(x), n, cu_seqlens_arg(cu_seqlens, n), _ptr(s),
                                                        _ptr(out), _stream()))
         return out
 
     def reset_state(self, slot_ids=None):
         """Zero the conv and recurrent state of `slot_ids` (default: every slot).  9B/gdn_layer.py:137-151."""
-        s = _slots(slot_ids, self.device)
+        s = _slots(slot_ids, self.device, self.max_slots)
         n = self.max_slots if s is None else s.numel()
         _lib.check(_lib.lib().gdn_state_reset(self._h, _ptr(s), n, _stream()))
 
@@ -177,7 +189,7 @@ class Qwen35GatedDeltaNetHIP:
         return conv
 
     def get_state(self, slot_ids=None, rec=True, conv=True):
-        s = _slots(slot_ids, self.device)
+        s = _slots(slot_ids, self.device, self.max_slots)
         n = self.batch if s is None else s.numel()
         r = torch.empty(n, self.nv, self.dk, self.dv, device=self.device) if rec else None
         c = torch.empty(n, self.conv_dim, 3, device=self.device) if conv else None
@@ -186,7 +198,7 @@ class Qwen35GatedDeltaNetHIP:
 
     def set_state(self, rec=None, conv=None, slot_ids=None):
         """Seed slots with rec [n, nv, dk, dv] and conv [n, conv_dim, 3] (None conv = zero history)."""
-        s = _slots(slot_ids, self.device)
+        s = _slots(slot_ids, self.device, self.max_slots)
         ref = rec if rec is not None else conv
         n = ref.shape[0] if s is None else s.numel()
         r = rec.to(self.device, torch.float32).contiguous() if rec is not None else None
@@ -194,10 +206,11 @@ class Qwen35GatedDeltaNetHIP:
         _lib.check(_lib.lib().gdn_state_set(self._h, _ptr(s), n, _ptr(r), _ptr(c), _stream()))
 
     def state_buffers(self):
-        """Device addresses (rec, conv) of the resident state buffers."""
-        r, c = ctypes.c_void_p(), ctypes.c_void_p()
-        _lib.check(_lib.lib().gdn_layer_state_buffers(self._h, ctypes.byref(r), ctypes.byref(c)))
-        return r.value, c.value
+        """Device addresses (rec, conv, conv_pos) of the resident state buffers: the recurrent states, the conv
+        history rings and their positions."""
+        r, c, p = ctypes.c_void_p(), ctypes.c_void_p(), ctypes.c_void_p()
+        _lib.check(_lib.lib().gdn_layer_state_buffers(self._h, ctypes.byref(r), ctypes.byref(c), ctypes.byref(p)))
+        return r.value, c.value, p.value
 
     def profile(self, max_calls):
         """Record stage times (HIP events on the launch stream) for the next `max_calls` forward calls."""
@@ -228,7 +241,7 @@ class Qwen35GatedDeltaNetHIP:
         v = torch.empty(M, self.nv, self.dv, device=dev)
         g = torch.empty(M, self.nv, device=dev)
         beta = torch.empty(M, self.nv, device=dev)
-        s = _slots(slot_ids, dev)
+        s = _slots(slot_ids, dev, self.max_slots, unique=True)
         P = P.contiguous()
         _lib.check(_lib.lib().gdn_conv_front(self._h, _ptr(P), B, T, _ptr(s), _ptr(qn), _ptr(kn), _ptr(v), _ptr(g),
                                              _ptr(beta), _stream()))
@@ -237,7 +250,7 @@ class Qwen35GatedDeltaNetHIP:
     def delta_rule(self, qn, kn, v, g, beta, B, T, slot_ids=None):
         """Recurrence on the front end's outputs, continuing the slots' states -> o [M, nv, dv] fp32."""
         o = torch.empty(B * T, self.nv, self.dv, device=self.device)
-        s = _slots(slot_ids, self.device)
+        s = _slots(slot_ids, self.device, self.max_slots, unique=True)
         t = [x.contiguous() for x in (qn, kn, v, g, beta)]
         _lib.check(_lib.lib().gdn_delta_rule(self._h, *[_ptr(x) for x in t], B, T, _ptr(s), _ptr(o), _stream()))
         return o

@@ -104,7 +104,7 @@ class Qwen35GDNStackHIP:
         if H != self.hidden:
             raise ValueError(f"hidden {H} != {self.hidden}")
         x = x.contiguous()
-        s = _slots(slot_ids, self.device)
+        s = _slots(slot_ids, self.device, self.max_slots, unique=True)
         for first, count in self._runs(layers, self.n_layers):
             out = torch.empty_like(x)
             _lib.check(_lib.lib().gdn_stack_forward(self._h, _ptr(x), B, T, _ptr(s), first, count, _ptr(out),
@@ -118,7 +118,7 @@ class Qwen35GDNStackHIP:
         n = len(cu_seqlens) - 1
         x = x.to(device=self.device, dtype=torch.bfloat16).reshape(-1, self.hidden).contiguous()
         cu = cu_seqlens_arg(cu_seqlens, n)
-        s = _slots(slot_ids, self.device)
+        s = _slots(slot_ids, self.device, self.max_slots, unique=True)
         for first, count in self._runs(layers, self.n_layers):
             out = torch.empty_like(x)
             _lib.check(_lib.lib().gdn_stack_forward_varlen(self._h, _ptr(x), n, cu, _ptr(s), first, count,

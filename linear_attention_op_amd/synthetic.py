@@ -56,3 +56,38 @@ def make_inputs(dims, B, T, gen, state_std=None):
 
 def to_numpy(w):
     return {k: v.float().numpy() for k, v in w.items()}
+
+
+def continuous_batch(dims, n_layers=24, n_prefill=8, prefill_len=2048, n_decode=56, seed=4, device="cuda"):
+    """The continuous-batching stack workload: `n_layers` layers and one step of `n_prefill` prompts of
+    `prefill_len` tokens followed by `n_decode` single-token streams (sequence i on slot i).
+
+    Drawn on the device from one torch generator seeded with `seed` (a CPU draw of 24 9B-shape layers takes
+    minutes): per layer w_qkv, w_z, w_a, w_b, conv_w, w_out ~ N(0, 0.02) rounded to bf16; then, from a CPU
+    generator with the same seed, norm_w, dt_bias, A_log of every layer as in make_weights; then the decode
+    streams' states S0 [n_decode, nv, dk, dv] ~ N(0, 0.01) for every layer (a GDN state has a fixed size, so
+    a long context changes only its values), and the step's input rows x [rows, H] ~ N(0, 1) in bf16.
+    Returns (layers: list of weight dicts, cu_seqlens: list, x, s0: list per layer)."""
+    dev = torch.device(device)
+    gg = torch.Generator(device=dev).manual_seed(seed)
+    gc = torch.Generator().manual_seed(seed)
+    H, nv, dk, dv = dims["hidden"], dims["num_v_heads"], dims["head_k_dim"], dims["head_v_dim"]
+    C, Vd = conv_dim(dims), nv * dv
+
+    def n(*shape):
+        return (torch.randn(*shape, generator=gg, device=dev) * 0.02).to(torch.bfloat16)
+
+    layers = []
+    for _ in range(n_layers):
+        layers.append({"w_qkv": n(C, H), "w_z": n(Vd, H), "w_a": n(nv, H), "w_b": n(nv, H),
+                       "conv_w": n(C, 4).float(), "w_out": n(H, Vd)})
+    for w in layers:
+        w["norm_w"] = torch.rand(dv, generator=gc) + 0.5
+        w["dt_bias"] = torch.rand(nv, generator=gc) * 2.0 - 1.0
+        w["A_log"] = torch.log(torch.rand(nv, generator=gc) * 16.0).clamp_min(-20.0)
+    s0 = [torch.randn(n_decode, nv, dk, dv, generator=gg, device=dev) * 0.01 for _ in range(n_layers)]
+    cu = [0]
+    for i in range(n_prefill + n_decode):
+        cu.append(cu[-1] + (prefill_len if i < n_prefill else 1))
+    x = torch.randn(cu[-1], H, generator=gg, device=dev).to(torch.bfloat16)
+    return layers, cu, x, s0

@@ -33,6 +33,8 @@ def _dims(**kw):
     (dict(conv_kernel=3), _lib.GDN_ERR_UNSUPPORTED),
     (dict(hidden=1000), _lib.GDN_ERR_UNSUPPORTED),
     (dict(hidden=0), _lib.GDN_ERR_INVALID_ARG),
+    # the fused mixer runs a k-head and its v-heads in one workgroup: at most 4 v-heads per k-head
+    (dict(num_k_heads=4, num_v_heads=32), _lib.GDN_ERR_UNSUPPORTED),
 ])
 def test_create_rejects_bad_geometry(kw, code):
     L = _lib.lib()
@@ -111,3 +113,30 @@ def test_weight_format_checks():
     assert L.gdn_quantize_mxfp4(None, 4, 64, p, p, None) == _lib.GDN_ERR_INVALID_ARG
     assert L.gdn_quantize_mxfp4(p, 0, 64, p, p, None) == _lib.GDN_ERR_SHAPE
     assert L.gdn_quantize_mxfp4(p, 4, 48, p, p, None) == _lib.GDN_ERR_UNSUPPORTED
+
+
+def test_stack_rejects_inter_norm_wider_than_its_kernel():
+    L = _lib.lib()
+    h = ctypes.c_void_p()
+    w = _lib.GdnWeights(*([1] * 9))  # never dereferenced: geometry is checked first
+    rc = L.gdn_stack_create(ctypes.byref(_dims(hidden=8192 + 128)), ctypes.byref(w), 2, 1, None, 1, 1,
+                            ctypes.byref(h))
+    assert rc == _lib.GDN_ERR_UNSUPPORTED and b"RMSNorm" in L.gdn_last_error()
+    assert h.value is None
+
+
+def test_host_slot_ids_are_checked_before_upload():
+    import torch
+
+    from linear_attention_op_amd.gdn_layer import _slots
+
+    cpu = torch.device("cpu")
+    assert _slots(None, cpu, 4) is None
+    assert _slots([3, 0, 2], cpu, 4, unique=True).tolist() == [3, 0, 2]
+    for bad in ([0, 4], [-1], torch.tensor([1, 9])):
+        with pytest.raises(_lib.GdnValueError) as e:
+            _slots(bad, cpu, 4)
+        assert e.value.code == _lib.GDN_ERR_SLOT
+    with pytest.raises(_lib.GdnValueError):
+        _slots([1, 1], cpu, 4, unique=True)
+    assert _slots([1, 1], cpu, 4).tolist() == [1, 1]  # state reads may name a slot twice

@@ -3,9 +3,11 @@
 Truth, by size:
   * small: the CPU oracle's whole layer (fp64) on the same seeded inputs -- output rel-L2 <= 1e-2,
     recurrent state <= 1e-3;
-  * full (9B shape, T = 4096 and 16384): the oracle's sequential recurrence on the GPU front end's
-    q, k, v, g, beta (T = 4096), and the GPU token-loop kernel (itself pinned to the oracle) at both
-    sizes -- state <= 1e-3, recurrence output <= 1e-3, layer output <= 1e-2;
+  * full (9B shape, T = 4096 and 16384, seed 3): the oracle's sequential recurrence on the GPU front end's
+    q, k, v, g, beta and the GPU token-loop kernel at both sizes -- state <= 1e-3, recurrence output
+    <= 1e-3; the whole layer against the oracle's layer at T = 4096 and against the per-op pipeline with
+    the token loop at T = 16384 -- output <= 1e-2, state <= 1e-3; both projections at M = 16384 against
+    fp64 products on a sample of rows;
   * size-independent: one launch of T tokens == the same tokens over several launches (state carried).
 """
 import numpy as np
@@ -101,7 +103,7 @@ def layer9b_long():
 @pytest.mark.parametrize("T", [4096, 16384])
 def test_chunked_recurrence_full_size(layer9b_long, T):
     """9B shape, one sequence of T tokens from a zero state (seed 3): the chunked recurrence against the
-    token-loop kernel on the same front-end outputs, and (T = 4096) against the oracle's recurrence."""
+    token-loop kernel on the same front-end outputs and against the oracle's sequential recurrence."""
     d, w, gen, layer = layer9b_long
     print(f"9B chunked recurrence T={T}", flush=True)
     x, _ = syn.make_inputs(d, 1, T, gen)
@@ -118,14 +120,14 @@ def test_chunked_recurrence_full_size(layer9b_long, T):
     r_o, r_s = rel(o_chunk, o_seq.reshape(T, nv, 128)), rel(s_chunk[0], seq.get_state())
     print(f"  chunked vs token loop: o {r_o:.2e} state {r_s:.2e}", flush=True)
     assert r_o < STATE_TOL and r_s < STATE_TOL
-    if T <= 4096:
-        c = [t.cpu().numpy() for t in (qn, kn, v, g, beta)]
-        want_o, want_s = oracle.recurrent_gated_delta_rule(
-            c[0].reshape(1, T, nk, 128), c[1].reshape(1, T, nk, 128), c[2].reshape(1, T, nv, 128),
-            c[3].reshape(1, T, nv), c[4].reshape(1, T, nv), use_qk_l2norm=False, scale=1.0)
-        r_o, r_s = rel(o_chunk, want_o.reshape(T, nv, 128)), rel(s_chunk, want_s)
-        print(f"  chunked vs oracle: o {r_o:.2e} state {r_s:.2e}", flush=True)
-        assert r_o < STATE_TOL and r_s < STATE_TOL
+    # the oracle's fp64 sequential rule at full size (9B/test_gated_delta_l1.py:69-78)
+    c = [t.cpu().numpy() for t in (qn, kn, v, g, beta)]
+    want_o, want_s = oracle.recurrent_gated_delta_rule(
+        c[0].reshape(1, T, nk, 128), c[1].reshape(1, T, nk, 128), c[2].reshape(1, T, nv, 128),
+        c[3].reshape(1, T, nv), c[4].reshape(1, T, nv), use_qk_l2norm=False, scale=1.0)
+    r_o, r_s = rel(o_chunk, want_o.reshape(T, nv, 128)), rel(s_chunk, want_s)
+    print(f"  chunked vs oracle: o {r_o:.2e} state {r_s:.2e}", flush=True)
+    assert r_o < STATE_TOL and r_s < STATE_TOL
 
 
 def test_chunked_layer_full_size_16k(layer9b_long):
@@ -151,3 +153,49 @@ def test_chunked_layer_full_size_16k(layer9b_long):
     r_out, r_s = rel(out.reshape(T, -1), want), rel(s_layer[0], seq.get_state())
     print(f"9B layer T=16384: out {r_out:.2e} state {r_s:.2e}", flush=True)
     assert r_out < OUT_TOL and r_s < STATE_TOL
+
+
+def test_chunked_layer_full_size_4096_against_oracle(layer9b_long):
+    """Whole 9B layer at T = 4096 (seed 3) from a zero state against the oracle's layer (fp64 projections,
+    conv, front end, sequential rule, gated norm): output <= 1e-2, final state <= 1e-3, conv history to
+    fp32 rounding of the projection."""
+    d, w, gen, layer = layer9b_long
+    T = 4096
+    print(f"9B layer T={T} vs oracle", flush=True)
+    x, _ = syn.make_inputs(d, 1, T, gen)
+    layer.reset_state()
+    out = layer(x)
+    rec, conv = layer.get_state()
+    torch.cuda.synchronize()
+    rec_o = np.zeros((1, d["num_v_heads"], 128, 128), np.float32)
+    conv_o = np.zeros((1, syn.conv_dim(d), 3), np.float32)
+    want = oracle.layer_forward(odims(d), syn.to_numpy(w), x.numpy(), rec_o, conv_o)
+    r_out, r_s, r_c = rel(out, want), rel(rec, rec_o), rel(conv, conv_o)
+    print(f"  out {r_out:.2e} state {r_s:.2e} conv {r_c:.2e}", flush=True)
+    assert r_out < OUT_TOL and r_s < STATE_TOL and r_c < 1e-6
+
+
+def test_projections_full_size_sampled_rows(layer9b_long):
+    """The prefill GEMMs at M = 16384 (in_proj N = 12352: the q|k|v|z rows as one GEMM and the a|b rows as
+    the transposed GEMV; out_proj N = 4096), 256 sampled rows of each output against fp64 products of the
+    same bf16 operands (9B/gdn_layer.py:255-259, 272-276)."""
+    d, w, gen, layer = layer9b_long
+    T = 16384
+    x = torch.randn(T, d["hidden"], generator=gen).bfloat16()
+    y = torch.randn(T, d["num_v_heads"] * 128, generator=gen).bfloat16()
+    P = layer.in_proj(x.cuda())
+    out = layer.out_proj(y.cuda())
+    torch.cuda.synchronize()
+    rows = torch.randperm(T, generator=gen)[:256]
+    w_in = torch.cat([w["w_qkv"], w["w_z"], w["w_a"], w["w_b"]]).double()
+    want_p = x[rows].double() @ w_in.T
+    want_o = y[rows].double() @ w["w_out"].double().T
+    r_p = rel(P[rows.cuda()], want_p)
+    r_o = rel(out[rows.cuda()], want_o)
+    # every column block of P: q | k | v | z | a | b
+    Cd, Vd = syn.conv_dim(d), d["num_v_heads"] * 128
+    blocks = [(0, Cd), (Cd, Cd + Vd), (Cd + Vd, P.shape[1])]
+    worst = max(rel(P[rows.cuda(), lo:hi], want_p[:, lo:hi]) for lo, hi in blocks)
+    print(f"  M={T}: in_proj {r_p:.2e} (worst block {worst:.2e}), out_proj {r_o:.2e}", flush=True)
+    assert r_p < 1e-5 and worst < 1e-5  # fp32 accumulation of exact bf16 products
+    assert r_o < 5e-3                   # bf16 output rounding

@@ -75,6 +75,7 @@ def test_state_addresses_are_stable_and_reset_zeroes():
     f = load("tiny_continue.npz")
     layer = Qwen35GatedDeltaNetHIP(f, dims=TINY, batch=1)
     addr = layer.state_buffers()
+    assert all(addr)
     x = torch.from_numpy(f["x"])
     for t in range(8):
         layer(x[:, t:t + 1])
@@ -284,3 +285,77 @@ def test_config_9b_prefill_short(layer9b):
     print(f"9B prefill T={T}: out {rel(out, want):.2e} state {rel(rec, rec_o):.2e}", flush=True)
     assert rel(out, want) < OUT_TOL
     assert rel(rec, rec_o) < STATE_TOL
+
+
+# ---- the conv history ring --------------------------------------------------------------------------
+def _device_bytes(ptr, nbytes):
+    """Raw copy of device memory at `ptr` (a state buffer address) to the host."""
+    import ctypes
+
+    out = torch.empty(nbytes, dtype=torch.uint8)
+    hip = ctypes.CDLL("libamdhip64.so")
+    torch.cuda.synchronize()
+    assert hip.hipMemcpy(ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(ptr), ctypes.c_size_t(nbytes), 2) == 0
+    return out
+
+
+@pytest.mark.parametrize("shape", ["0.8b", "9b"])
+def test_fused_mixer_ring_matches_single_token_launches(shape):
+    """Launches of 1-5 tokens through the fused mixer (k-head groups of 1 and 2 v-heads; one workgroup per group
+    for several tokens, per v-head for one) leave the same conv history, bit for bit, and the same states as the
+    same tokens run one per launch; every v-head's ring position advances by the tokens of each launch, and the
+    raw ring read from its position equals the time-ordered export."""
+    d = syn.SHAPES[shape]
+    w, gen = syn.make_weights(d, seed=21)
+    B, Ts = 2, (1, 2, 3, 4, 5, 1, 1, 2)
+    x, s0 = syn.make_inputs(d, B, sum(Ts), gen, state_std=0.01)
+    a = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B)
+    b = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B)
+    a.set_state(rec=s0.cuda())
+    b.set_state(rec=s0.cuda())
+    nk, nv, dk, dv = d["num_k_heads"], d["num_v_heads"], d["head_k_dim"], d["head_v_dim"]
+    R, CH = nv // nk, 2 * dk + (nv // nk) * dv
+    xg = x.cuda()
+    t0 = 0
+    for T in Ts:
+        a(xg[:, t0:t0 + T])
+        for t in range(t0, t0 + T):
+            b(xg[:, t:t + 1])
+        t0 += T
+        ca, cb = a.get_conv_state(), b.get_conv_state()
+        torch.cuda.synchronize()
+        assert torch.equal(ca, cb), f"history after {t0} tokens"
+        rec_p, conv_p, pos_p = a.state_buffers()
+        pos = _device_bytes(pos_p, B * nv * 4).view(torch.int32).reshape(B, nv)
+        assert (pos == t0 % 4).all(), (t0, pos)
+        ring = _device_bytes(conv_p, B * nk * 4 * CH * 4).view(torch.float32).reshape(B, nk, 4, CH)
+        # window entry j (time order) at ring entry (pos + 1 + j) % 4; channels of group kh: q, k of kh, then v
+        # of its R v-heads
+        Kd = nk * dk
+        for kh in (0, nk - 1):
+            cols = list(range(kh * dk, kh * dk + dk)) + list(range(Kd + kh * dk, Kd + kh * dk + dk)) + \
+                list(range(2 * Kd + kh * R * dv, 2 * Kd + (kh + 1) * R * dv))
+            for j in range(3):
+                assert torch.equal(ring[:, kh, (t0 + 1 + j) % 4, :], ca.cpu()[:, cols, j]), (t0, kh, j)
+    assert rel(a.get_recurrent_state(), b.get_recurrent_state()) < 1e-6
+
+
+def test_out_of_range_device_slot_is_skipped(layer08):
+    """A device slot id outside [0, max_slots) is skipped by the kernels: the other sequence's result and every
+    slot's state are as without it."""
+    d, w, wn, gen = layer08
+    x, s0 = syn.make_inputs(d, 2, 1, gen, state_std=0.01)
+    ref = Qwen35GatedDeltaNetHIP(w, dims=d, batch=1, max_slots=3)
+    lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=1, max_slots=3)
+    for L in (ref, lay):
+        L.set_state(rec=s0[:1].expand(3, -1, -1, -1).contiguous().cuda(), slot_ids=[0, 1, 2])
+    want = ref(x[:1], slot_ids=[1])
+    before = lay.get_recurrent_state([0, 1, 2])
+    got = lay(x, slot_ids=torch.tensor([1, 7], dtype=torch.int32, device="cuda"))  # 7 >= max_slots
+    after = lay.get_recurrent_state([0, 1, 2])
+    torch.cuda.synchronize()
+    assert torch.equal(got[:1], want)
+    assert torch.equal(after[1], ref.get_recurrent_state([1])[0])
+    assert torch.equal(after[0], before[0]) and torch.equal(after[2], before[2])
+    with pytest.raises(ValueError):
+        lay(x, slot_ids=[1, 7])  # host ids are checked before the launch

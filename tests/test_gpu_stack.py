@@ -25,7 +25,9 @@ pytestmark = [pytest.mark.gpu, pytest.mark.skipif(not torch.cuda.is_available(),
 
 
 def rel(a, b):
-    a, b = a.double().cpu(), b.double().cpu()
+    """rel-L2 in fp64, on the device of `a` (large tensors are not copied to the host)."""
+    b = b.to(a.device)
+    a, b = a.double(), b.double()
     return ((a - b).norm() / b.norm()).item()
 
 
@@ -232,3 +234,68 @@ def test_layer_and_stack_from_checkpoint(tmp_path):
     sb = Qwen35GDNStackHIP(ws, dims=d, batch=B)
     assert sa.n_layers == 2
     assert torch.equal(sa(x[:, 0].cuda()), sb(x[:, 0].cuda()))
+
+
+def test_continuous_batch_stack_9b():
+    """The continuous-batching workload at full size: 24 9B-shape layers (seed 4) with the decoder RMSNorm
+    between layers, one step of 8 prompts x 2048 tokens + 56 decode streams (states 0.01 randn) as one
+    variable-length launch per layer (0.8B/gdn_l1.py:327-341 runs its layers back to back the same way;
+    layer_compute.cpp:231 maps rows to state slots).
+      * layer 0 against the oracle, fed the bf16 input the GPU layer saw: the 56 decode rows and the first
+        prompt (2048 tokens from a zero state), output (after the inter-layer norm) <= 1e-2, states <= 1e-3;
+      * every layer: the varlen launch equals the same sequences run as two separate launches (the 8 prompts,
+        the 56 streams) on a second stack, given the same input -- outputs <= 2e-3, states <= 1e-4 -- and
+        every state stays finite."""
+    print("continuous batch: 24 x 9B layers, 8 x 2048 prefill + 56 decode", flush=True)
+    d = syn.SHAPES["9b"]
+    n_pre, T_pre, n_dec, n_layers = 8, 2048, 56, 24
+    layers, cu, x, s0 = syn.continuous_batch(d, n_layers=n_layers, n_prefill=n_pre, prefill_len=T_pre,
+                                             n_decode=n_dec, seed=4)
+    n_seq, rows, H = n_pre + n_dec, cu[-1], d["hidden"]
+    nv, dk, dv = d["num_v_heads"], d["head_k_dim"], d["head_v_dim"]
+    slots = torch.arange(n_seq, dtype=torch.int32, device="cuda")
+    a = Qwen35GDNStackHIP(layers, dims=d, batch=n_seq, max_slots=n_seq, max_tokens=rows, inter_norm=True)
+    b = Qwen35GDNStackHIP(layers, dims=d, batch=n_seq, max_slots=n_seq, max_tokens=n_pre * T_pre, inter_norm=True)
+    w0 = {k: v.float().cpu().numpy() for k, v in layers[0].items()}
+    del layers
+    for i in range(n_layers):
+        for s in (a, b):
+            s.layers[i].set_state(rec=s0[i], slot_ids=slots[n_pre:])
+    dm = oracle.dims(H, d["num_k_heads"], nv, dk, dv)
+    s0_dec = s0[0].cpu().numpy()
+    del s0
+    h = x
+    for i in range(n_layers):
+        out_v = a.forward_varlen(h, cu, slot_ids=slots, layers=[i])
+        pre = b(h[:n_pre * T_pre].view(n_pre, T_pre, H), layers=[i], slot_ids=slots[:n_pre])
+        dec = b(h[n_pre * T_pre:].view(n_dec, 1, H), layers=[i], slot_ids=slots[n_pre:])
+        want = torch.cat([pre.reshape(-1, H), dec.reshape(-1, H)])
+        sa, sb = a.get_recurrent_state(i, slots), b.get_recurrent_state(i, slots)
+        torch.cuda.synchronize()
+        r, rs = rel(out_v.float(), want.float()), rel(sa, sb)
+        assert torch.isfinite(sa).all() and torch.isfinite(out_v.float()).all(), f"layer {i}"
+        assert r < 2e-3 and rs < 1e-4, f"layer {i}: varlen vs separate launches out {r:.2e} state {rs:.2e}"
+        if i == 0:
+            # the oracle: decode rows (one token each from their states) and prompt 0 (zero state)
+            hin = h.float().cpu().numpy()
+            rec_d = s0_dec.copy()
+            conv_d = np.zeros((n_dec, syn.conv_dim(d), 3), np.float32)
+            want_d = oracle.layer_forward(dm, w0, hin[n_pre * T_pre:][:, None], rec_d, conv_d)[:, 0]
+            rec_p = np.zeros((1, nv, dk, dv), np.float32)
+            conv_p = np.zeros((1, syn.conv_dim(d), 3), np.float32)
+            want_p = oracle.layer_forward(dm, w0, hin[None, :T_pre], rec_p, conv_p)[0]
+
+            def norm(o):  # the decoder RMSNorm after the layer (w = 0), float32 on bf16 values
+                o = torch.from_numpy(o).bfloat16().float()
+                return (o * torch.rsqrt(o.pow(2).mean(-1, keepdim=True) + 1e-6)).bfloat16().float()
+
+            got = out_v.float().cpu()
+            r_d, r_p = rel(got[n_pre * T_pre:], norm(want_d)), rel(got[:T_pre], norm(want_p))
+            r_sd = rel(sa[n_pre:], torch.from_numpy(rec_d))
+            r_sp = rel(sa[0], torch.from_numpy(rec_p[0]))
+            print(f"  layer 0 vs oracle: decode out {r_d:.2e} state {r_sd:.2e}; prompt out {r_p:.2e} "
+                  f"state {r_sp:.2e}", flush=True)
+            assert r_d < 1e-2 and r_p < 1e-2 and r_sd < 1e-3 and r_sp < 1e-3
+        if i % 8 == 7:
+            print(f"  layer {i}: varlen vs separate out {r:.2e} state {rs:.2e}", flush=True)
+        h = out_v
