@@ -239,6 +239,20 @@ int gdn_delta_rule_fla_ws(const float* q, const float* k, const float* v, const 
                           int B, int T, int Hk, int Hv, int dk, int dv, float* state, int use_qk_l2norm,
                           float scale, float* o, void* workspace, size_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference: gdn_delta_rule_fla_ws for callers that cannot allocate device memory
+ * (code under HIP-graph capture, serving loops and harnesses that forbid hipMalloc).  The chunk-64 workspace
+ * is a static device array of GDN_NOALLOC_SCRATCH_BYTES that the library holds on every device it runs on
+ * until the process ends; nothing is allocated and no workspace is passed.  Launches that need more
+ * (B * Hv * ceil(T / 64) above 511 for 128-wide heads) return GDN_ERR_SHAPE; launches the token loop runs
+ * (T <= 64, other head sizes) need none.  Same arguments, layouts and results as gdn_delta_rule_fla_ws with a
+ * large enough workspace.  All calls on one device share that device's array: calls that overlap in time on
+ * one device (other streams, other threads) race; the array keeps the last call's contents and needs no
+ * clearing (every call writes all it reads). */
+#define GDN_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+int gdn_delta_rule_fla_noalloc(const float* q, const float* k, const float* v, const float* g, const float* beta,
+                               int B, int T, int Hk, int Hv, int dk, int dv, float* state, int use_qk_l2norm,
+                               float scale, float* o, void* stream);
+
 /* Projection y[M, N] = x[M, K] . w[N, K]^T, bf16 inputs, fp32 accumulation (the ttnn.linear call sites
  * 9B/gdn_layer.py:255, 259, 272).  out_fp32 != 0: y is fp32, else bf16.  K % 128 == 0. */
 int gdn_linear_bf16(const void* x, const void* w, int M, int N, int K, void* y, int out_fp32, void* stream);

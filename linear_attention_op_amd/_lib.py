@@ -97,6 +97,7 @@ SIGNATURES = {
     "gdn_delta_rule_fla": (_I, [_V, _V, _V, _V, _V, _I, _I, _I, _I, _I, _I, _V, _I, _F, _V, _V]),
     "gdn_delta_rule_fla_workspace_size": (_Z, [_I, _I, _I, _I, _I]),
     "gdn_delta_rule_fla_ws": (_I, [_V, _V, _V, _V, _V, _I, _I, _I, _I, _I, _I, _V, _I, _F, _V, _V, _Z, _V]),
+    "gdn_delta_rule_fla_noalloc": (_I, [_V, _V, _V, _V, _V, _I, _I, _I, _I, _I, _I, _V, _I, _F, _V, _V]),
     "gdn_linear_bf16": (_I, [_V, _V, _I, _I, _I, _V, _I, _V]),
     "gdn_quantize_fp8": (_I, [_V, _I, _I, _V, _V, _V]),
     "gdn_quantize_mxfp4": (_I, [_V, _I, _I, _V, _V, _V]),

@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -697,6 +698,61 @@ int gdn_delta_rule_fla_ws(const float* q, const float* k, const float* v, const 
     else
         HIP_OK(gdn::launch_delta_seq(r, dk, dv, as_stream(stream)));
     return GDN_OK;
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------------------------------------
+// gdn_delta_rule_fla_noalloc: gdn_delta_rule_fla_ws with the chunk workspace in a static device array, for
+// callers that cannot allocate.  Each device that runs it holds its own copy of the array until the process
+// ends; host code uses the copy's device address from hipGetSymbolAddress, taken once per device.
+// ------------------------------------------------------------------------------------------------
+namespace {
+
+__device__ __align__(256) unsigned char scratch[GDN_NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+std::vector<void*> g_scratch_addr;  // per device: the address of that device's `scratch`
+
+// The address of the current device's scratch array (looked up on the first call on that device).
+int scratch_address(void** out) {
+    int dev = 0;
+    HIP_OK(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if ((size_t)dev >= g_scratch_addr.size()) g_scratch_addr.resize((size_t)dev + 1, nullptr);
+    if (!g_scratch_addr[dev]) {
+        void* p = nullptr;
+        HIP_OK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        if (!p) return fail(GDN_ERR_HIP, "hipGetSymbolAddress returned no address for the scratch array");
+        g_scratch_addr[dev] = p;
+    }
+    *out = g_scratch_addr[dev];
+    return GDN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gdn_delta_rule_fla_noalloc(const float* q, const float* k, const float* v, const float* g, const float* beta,
+                               int B, int T, int Hk, int Hv, int dk, int dv, float* state, int use_qk_l2norm,
+                               float scale, float* o, void* stream) {
+    if (B <= 0 || T <= 0 || Hv <= 0)
+        return fail(GDN_ERR_SHAPE, "gdn_delta_rule_fla_noalloc: B=%d T=%d Hv=%d", B, T, Hv);
+    const size_t need = gdn_delta_rule_fla_workspace_size(B, T, Hv, dk, dv);
+    if (need > GDN_NOALLOC_SCRATCH_BYTES)
+        return fail(GDN_ERR_SHAPE,
+                    "gdn_delta_rule_fla_noalloc: this launch needs %zu bytes of chunk workspace, more than the "
+                    "%zu-byte static scratch array (B * Hv * ceil(T / 64) must be at most %zu)",
+                    need, (size_t)GDN_NOALLOC_SCRATCH_BYTES,
+                    (size_t)GDN_NOALLOC_SCRATCH_BYTES / gdn::delta_chunked_workspace(1, 64, 1, 128, 128));
+    void* ws = nullptr;
+    if (need > 0) {
+        int rc = scratch_address(&ws);
+        if (rc) return rc;
+    }
+    return gdn_delta_rule_fla_ws(q, k, v, g, beta, B, T, Hk, Hv, dk, dv, state, use_qk_l2norm, scale, o, ws,
+                                 need > 0 ? (size_t)GDN_NOALLOC_SCRATCH_BYTES : 0, stream);
 }
 
 int gdn_linear_bf16(const void* x, const void* w, int M, int N, int K, void* y, int out_fp32, void* stream) {
