@@ -218,7 +218,9 @@ def pmc_child(steps=4):
 def profile_child(which):
     """Workload for an external profiler (rocprofv3 --kernel-trace / --pmc put this process after `--`):
     `decode`: 9B decode at batch 64, 4 layer copies rotated as in the benchmark, 3 warm-up + 12 steps;
-    `prefill`: one 16384-token prefill of a 9B layer, 1 warm-up + 3 runs."""
+    `prefill`: one 16384-token prefill of a 9B layer, 1 warm-up + 3 runs;
+    `small`: 9B decode at batch 1 and at batch 8, then the 0.8B shape at batch 1, 8 layer copies each rotated,
+    3 warm-up + 12 steps each."""
     import torch
 
     from linear_attention_op_amd import Qwen35GatedDeltaNetHIP
@@ -227,7 +229,25 @@ def profile_child(which):
     dev = torch.device("cuda", 0)
     d = syn.SHAPES["9b"]
     w, _ = syn.make_weights(d, seed=2)
-    if which == "decode":
+    if which == "small":
+        for shape, B in (("9b", 1), ("9b", 8), ("0.8b", 1)):
+            ds = syn.SHAPES[shape]
+            ws, _ = syn.make_weights(ds, seed=0)
+            layers = []
+            for i in range(8):
+                gg = torch.Generator(device=dev).manual_seed(200 + i)
+                wi = {k: (torch.randn(v.shape, generator=gg, device=dev) * v.float().std()).to(v.dtype)
+                      if k.startswith("w_") or k == "conv_w" else v for k, v in ws.items()}
+                lay = Qwen35GatedDeltaNetHIP(wi, dims=ds, batch=B, max_tokens=64)
+                lay.set_state(rec=torch.randn(B, ds["num_v_heads"], 128, 128, device=dev) * 0.01)
+                layers.append(lay)
+            x = torch.randn(B, 1, ds["hidden"], device=dev).to(torch.bfloat16)
+            for i in range(15):
+                layers[i % 8](x)
+            torch.cuda.synchronize()
+            for lay in layers:
+                lay.close()
+    elif which == "decode":
         layers = []
         for i in range(4):
             gg = torch.Generator(device=dev).manual_seed(100 + i)
