@@ -30,19 +30,25 @@ struct DeltaTile {
         rg = tid / CG;
     }
     // The state is streamed: read once and written once per launch, so both directions use
-    // non-temporal accesses and do not displace the projection weights from the caches.
+    // non-temporal accesses and do not displace the projection weights from the caches.  Row i of the
+    // thread is at S + RG DV i (the same for every thread: a scalar base) + rg DV + 4 cg (one 32-bit offset
+    // per thread), so the 16 accesses share a single address register.
     __device__ __forceinline__ void load(const float* S) {
+        const unsigned off = (unsigned)(rg * DV + 4 * cg);
 #pragma unroll
         for (int i = 0; i < RPT; ++i) {
-            const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(S + (size_t)(rg + RG * i) * DV + 4 * cg));
+            const float* row = S + (size_t)RG * DV * i;
+            const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(row + off));
             s[i] = make_float4(v[0], v[1], v[2], v[3]);
         }
     }
     __device__ __forceinline__ void store(float* S) const {
+        const unsigned off = (unsigned)(rg * DV + 4 * cg);
 #pragma unroll
         for (int i = 0; i < RPT; ++i) {
+            float* row = S + (size_t)RG * DV * i;
             const f32x4 v = {s[i].x, s[i].y, s[i].z, s[i].w};
-            __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(S + (size_t)(rg + RG * i) * DV + 4 * cg));
+            __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(row + off));
         }
     }
 

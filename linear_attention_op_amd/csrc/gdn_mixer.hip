@@ -47,7 +47,7 @@ __global__ __launch_bounds__(PER_HEAD ? 256 : 256 * R) void mixer_kernel(MixerAr
     const int Kd = nk * DK, Vd = nv * DV, CD = 2 * Kd + Vd;
     const int slot = a.slot_ids ? a.slot_ids[b] : b;
     if ((unsigned)slot >= (unsigned)a.max_slots) return;
-    const int T = a.T;
+    const int T = PER_HEAD ? 1 : a.T;  // per-head workgroups run single-token launches only
 
     __shared__ float sq[DK], sk[DK], sv[HW][DV];
     __shared__ float red[HW][4][2][DV];
