@@ -133,55 +133,70 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
             *reinterpret_cast<float4*>(&dst[(4 * prow + j) * LDK + pc4]) = x[j];
         }
     };
+    // The fused front end (FUSED), from the projection rows: causal conv (4 taps over the inputs at t - 3 .. t,
+    // the slot's history before t = 0) + SiLU, as conv_front_kernel (layer_compute.cpp C1, 74-103).  The window
+    // of the thread's 4 tokens is 7 input rows, loaded one tensor at a time (register budget).
+    const int R = Hv / Hk;
+    const int Kd = f.nk * DK, Vd = f.nv * DV, CD = 2 * Kd + Vd, CH = conv_group_width(DK, DV, R);
+    const float* hg = nullptr;  // the k-head group's history ring (q and k of kh, v of this head at 2 DK + (h % R) DV)
+    int pos = 0;
     if constexpr (FUSED) {
-        // The front end, from the projection rows: causal conv (4 taps over the inputs at t - 3 .. t, the
-        // slot's history before t = 0) + SiLU, as conv_front_kernel (layer_compute.cpp C1, 74-103).  The
-        // window of the thread's 4 tokens is 7 input rows, loaded one tensor at a time (register budget).
-        const int R = Hv / Hk;
-        const int Kd = f.nk * DK, Vd = f.nv * DV, CD = 2 * Kd + Vd, CH = conv_group_width(DK, DV, R);
         const int slot = f.slot_ids ? f.slot_ids[b] : b;
-        // the k-head group's history ring (q and k of kh, v of this head at 2 DK + (h % R) DV)
-        const float* hg = f.conv_state + ((size_t)slot * f.nk + kh) * CONV_RING * CH;
-        const int pos = f.conv_pos[(size_t)slot * f.nv + h];
-        const int colq = kh * DK + pc4, colk = Kd + kh * DK + pc4, colv = 2 * Kd + h * DV + pc4;
-        auto in_row = [&](int tk, int col, const float* hist, int local) -> float4 {
-            const int tkc = min(tk, len - 1);  // rows past the end read a valid row, zeroed below
-            const int t = t0 + tkc;
-            const float* p = t >= 0 ? f.P + (size_t)((long long)row0 + tkc) * f.NP + col
-                                    : hist + ring_index(pos, 3 + t) * CH + local;
-            return keep_if(tk < len, *reinterpret_cast<const float4*>(p));
-        };
+        hg = f.conv_state + ((size_t)slot * f.nk + kh) * CONV_RING * CH;
+        pos = f.conv_pos[(size_t)slot * f.nv + h];
+    }
+    const int colq = kh * DK + pc4, colk = Kd + kh * DK + pc4, colv = 2 * Kd + h * DV + pc4;
+    const int locv = 2 * DK + (h % R) * DV + pc4;
+    auto in_row = [&](int tk, int col, int local) -> float4 {
+        const int tkc = min(tk, len - 1);  // rows past the end read a valid row, zeroed below
+        const int t = t0 + tkc;
+        const float* p = t >= 0 ? f.P + (size_t)((long long)row0 + tkc) * f.NP + col
+                                : hg + ring_index(pos, 3 + t) * CH + local;
+        return keep_if(tk < len, *reinterpret_cast<const float4*>(p));
+    };
+    auto window = [&](int col, int local, float4* x) {
+#pragma unroll
+        for (int r = 0; r < 7; ++r) x[r] = in_row(4 * prow - 3 + r, col, local);
+    };
+    auto convolve = [&](int col, const float4* x, float4* out) {
+        float4 w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = f.conv_w[col + i];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const float4 x0 = x[j], x1 = x[j + 1], x2 = x[j + 2], x3 = x[j + 3];
+            float4 o;
+            o.x = siluf_(w[0].x * x0.x + w[0].y * x1.x + w[0].z * x2.x + w[0].w * x3.x);
+            o.y = siluf_(w[1].x * x0.y + w[1].y * x1.y + w[1].z * x2.y + w[1].w * x3.y);
+            o.z = siluf_(w[2].x * x0.z + w[2].y * x1.z + w[2].z * x2.z + w[2].w * x3.z);
+            o.w = siluf_(w[3].x * x0.w + w[3].y * x1.w + w[3].z * x2.w + w[3].w * x3.w);
+            out[j] = keep_if(4 * prow + j < len, o);
+        }
+    };
+    if constexpr (FUSED) {
         if (wave == 0 && lane < len) {
             const float* Pr = f.P + (row0 + lane) * f.NP + CD + Vd;
             gv = f.neg_A[h] * softplusf_(Pr[h] + f.dt_bias[h]);
             bv = sigmoidf_(Pr[f.nv + h]);
         }
-        auto conv4 = [&](int col, const float* hist, int local, float4* out) {
-            float4 x[7], w[4];
-#pragma unroll
-            for (int r = 0; r < 7; ++r) x[r] = in_row(4 * prow - 3 + r, col, hist, local);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) w[i] = f.conv_w[col + i];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float4 x0 = x[j], x1 = x[j + 1], x2 = x[j + 2], x3 = x[j + 3];
-                float4 o;
-                o.x = siluf_(w[0].x * x0.x + w[0].y * x1.x + w[0].z * x2.x + w[0].w * x3.x);
-                o.y = siluf_(w[1].x * x0.y + w[1].y * x1.y + w[1].z * x2.y + w[1].w * x3.y);
-                o.z = siluf_(w[2].x * x0.z + w[2].y * x1.z + w[2].z * x2.z + w[2].w * x3.z);
-                o.w = siluf_(w[3].x * x0.w + w[3].y * x1.w + w[3].z * x2.w + w[3].w * x3.w);
-                out[j] = keep_if(4 * prow + j < len, o);
-            }
-        };
-        // one tensor at a time, the queries normalised and stored before the next window is loaded
+        // the queries normalised and stored before the keys' window is loaded
         {
-            float4 qr[4];
-            conv4(colq, hg, pc4, qr);
+            float4 x[7], qr[4];
+            window(colq, pc4, x);
+            convolve(colq, x, qr);
             l2store(qr, a.scale, sQ);
         }
-        conv4(colk, hg, DK + pc4, kr);
+        {
+            float4 x[7];
+            window(colk, DK + pc4, x);
+            convolve(colk, x, kr);
+        }
         l2store(kr, 1.f, sK);
-        conv4(colv, hg, 2 * DK + (h % R) * DV + pc4, vr);
+        {
+            float4 x[7];
+            window(colv, locv, x);
+            convolve(colv, x, vr);
+        }
     } else {
         float4 qr[4];
 #pragma unroll
@@ -400,6 +415,44 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
     __syncthreads();
 
     // ---- 5, 6. [T; M2] x (beta K e^G | beta V) -----------------------------------------------------------
+    // X = beta K e^G and beta V, transposed and split into bf16 hi | lo planes, from the keys and values in
+    // registers (thread (prow, pc4): tokens 4 prow + j of channels pc4 + cc, half `prow % 2` of the 8-token
+    // group prow / 2).  Element (r, tok) at r * CK + ((tok / 8) ^ ((r / 4) % 8)) * 8 + tok % 8.  A store
+    // instruction writes rows 4 l + cc (l < 32, one cc): keyed on r / 4 the xor spreads them over eight 16-byte
+    // slots (4-way bank conflicts; keyed on r % 8, two slots and 16-way), and the 16-byte fragment reads below
+    // stay at two lanes per bank group.
+    // Order, for the register budget: X^T goes where L and the phase-3 scratch were (its hi plane after T in
+    // the key region, its lo plane over L) while T and M2 are still in LDS, so the keys leave the registers
+    // before T and M2 enter them; W and Q' follow (the queries leave); then (beta V)^T goes over T and M2.
+    u16* XTh = reinterpret_cast<u16*>(sK + CK * LDT);
+    u16* XTl = reinterpret_cast<u16*>(sL);
+    u16* VTh = reinterpret_cast<u16*>(sT);
+    u16* VTl = reinterpret_cast<u16*>(sA);
+    static_assert(DK * CK <= 2 * (CK * LDK - CK * LDT) && DV * CK <= 2 * CK * LDT, "X^T / V^T planes");
+    auto put_t = [&](u16* hp, u16* lp, const float4* x, const float* sc) {
+        const int tg = prow >> 1, half = (prow & 1) * 4;
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            const int r = pc4 + cc;
+            u16x4 h4, l4;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float v = (cc == 0 ? x[j].x : (cc == 1 ? x[j].y : (cc == 2 ? x[j].z : x[j].w))) * sc[j];
+                const __bf16 vh = (__bf16)v;
+                h4[j] = __builtin_bit_cast(u16, vh);
+                l4[j] = (u16)bf16_bits(v - (float)vh);
+            }
+            const int o = r * CK + ((tg ^ ((r >> 2) & 7)) << 3) + half;
+            *reinterpret_cast<u16x4*>(hp + o) = h4;
+            *reinterpret_cast<u16x4*>(lp + o) = l4;
+        }
+    };
+    {
+        float sc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sc[j] = sBeta[4 * prow + j] * sEG[4 * prow + j];
+        put_t(XTh, XTl, kr, sc);
+    }
     const int nks = (16 * mi + 15 >= 32) ? 2 : 1;  // row tile mi of T and M2 is zero past column 16 mi + 15
     Split8 At[2], Am[2];
 #pragma unroll
@@ -411,50 +464,10 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
         At[s] = split8(tv);
         Am[s] = split8(mv);
     }
-    __syncthreads();  // T and M2 are in registers: both regions are free
-    // X = beta K e^G (over sK) and beta V (over sLA), transposed and split into bf16 hi | lo planes, from the
-    // keys and values in registers (thread (prow, pc4): tokens 4 prow + j of channels pc4 + cc, half
-    // `prow % 2` of the 8-token group prow / 2).  Element (r, tok) at r * CK + ((tok / 8) ^ (r % 8)) * 8 +
-    // tok % 8: the xor puts the 16-byte reads of eight consecutive rows in distinct banks.
-    u16* XTh = reinterpret_cast<u16*>(sK);
-    u16* XTl = XTh + DK * CK;
-    u16* VTh = reinterpret_cast<u16*>(sLA);
-    u16* VTl = VTh + DV * CK;
-    {
-        const int tg = prow >> 1, half = (prow & 1) * 4;
-        float bt[4], sc[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int tok = 4 * prow + j;
-            bt[j] = sBeta[tok];
-            sc[j] = bt[j] * sEG[tok];
-        }
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) {
-            const int r = pc4 + cc;
-            u16x4 xh4, xl4, vh4, vl4;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float kv = cc == 0 ? kr[j].x : (cc == 1 ? kr[j].y : (cc == 2 ? kr[j].z : kr[j].w));
-                const float vv = cc == 0 ? vr[j].x : (cc == 1 ? vr[j].y : (cc == 2 ? vr[j].z : vr[j].w));
-                const float x = kv * sc[j], y = vv * bt[j];
-                const __bf16 xh = (__bf16)x, yh = (__bf16)y;
-                xh4[j] = __builtin_bit_cast(u16, xh);
-                xl4[j] = (u16)bf16_bits(x - (float)xh);
-                vh4[j] = __builtin_bit_cast(u16, yh);
-                vl4[j] = (u16)bf16_bits(y - (float)yh);
-            }
-            const int o = r * CK + ((tg ^ (r & 7)) << 3) + half;
-            *reinterpret_cast<u16x4*>(XTh + o) = xh4;
-            *reinterpret_cast<u16x4*>(XTl + o) = xl4;
-            *reinterpret_cast<u16x4*>(VTh + o) = vh4;
-            *reinterpret_cast<u16x4*>(VTl + o) = vl4;
-        }
-    }
-    __syncthreads();  // X^T and (beta V)^T are complete
+    __syncthreads();  // X^T is complete; T and M2 are in registers, so their regions are free
     // operand of token group (4 s + grp) for row r (16-byte reads, the xor layout above)
     auto tfrag = [&](const u16* hp, const u16* lp, int r, int s) {
-        const int o = r * CK + (((4 * s + grp) ^ (r & 7)) << 3);
+        const int o = r * CK + (((4 * s + grp) ^ ((r >> 2) & 7)) << 3);
         return Split8{*reinterpret_cast<const bf16x8*>(hp + o), *reinterpret_cast<const bf16x8*>(lp + o)};
     };
 
@@ -491,6 +504,13 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
         *reinterpret_cast<u16x8*>(Wf + f8) = fw;
         *reinterpret_cast<u16x8*>(Qf + f8) = fq;
     }
+    {
+        float bt[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) bt[j] = sBeta[4 * prow + j];
+        put_t(VTh, VTl, vr, bt);
+    }
+    __syncthreads();  // (beta V)^T is complete
     // 6. U = T (beta V) (lane (m, grp): tokens 16 mi + 4 grp + i of column 16 n + m) and the intra-chunk
     //    output M2 (beta V) into o
     float* U = ws.U + hc * CK * DV;
