@@ -243,7 +243,7 @@ int gdn_delta_rule_fla_ws(const float* q, const float* k, const float* v, const 
  * (code under HIP-graph capture, serving loops and harnesses that forbid hipMalloc).  The chunk-64 workspace
  * is a static device array of GDN_NOALLOC_SCRATCH_BYTES that the library holds on every device it runs on
  * until the process ends; nothing is allocated and no workspace is passed.  Launches that need more
- * (B * Hv * ceil(T / 64) above 511 for 128-wide heads) return GDN_ERR_SHAPE; launches the token loop runs
+ * (B * Hv * ceil(T / 64) above 408 for 128-wide heads) return GDN_ERR_SHAPE; launches the token loop runs
  * (T <= 64, other head sizes) need none.  Same arguments, layouts and results as gdn_delta_rule_fla_ws with a
  * large enough workspace.  All calls on one device share that device's array: calls that overlap in time on
  * one device (other streams, other threads) race; the array keeps the last call's contents and needs no

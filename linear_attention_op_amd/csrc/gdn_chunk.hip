@@ -53,6 +53,8 @@ struct ChunkWs {
     u16* Kf;    // [B, Hv, NC][8 w][2 s][2 plane][64 lane][8]: Kt[16 w + m][32 s + 8 grp + j], plane 0 hi, 1 lo
     float* U;   // [B, Hv, NC][4 mi][DV / 16 n][64 lane][4]: U[16 mi + 4 grp + i][16 n + m] (the prep pass's
                 //   MFMA C order: one 16-byte store per lane; the state pass reads 8 contiguous bytes)
+    float* O;   // the intra-chunk output M2 (beta V), laid out as U (in the output's own layout each lane's
+                //   four rows would be four 4-byte stores, twice the prep pass's store instructions)
     float* G;   // [B, Hv, NC, CK]       G (in-chunk cumulative log decay)
     int NC;     // chunks per sequence
 };
@@ -512,8 +514,9 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
     }
     __syncthreads();  // (beta V)^T is complete
     // 6. U = T (beta V) (lane (m, grp): tokens 16 mi + 4 grp + i of column 16 n + m) and the intra-chunk
-    //    output M2 (beta V) into o
+    //    output M2 (beta V), both in U's layout
     float* U = ws.U + hc * CK * DV;
+    float* O = ws.O + hc * CK * DV;
 #pragma unroll
     for (int nn = 0; nn < 4; ++nn) {
         const int n = 4 * hf + nn, col = 16 * n + m;
@@ -526,11 +529,7 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
             accM = mfma3(Am[s], V, accM);
         }
         *reinterpret_cast<f32x4*>(U + ((size_t)(mi * (DV / 16) + n) * 64 + lane) * 4) = accT;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int r = 16 * mi + 4 * grp + i;
-            if (r < len) a.o[((row0 + r) * Hv + h) * DV + col] = accM[i];
-        }
+        *reinterpret_cast<f32x4*>(O + ((size_t)(mi * (DV / 16) + n) * 64 + lane) * 4) = accM;
     }
     if (tid < CK) ws.G[hc * CK + tid] = sG[tid];
 }
@@ -571,7 +570,7 @@ struct StateOps {
     u16x8 kh[2], kl[2];   // Kt [16 wave + m][32 s + 8 grp + j] (hi / lo)
     float glast;          // G of the chunk's last token
     float2 u;             // U[2 p + e][n0 + col], e < 2
-    float2 o;             // intra-chunk output at the same places
+    float2 o;             // the intra-chunk output at the same places
 };
 
 __device__ __forceinline__ Split4 frag4(const u16x8 v) {
@@ -631,15 +630,12 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
             }
             op.glast = ws.G[hc * CK + CK - 1];
         } else {
-            const int t0 = c * CK, len = min(CK, T - t0);
-            const size_t row0 = (size_t)b * T + t0;
-            // tokens 2p, 2p + 1 of column n0 + col: token tile p / 8, lane 16 ((p / 2) % 4) + col, slots 2 (p % 2) + e
-            op.u = *reinterpret_cast<const float2*>(
-                ws.U + hc * CK * DV + ((size_t)((p >> 3) * (DV / 16) + cb) * 64 + 16 * ((p >> 1) & 3) + col) * 4 +
-                2 * (p & 1));
-            // rows past the end of a partial chunk read a valid row (the value is not used): no branch
-            op.o.x = a.o[((row0 + min(2 * p, len - 1)) * Hv + h) * DV + n0 + col];
-            op.o.y = a.o[((row0 + min(2 * p + 1, len - 1)) * Hv + h) * DV + n0 + col];
+            // U and the intra-chunk output for tokens 2p, 2p + 1 of column n0 + col: token tile p / 8, lane
+            // 16 ((p / 2) % 4) + col, slots 2 (p % 2) + e
+            const size_t uo = hc * CK * DV + ((size_t)((p >> 3) * (DV / 16) + cb) * 64 + 16 * ((p >> 1) & 3) + col) * 4 +
+                              2 * (p & 1);
+            op.u = *reinterpret_cast<const float2*>(ws.U + uo);
+            op.o = *reinterpret_cast<const float2*>(ws.O + uo);
         }
     };
     using P0 = std::integral_constant<int, 0>;
@@ -764,14 +760,15 @@ static ChunkWs chunk_ws(const DeltaArgs& a, void* workspace) {
     ws.Kf = p, p += n * CK * D * 2;
     float* f = reinterpret_cast<float*>(p);
     ws.U = f, f += n * CK * D;
+    ws.O = f, f += n * CK * D;
     ws.G = f;
     return ws;
 }
 
 size_t delta_chunked_workspace(int B, int T, int Hv, int dk, int dv) {
     const size_t NC = (size_t)(T + CK - 1) / CK;
-    // W, Q', keys: bf16 hi + lo (4 bytes per value); U, G: fp32
-    return (size_t)B * Hv * NC * ((size_t)CK * dk * 3 + (size_t)CK * dv + CK) * sizeof(float);
+    // W, Q', keys: bf16 hi + lo (4 bytes per value); U, the intra-chunk output, G: fp32
+    return (size_t)B * Hv * NC * ((size_t)CK * dk * 3 + (size_t)CK * dv * 2 + CK) * sizeof(float);
 }
 
 bool delta_chunked_supported(int dk, int dv) { return dk == 128 && dv == 128; }

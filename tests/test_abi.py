@@ -72,8 +72,8 @@ def test_linear_and_recurrence_shape_checks():
 def test_chunked_recurrence_workspace_checks():
     L = _lib.lib()
     need = L.gdn_delta_rule_fla_workspace_size(2, 200, 32, 128, 128)
-    # W, Q', keys (bf16 hi + lo) and U, G (fp32) for 4 chunks of 64 tokens per (sequence, v-head)
-    assert need == 2 * 32 * 4 * (64 * 128 * 3 + 64 * 128 + 64) * 4
+    # W, Q', keys (bf16 hi + lo) and U, the intra-chunk output, G (fp32) for 4 chunks of 64 tokens per (sequence, v-head)
+    assert need == 2 * 32 * 4 * (64 * 128 * 3 + 64 * 128 * 2 + 64) * 4
     assert L.gdn_delta_rule_fla_workspace_size(2, 64, 32, 128, 128) == 0  # one chunk: the token loop
     assert L.gdn_delta_rule_fla_workspace_size(2, 200, 32, 64, 64) == 0   # chunked form is for 128 x 128
     assert L.gdn_delta_rule_fla_workspace_size(0, 200, 32, 128, 128) == 0

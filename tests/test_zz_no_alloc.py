@@ -59,7 +59,7 @@ def test_noalloc_equals_workspace_entry(shapes):
 def test_noalloc_rejects_launches_beyond_the_array():
     L = _lib.lib()
     p = ctypes.c_void_p(16)  # never dereferenced: the size is checked before any launch
-    # one 16384-token sequence of 32 heads: 8192 head-chunks of workspace, the array holds 511
+    # one 16384-token sequence of 32 heads: 8192 head-chunks of workspace, the array holds 408
     rc = L.gdn_delta_rule_fla_noalloc(p, p, p, p, p, 1, 16384, 16, 32, 128, 128, p, 1, 0.0, p, None)
     assert rc == _lib.GDN_ERR_SHAPE
     assert b"static scratch" in L.gdn_last_error()
