@@ -15,8 +15,8 @@
 //
 // Two kernels:
 //  * chunk_prep_kernel: every (sequence, v-head, chunk) in parallel.  Everything that does not depend on
-//    S: G, L, T, U, W, Q', the decay-scaled transposed keys and the intra-chunk output Aqk U (written
-//    straight into o).
+//    S: G, L, T, U, W, Q', the decay-scaled transposed keys and the intra-chunk output Aqk U (into the
+//    workspace, laid out as U).
 //  * chunk_state_kernel: the sequential pass over chunks.  A workgroup owns 16 value columns of one
 //    (sequence, v-head) state; its eight waves own 16 state rows each, held in MFMA accumulators for the
 //    whole launch (state read once, written once).  Per chunk: W S and Q' S (partials over the waves'
@@ -25,8 +25,10 @@
 //    parts spread over its own work.  Workgroup ids put the 8 column blocks of a head on one XCD so that they
 //    share that XCD's L2 copy of W, Q' and the keys.
 //
-// Precision: every product that feeds the state or the output goes through split bf16 (hi + lo, three
-// MFMAs, ~2^-17 relative), so the chunked state matches the fp32 sequential rule to ~1e-5.
+// Precision: every product that feeds the state goes through split bf16 (hi + lo, three MFMAs, ~2^-17
+// relative), so the chunked state matches the fp32 sequential rule to ~1e-5.  So does Q' S in the
+// recurrence-only op (fp32 output); in the layer, whose output is bf16 after the gated norm, Q' is bf16
+// alone (two MFMAs, S still split): output error 2.3-2.5e-3 against the fp64 oracle, as with split Q'.
 #include <cmath>
 #include <type_traits>
 
@@ -504,7 +506,14 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
         }
         const size_t f8 = ((size_t)(mi * 8 + n) * 64 + lane) * 8;
         *reinterpret_cast<u16x8*>(Wf + f8) = fw;
-        *reinterpret_cast<u16x8*>(Qf + f8) = fq;
+        if constexpr (FUSED) {
+            // the layer: Q' in bf16 alone (it only feeds the output), row tiles in pairs so that the state pass
+            // reads two of them per 16-byte load: [mi / 2][n][lane][mi % 2][4]
+            const u16x4 qh4 = {fq[0], fq[1], fq[2], fq[3]};
+            *reinterpret_cast<u16x4*>(Qf + ((size_t)((mi >> 1) * 8 + n) * 64 + lane) * 8 + (mi & 1) * 4) = qh4;
+        } else {
+            *reinterpret_cast<u16x8*>(Qf + f8) = fq;
+        }
     }
     {
         float bt[4];
@@ -564,9 +573,10 @@ __device__ __forceinline__ f32x4 mfma3k16(const Split4& a, const Split4& b, f32x
 }
 
 // One chunk's operands for one lane (about 50 VGPRs, so three chunks fit in registers).
+template <bool QSPLIT>
 struct StateOps {
-    u16x8 w[4];           // W [16 rt + m][16 wave + 4 grp + j]: hi j < 4, then lo
-    u16x8 q[4];           // Q' at the same place
+    u16x8 w[4];                  // W [16 rt + m][16 wave + 4 grp + j]: hi j < 4, then lo
+    u16x8 q[QSPLIT ? 4 : 2];     // Q' at the same place; without the lo half, row tiles 2 i and 2 i + 1 in q[i]
     u16x8 kh[2], kl[2];   // Kt [16 wave + m][32 s + 8 grp + j] (hi / lo)
     float glast;          // G of the chunk's last token
     float2 u;             // U[2 p + e][n0 + col], e < 2
@@ -580,7 +590,9 @@ __device__ __forceinline__ Split4 frag4(const u16x8 v) {
     return r;
 }
 
-template <int DK, int DV>
+// QSPLIT: Q' as bf16 hi and lo (the recurrence-only op, whose fp32 output is held to 1e-3), or hi alone (the
+// layer, whose output is bf16 after the gated norm; Q' does not enter the state)
+template <int DK, int DV, bool QSPLIT>
 __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs ws) {
     static_assert(DK == 128 && DV == 128, "chunked path is specialised for 128-wide heads");
     constexpr int NWV = 8, RS = CK + 4;
@@ -610,13 +622,14 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
     // One chunk's operands, loaded in four parts (W; Q'; keys and G; U and o).  A step issues the parts of the
     // chunk two ahead at four points of its own work, so the address units stream them while it computes
     // rather than stalling every wave on a burst of loads between steps.
-    auto load_part = [&](int c, StateOps& op, auto part) {
+    auto load_part = [&](int c, StateOps<QSPLIT>& op, auto part) {
         constexpr int P = decltype(part)::value;
         const size_t hc = ((size_t)b * Hv + h) * ws.NC + c;
         if constexpr (P == 0 || P == 1) {
             const u16* src = (P == 0 ? ws.Wf : ws.Qf) + hc * CK * DK * 2 + ((size_t)wave * 64 + lane) * 8;
+            constexpr int NL = P == 0 || QSPLIT ? 4 : 2;
 #pragma unroll
-            for (int rt = 0; rt < 4; ++rt) {
+            for (int rt = 0; rt < NL; ++rt) {
                 const u16x8 v = *reinterpret_cast<const u16x8*>(src + (size_t)rt * 8 * 64 * 8);
                 if constexpr (P == 0) op.w[rt] = v;
                 else op.q[rt] = v;
@@ -642,14 +655,14 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
     using P1 = std::integral_constant<int, 1>;
     using P2 = std::integral_constant<int, 2>;
     using P3 = std::integral_constant<int, 3>;
-    auto load_ops = [&](int c, StateOps& op) {
+    auto load_ops = [&](int c, StateOps<QSPLIT>& op) {
         load_part(c, op, P0{});
         load_part(c, op, P1{});
         load_part(c, op, P2{});
         load_part(c, op, P3{});
     };
     // part P of the loads into `nxt` (when LD), fenced so that the scheduler keeps it at this point
-    auto issue = [&](int cn, StateOps& nxt, auto ld, auto part) {
+    auto issue = [&](int cn, StateOps<QSPLIT>& nxt, auto ld, auto part) {
         if constexpr (decltype(ld)::value) {
             __builtin_amdgcn_sched_barrier(0);
             load_part(cn, nxt, part);
@@ -659,7 +672,7 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
 
     // FULL: the chunk has CK tokens (no per-token bounds test)
     // LD: load chunk cn into nxt along the way
-    auto step = [&](int c, const StateOps& cur, auto full, int cn, StateOps& nxt, auto ld) {
+    auto step = [&](int c, const StateOps<QSPLIT>& cur, auto full, int cn, StateOps<QSPLIT>& nxt, auto ld) {
         constexpr bool FULL = decltype(full)::value;
         const int t0 = c * CK, len = FULL ? CK : min(CK, T - t0);
         const size_t row0 = (size_t)b * T + t0;
@@ -671,7 +684,15 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
         for (int rt = 0; rt < 4; ++rt) {
             const f32x4 z = {0.f, 0.f, 0.f, 0.f};
             const f32x4 pw = mfma3k16(frag4(cur.w[rt]), Sb, z);
-            const f32x4 pq = mfma3k16(frag4(cur.q[rt]), Sb, z);
+            f32x4 pq;
+            if constexpr (QSPLIT) {
+                pq = mfma3k16(frag4(cur.q[rt]), Sb, z);
+            } else {
+                const u16x8 v = cur.q[rt >> 1];
+                const s16x4 qa = __builtin_bit_cast(s16x4, (rt & 1) ? __builtin_shufflevector(v, v, 4, 5, 6, 7)
+                                                                    : __builtin_shufflevector(v, v, 0, 1, 2, 3));
+                pq = mfma16k16(qa, Sb.h, mfma16k16(qa, Sb.l, z));
+            }
             *reinterpret_cast<f32x4*>(&red[wave][0][m][16 * rt + 4 * grp]) = pw;
             *reinterpret_cast<f32x4*>(&red[wave][1][m][16 * rt + 4 * grp]) = pq;
         }
@@ -725,7 +746,7 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
     using Yes = std::integral_constant<bool, true>;
     using No = std::integral_constant<bool, false>;
     const int NCF = T / CK;  // full chunks
-    StateOps A, B, C;
+    StateOps<QSPLIT> A, B, C;
     load_ops(0, A);
     load_ops(min(1, NC - 1), B);
     int c = 0;
@@ -783,7 +804,7 @@ hipError_t launch_delta_chunked(const DeltaArgs& a, int dk, int dv, void* worksp
                        FrontArgs{});
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((chunk_state_kernel<128, 128>), dim3(a.Hv * (128 / 16), a.B), dim3(512), 0, stream, a, ws);
+    hipLaunchKernelGGL((chunk_state_kernel<128, 128, true>), dim3(a.Hv * (128 / 16), a.B), dim3(512), 0, stream, a, ws);
     return hipGetLastError();
 }
 
@@ -804,7 +825,8 @@ hipError_t launch_front_chunked(const FrontArgs& f, float* conv_state, int* conv
     e = launch_conv_commit(f.P, f.NP, f.B, f.T, f.slot_ids, f.max_slots, f.nk, f.nv, f.dk, f.dv, conv_state,
                            conv_pos, stream);
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((chunk_state_kernel<128, 128>), dim3(a.Hv * (128 / 16), a.B), dim3(512), 0, stream, a, ws);
+    hipLaunchKernelGGL((chunk_state_kernel<128, 128, false>), dim3(a.Hv * (128 / 16), a.B), dim3(512), 0, stream, a,
+                       ws);
     return hipGetLastError();
 }
 
