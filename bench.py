@@ -27,18 +27,21 @@ HBM_PEAK = 8.0e12        # B/s, MI355X HBM3E
 BF16_PEAK = 2.5e15       # FLOP/s, MI355X dense bf16 MFMA
 
 
-def decode_bytes(d, B, fp8=False, fp4=False):
+def decode_bytes(d, B, weights="bf16"):
     """Algorithmic HBM bytes of one decode layer step: weights once plus per-sequence state and I/O.
     W = bf16 projections (qkv, z, a, b, out) + bf16 conv taps (fp8: qkv, z and out as 1-byte codes plus an
-    fp32 scale per row; fp4: the same as half-byte codes plus a 1-byte scale per 32; a and b bf16); s = fp32
-    state read + write, fp32 conv history (3 reads + 1 write per channel), bf16 x in and out."""
+    fp32 scale per row; mxfp4: the same as half-byte codes plus a 1-byte scale per 32; mxint8: 1-byte codes
+    plus a 1-byte scale per 32; a and b bf16); s = fp32 state read + write, fp32 conv history (3 reads + 1 write
+    per channel), bf16 x in and out."""
     H, nk, nv, dk, dv = d["hidden"], d["num_k_heads"], d["num_v_heads"], d["head_k_dim"], d["head_v_dim"]
     C, Vd = 2 * nk * dk + nv * dv, nv * dv
     q = C * H + Vd * H + H * Vd  # quantized weights
-    if fp8:
+    if weights == "fp8":
         W = q + 4 * (C + Vd + H) + 2 * 2 * nv * H + 2 * C * 4
-    elif fp4:
+    elif weights == "mxfp4":
         W = q // 2 + q // 32 + 2 * 2 * nv * H + 2 * C * 4
+    elif weights == "mxint8":
+        W = q + q // 32 + 2 * 2 * nv * H + 2 * C * 4
     else:
         W = 2 * (C * H + Vd * H + 2 * nv * H + H * Vd) + 2 * C * 4
     s = nv * dk * dv * 4 * 2 + C * 4 * 4 + 2 * H * 2
@@ -445,7 +448,7 @@ def small_batch_decode(shape, B, copies=8, steps=400, warmup=40, weight_dtype="b
         graphs[i % copies].replay()
     torch.cuda.synchronize()
     us = (time.perf_counter() - t0) / steps * 1e6
-    W, s = decode_bytes(d, B, fp8=weight_dtype == "fp8", fp4=weight_dtype == "mxfp4")
+    W, s = decode_bytes(d, B, weight_dtype)
     out = {"shape": shape, "batch": B, "weights": weight_dtype, "us_per_step": us, "tok_per_s": B / (us * 1e-6),
            "hbm_frac": (W + B * s) / (us * 1e-6) / HBM_PEAK, "mode": "HIP graph per step"}
     for lay in layers:
@@ -640,68 +643,49 @@ def main():
         lay.close()
     del layers[1:]
 
-    # the same decode step on E4M3 weights (q|k|v|z and out_proj one byte per weight, per-row scales)
-    fp8 = None
+    # the same decode step on low-precision weights: E4M3 (one byte per weight, per-row scales), MXFP4 (half a
+    # byte, a scale per 32) and MXINT8 (one byte, a scale per 32: the bfloat8_b counterpart)
+    lowp = {}
     if not args.no_fp8:
-        print(f"[bench] FP8-weight decode, {L} copies", file=sys.stderr, flush=True)
-        lays8 = []
-        for i in range(L):
-            lay = Qwen35GatedDeltaNetHIP(copy_weights(i), dims=d, batch=B, max_tokens=max(B, 64), weight_dtype="fp8")
-            lay.set_state(rec=torch.randn(B, d["num_v_heads"], 128, 128, device=dev) * 0.01)
-            lays8.append(lay)
-        wall8, st8 = eager_decode(lays8, xs, args.steps, args.warmup)
-        W8, s8 = decode_bytes(d, B, fp8=True)
-        b8 = W8 + B * s8
-        fp8 = {"ms_per_step": wall8, "tok_per_s": B / (wall8 / 1e3), "bytes_per_step": b8,
-               "frac": b8 / (wall8 / 1e3) / HBM_PEAK, "event_step_us": st8["total"] * 1e3,
-               "stage_us": {k: v * 1e3 for k, v in st8.items()},
-               "weights": "E4M3, one fp32 scale per row (a|b rows bf16)"}
+        for wd, desc in (("fp8", "E4M3, one fp32 scale per row (a|b rows bf16)"),
+                         ("mxfp4", "MXFP4 (E2M1, one E8M0 scale per 32; a|b rows bf16)"),
+                         ("mxint8", "MXINT8 (int8 codes, one E8M0 scale per 32; a|b rows bf16)")):
+            print(f"[bench] {wd}-weight decode, {L} copies", file=sys.stderr, flush=True)
+            lays = []
+            for i in range(L):
+                lay = Qwen35GatedDeltaNetHIP(copy_weights(i), dims=d, batch=B, max_tokens=max(B, 64), weight_dtype=wd)
+                lay.set_state(rec=torch.randn(B, d["num_v_heads"], 128, 128, device=dev) * 0.01)
+                lays.append(lay)
+            wall, st = eager_decode(lays, xs, args.steps, args.warmup)
+            Wq, sq = decode_bytes(d, B, wd)
+            bq = Wq + B * sq
+            lowp[wd] = {"ms_per_step": wall, "tok_per_s": B / (wall / 1e3), "bytes_per_step": bq,
+                        "frac": bq / (wall / 1e3) / HBM_PEAK, "event_step_us": st["total"] * 1e3,
+                        "stage_us": {k: v * 1e3 for k, v in st.items()}, "weights": desc}
+            print(f"[bench] {wd} decode B={B}: {wall * 1e3:.1f} us/step wall, stages (us) "
+                  f"{ {k: round(v * 1e3, 1) for k, v in st.items()} }", file=sys.stderr, flush=True)
+            for lay in lays:
+                lay.close()
+            del lays
         # in_proj weight stream (q|k|v|z codes + scales + bf16 a|b rows) over the in_proj stage time
         H, nv = d["hidden"], d["num_v_heads"]
         n1 = 2 * d["num_k_heads"] * 128 + 2 * nv * 128
-        fp8["in_proj_GBps"] = (n1 * H + 4 * n1 + 2 * 2 * nv * H) / (st8["in_proj"] / 1e3) / 1e9
-        print(f"[bench] fp8 decode B={B}: {wall8 * 1e3:.1f} us/step wall, stages (us) "
-              f"{ {k: round(v * 1e3, 1) for k, v in st8.items()} }", file=sys.stderr, flush=True)
-        for lay in lays8:
-            lay.close()
-        del lays8
-
-    # the same decode step on MXFP4 weights (q|k|v|z and out_proj half a byte per weight, a scale per 32)
-    fp4 = None
-    if not args.no_fp8:
-        print(f"[bench] MXFP4-weight decode, {L} copies", file=sys.stderr, flush=True)
-        lays4 = []
-        for i in range(L):
-            lay = Qwen35GatedDeltaNetHIP(copy_weights(i), dims=d, batch=B, max_tokens=max(B, 64),
-                                         weight_dtype="mxfp4")
-            lay.set_state(rec=torch.randn(B, d["num_v_heads"], 128, 128, device=dev) * 0.01)
-            lays4.append(lay)
-        wall4, st4 = eager_decode(lays4, xs, args.steps, args.warmup)
-        W4, s4 = decode_bytes(d, B, fp4=True)
-        b4 = W4 + B * s4
-        fp4 = {"ms_per_step": wall4, "tok_per_s": B / (wall4 / 1e3), "bytes_per_step": b4,
-               "frac": b4 / (wall4 / 1e3) / HBM_PEAK, "event_step_us": st4["total"] * 1e3,
-               "stage_us": {k: v * 1e3 for k, v in st4.items()},
-               "weights": "MXFP4 (E2M1, one E8M0 scale per 32; a|b rows bf16)"}
-        print(f"[bench] mxfp4 decode B={B}: {wall4 * 1e3:.1f} us/step wall, stages (us) "
-              f"{ {k: round(v * 1e3, 1) for k, v in st4.items()} }", file=sys.stderr, flush=True)
-        for lay in lays4:
-            lay.close()
-        del lays4
+        lowp["fp8"]["in_proj_GBps"] = (n1 * H + 4 * n1 + 2 * 2 * nv * H) / (lowp["fp8"]["stage_us"]["in_proj"] / 1e6) / 1e9
 
     prefill = None
     prefill_lowp = None
     if not args.no_prefill:
         prefill = prefill_bench(w0, d, args.prefill_len, args.prefill_steps)
         if not args.no_fp8:
-            prefill_lowp = [prefill_bench(w0, d, args.prefill_len, args.prefill_steps, wd) for wd in ("fp8", "mxfp4")]
+            prefill_lowp = [prefill_bench(w0, d, args.prefill_len, args.prefill_steps, wd)
+                            for wd in ("fp8", "mxfp4", "mxint8")]
 
     # small-batch decode latency (the reference's headline configurations are batch 1)
     small = None
     if not args.no_small:
         small = [small_batch_decode("0.8b", 1), small_batch_decode("9b", 1), small_batch_decode("9b", 8)]
         if not args.no_fp8:
-            small += [small_batch_decode("9b", 1, weight_dtype="fp8"), small_batch_decode("9b", 1, weight_dtype="mxfp4")]
+            small += [small_batch_decode("9b", 1, weight_dtype=wd) for wd in ("fp8", "mxfp4", "mxint8")]
         for r in small:
             print(f"[bench] decode {r['shape']} B={r['batch']} {r['weights']}: {r['us_per_step']:.1f} us/step (graph), "
                   f"{r['hbm_frac'] * 100:.0f}% of HBM roofline", file=sys.stderr, flush=True)
@@ -731,7 +715,8 @@ def main():
                    "hidden": d["hidden"], "num_k_heads": d["num_k_heads"], "num_v_heads": d["num_v_heads"],
                    "head_dim": 128, "batch": B, "state_dtype": "fp32", "weights": "bf16 N(0,0.02) seed 2"},
         "roofline": roofline, "layer_roofline": layer_roof, "stream_ceiling": ceiling, "prefill": prefill,
-        "prefill_lowp_weights": prefill_lowp, "stack": stack, "fp8_decode": fp8, "mxfp4_decode": fp4,
+        "prefill_lowp_weights": prefill_lowp, "stack": stack, "fp8_decode": lowp.get("fp8"),
+        "mxfp4_decode": lowp.get("mxfp4"), "mxint8_decode": lowp.get("mxint8"),
         "small_batch_decode": small,
         "cpu_baseline": cpu,
     }

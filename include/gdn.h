@@ -82,6 +82,11 @@ typedef enum gdn_weight_format {
                                 * one E8M0 scale per row and 32 columns (see gdn_quantize_mxfp4); the a|b
                                 * rows stay bf16.
                                 * Activations and accumulation are unchanged (bf16 x bf16 MFMA, fp32). */
+    GDN_WEIGHTS_MXINT8 = 3,    /* the counterpart of bfloat8_b: the same matrices as OCP MXINT8, int8 codes
+                                * worth code * 2^-6 with one E8M0 scale per row and 32 columns (see
+                                * gdn_quantize_mxint8): 7 significant bits under a shared exponent, as
+                                * bfloat8_b keeps; the a|b rows stay bf16.
+                                * Activations and accumulation are unchanged (bf16 x bf16 MFMA, fp32). */
 } gdn_weight_format;
 
 /* ---- layer handle: mirrors Qwen35GatedDeltaNetTT (9B/gdn_layer.py:54-292) ------------------------ */
@@ -272,6 +277,14 @@ int gdn_quantize_fp8(const void* w, int N, int K, void* q, float* scale, void* s
  * round-to-nearest-even(w / X) on the E2M1 grid {0, 0.5, 1, 1.5, 2, 3, 4, 6}, saturating at +-6.  The
  * dequantized value is decode(code) * 2^(scale code - 127). */
 int gdn_quantize_mxfp4(const void* w, int N, int K, void* q, void* scale, void* stream);
+
+/* The MXINT8 weight quantizer of GDN_WEIGHTS_MXINT8 (the reference's conversion to bfloat8_b, ttnn.from_torch(...,
+ * dtype=weight_dtype) at 9B/gdn_layer.py:115-120 and 0.8B/gdn_l1.py:79-80, re-specified for OCP MXINT8): w bf16
+ * [N, K] (device, K % 32 == 0) -> q int8 [N, K] codes and scale uint8 [N, K / 32] E8M0 codes, block j of row n
+ * (columns 32 j .. 32 j + 31) scaled by X = 2^floor(log2 max |w|) (exponent clamped to [-127, 127], code =
+ * exponent + 127; 0 for an all-zero block) and each value coded as round-to-nearest-even(64 w / X) saturated
+ * to [-128, 127].  The dequantized value is code * 2^(scale code - 133). */
+int gdn_quantize_mxint8(const void* w, int N, int K, void* q, void* scale, void* stream);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* gdn_last_error(void);

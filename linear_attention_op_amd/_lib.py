@@ -23,13 +23,16 @@ GDN_ERR_OUT_OF_MEMORY = -6
 GDN_WEIGHTS_BF16 = 0
 GDN_WEIGHTS_FP8_E4M3 = 1
 GDN_WEIGHTS_MXFP4 = 2
+GDN_WEIGHTS_MXINT8 = 3
 WEIGHT_FORMATS = {"bf16": GDN_WEIGHTS_BF16, "bfloat16": GDN_WEIGHTS_BF16, "fp8": GDN_WEIGHTS_FP8_E4M3,
-                  "fp8_e4m3": GDN_WEIGHTS_FP8_E4M3, "mxfp4": GDN_WEIGHTS_MXFP4, "fp4": GDN_WEIGHTS_MXFP4}
-WEIGHT_NAMES = {GDN_WEIGHTS_BF16: "bf16", GDN_WEIGHTS_FP8_E4M3: "fp8", GDN_WEIGHTS_MXFP4: "mxfp4"}
+                  "fp8_e4m3": GDN_WEIGHTS_FP8_E4M3, "mxfp4": GDN_WEIGHTS_MXFP4, "fp4": GDN_WEIGHTS_MXFP4,
+                  "mxint8": GDN_WEIGHTS_MXINT8, "int8": GDN_WEIGHTS_MXINT8}
+WEIGHT_NAMES = {GDN_WEIGHTS_BF16: "bf16", GDN_WEIGHTS_FP8_E4M3: "fp8", GDN_WEIGHTS_MXFP4: "mxfp4",
+                GDN_WEIGHTS_MXINT8: "mxint8"}
 
 
 def weight_format(weight_dtype):
-    """gdn_weight_format of a weight_dtype name ("bf16", "fp8" or "mxfp4")."""
+    """gdn_weight_format of a weight_dtype name ("bf16", "fp8", "mxfp4" or "mxint8")."""
     try:
         return WEIGHT_FORMATS[str(weight_dtype).lower()]
     except KeyError:
@@ -101,6 +104,7 @@ SIGNATURES = {
     "gdn_linear_bf16": (_I, [_V, _V, _I, _I, _I, _V, _I, _V]),
     "gdn_quantize_fp8": (_I, [_V, _I, _I, _V, _V, _V]),
     "gdn_quantize_mxfp4": (_I, [_V, _I, _I, _V, _V, _V]),
+    "gdn_quantize_mxint8": (_I, [_V, _I, _I, _V, _V, _V]),
     "gdn_last_error": (ctypes.c_char_p, []),
     "gdn_version": (_I, []),
 }

@@ -69,6 +69,10 @@ struct gdn_layer {
     u8* s_in4 = nullptr;      // mxfp4: E8M0 scale codes of w_in4 (f4_scale_offset order)
     u8* w_out4 = nullptr;     // mxfp4: [H, Vd] W_F4 layout
     u8* s_out4 = nullptr;     // mxfp4: scale codes of w_out4
+    u8* w_in_i8 = nullptr;    // mxint8: [CD + Vd, H] rows q | k | v | z, int8 codes in W_I8 layout
+    u8* s_in_i8 = nullptr;    // mxint8: E8M0 scale codes of w_in_i8 (f4_scale_offset order)
+    u8* w_out_i8 = nullptr;   // mxint8: [H, Vd] W_I8 layout
+    u8* s_out_i8 = nullptr;   // mxint8: scale codes of w_out_i8
     float4* conv_w = nullptr; // [CD] taps
     float* neg_A = nullptr;   // [nv]
     float* dt_bias = nullptr; // [nv]
@@ -160,6 +164,7 @@ hipError_t run_delta(gdn_layer* L, const gdn::DeltaArgs& r, hipStream_t st) {
 
 bool fp8(const gdn_layer* L) { return L->wfmt == GDN_WEIGHTS_FP8_E4M3; }
 bool fp4(const gdn_layer* L) { return L->wfmt == GDN_WEIGHTS_MXFP4; }
+bool int8w(const gdn_layer* L) { return L->wfmt == GDN_WEIGHTS_MXINT8; }
 // the q | k | v | z rows of in_proj, and out_proj, as stored: (weights, layout, scales)
 struct QW {
     const void* w;
@@ -169,11 +174,13 @@ struct QW {
 QW w_in_q(const gdn_layer* L) {
     if (fp8(L)) return {L->w_in8, gdn::W_F8, L->s_in};
     if (fp4(L)) return {L->w_in4, gdn::W_F4, reinterpret_cast<const float*>(L->s_in4)};
+    if (int8w(L)) return {L->w_in_i8, gdn::W_I8, reinterpret_cast<const float*>(L->s_in_i8)};
     return {L->w_in, gdn::W_FRAG, nullptr};
 }
 QW w_out_q(const gdn_layer* L) {
     if (fp8(L)) return {L->w_out8, gdn::W_F8, L->s_out};
     if (fp4(L)) return {L->w_out4, gdn::W_F4, reinterpret_cast<const float*>(L->s_out4)};
+    if (int8w(L)) return {L->w_out_i8, gdn::W_I8, reinterpret_cast<const float*>(L->s_out_i8)};
     return {L->w_out, gdn::W_FRAG, nullptr};
 }
 
@@ -359,7 +366,8 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
     *out = nullptr;
     int rc = check_dims(dims);
     if (rc) return rc;
-    if (wfmt != GDN_WEIGHTS_BF16 && wfmt != GDN_WEIGHTS_FP8_E4M3 && wfmt != GDN_WEIGHTS_MXFP4)
+    if (wfmt != GDN_WEIGHTS_BF16 && wfmt != GDN_WEIGHTS_FP8_E4M3 && wfmt != GDN_WEIGHTS_MXFP4 &&
+        wfmt != GDN_WEIGHTS_MXINT8)
         return fail(GDN_ERR_INVALID_ARG, "unknown weight format %d", wfmt);
     if (!w || !w->in_proj_qkv || !w->in_proj_z || !w->in_proj_a || !w->in_proj_b || !w->conv1d || !w->A_log ||
         !w->dt_bias || !w->norm_weight || !w->out_proj)
@@ -394,6 +402,13 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
         take(L->alloc(&L->w_ab, gdn::frag_elems(2 * nv, H)));
         take(L->alloc(&L->w_out4, gdn::frag_elems(H, L->Vd) / 2));
         take(L->alloc(&L->s_out4, gdn::frag_elems(H, L->Vd) / 32));
+    } else if (wfmt == GDN_WEIGHTS_MXINT8) {
+        // codes: a byte per weight; scales: a byte per 32 (rows padded to 16)
+        take(L->alloc(&L->w_in_i8, gdn::frag_elems(N1, H)));
+        take(L->alloc(&L->s_in_i8, gdn::frag_elems(N1, H) / 32));
+        take(L->alloc(&L->w_ab, gdn::frag_elems(2 * nv, H)));
+        take(L->alloc(&L->w_out_i8, gdn::frag_elems(H, L->Vd)));
+        take(L->alloc(&L->s_out_i8, gdn::frag_elems(H, L->Vd) / 32));
     } else {
         take(L->alloc(&L->w_in, gdn::frag_elems(L->NP, H)));
         take(L->alloc(&L->w_out, gdn::frag_elems(H, L->Vd)));
@@ -444,7 +459,8 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
 
     // fused in_proj rows: q | k | v (in_proj_qkv), z, a, b -- one weight stream per token.  The HF
     // row-major weights are staged in a temporary device buffer and re-laid out into fragment blocks
-    // (FP8 / MXFP4: the q | k | v | z rows and out_proj quantized to E4M3 with per-row scales or to MXFP4, as
+    // (FP8 / MXFP4 / MXINT8: the q | k | v | z rows and out_proj quantized to E4M3 with per-row scales, to MXFP4
+    // or to MXINT8, as
     // the reference converts w_in and w_out to its weight_dtype and keeps w_ab bf16, 9B/gdn_layer.py:115-120).
     const size_t row = (size_t)H * sizeof(u16);
     u16* stage = nullptr;
@@ -461,6 +477,9 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
         } else if (wfmt == GDN_WEIGHTS_MXFP4) {
             e = gdn::launch_quantize_mxfp4(stage, N1, H, L->w_in4, L->s_in4, 1, nullptr);
             if (e == hipSuccess) e = gdn::launch_frag_tile(stage + (size_t)N1 * H, 2 * nv, H, L->w_ab, nullptr);
+        } else if (wfmt == GDN_WEIGHTS_MXINT8) {
+            e = gdn::launch_quantize_mxint8(stage, N1, H, L->w_in_i8, L->s_in_i8, 1, nullptr);
+            if (e == hipSuccess) e = gdn::launch_frag_tile(stage + (size_t)N1 * H, 2 * nv, H, L->w_ab, nullptr);
         } else {
             e = gdn::launch_frag_tile(stage, L->NP, H, L->w_in, nullptr);
         }
@@ -473,6 +492,8 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
             e = gdn::launch_quantize_e4m3(stage, H, L->Vd, L->w_out8, L->s_out, 1, nullptr);
         else if (wfmt == GDN_WEIGHTS_MXFP4)
             e = gdn::launch_quantize_mxfp4(stage, H, L->Vd, L->w_out4, L->s_out4, 1, nullptr);
+        else if (wfmt == GDN_WEIGHTS_MXINT8)
+            e = gdn::launch_quantize_mxint8(stage, H, L->Vd, L->w_out_i8, L->s_out_i8, 1, nullptr);
         else
             e = gdn::launch_frag_tile(stage, H, L->Vd, L->w_out, nullptr);
     }
@@ -776,6 +797,14 @@ int gdn_quantize_mxfp4(const void* w, int N, int K, void* q, void* scale, void* 
     if (N <= 0 || K <= 0) return fail(GDN_ERR_SHAPE, "N=%d K=%d", N, K);
     if (K % 32) return fail(GDN_ERR_UNSUPPORTED, "K=%d is not a multiple of 32", K);
     HIP_OK(gdn::launch_quantize_mxfp4(w, N, K, (u8*)q, (u8*)scale, 0, as_stream(stream)));
+    return GDN_OK;
+}
+
+int gdn_quantize_mxint8(const void* w, int N, int K, void* q, void* scale, void* stream) {
+    if (!w || !q || !scale) return fail(GDN_ERR_INVALID_ARG, "gdn_quantize_mxint8: NULL argument");
+    if (N <= 0 || K <= 0) return fail(GDN_ERR_SHAPE, "N=%d K=%d", N, K);
+    if (K % 32) return fail(GDN_ERR_UNSUPPORTED, "K=%d is not a multiple of 32", K);
+    HIP_OK(gdn::launch_quantize_mxint8(w, N, K, (u8*)q, (u8*)scale, 0, as_stream(stream)));
     return GDN_OK;
 }
 

@@ -112,16 +112,19 @@ __host__ __device__ __forceinline__ uint32_t e2m1_code(float v) {
                      : a <= 2.5f ? 4u : a < 3.5f ? 5u : a <= 5.0f ? 6u : 7u;
     return (signbit(v) ? 8u : 0u) | c;
 }
-// E8M0 exponent byte of the block scale 2^(floor(log2 amax) - 2), clamped to [-127, 127]; 0 for amax 0.
+// E8M0 exponent byte of the block scale 2^(floor(log2 amax) - EMAX), clamped to [-127, 127]; 0 for amax 0.
+// EMAX is the exponent of the element format's largest power of two: 2 for E2M1, 0 for MXINT8.
+template <int EMAX = 2>
 __host__ __device__ __forceinline__ uint32_t mx_scale_code(float amax) {
     if (!(amax > 0.f)) return 0u;
     union { float f; uint32_t u; } b{amax};
     int e = (int)((b.u >> 23) & 0xffu) - 127;  // floor(log2 amax) for a normal amax
     if (((b.u >> 23) & 0xffu) == 0u) e = -127;  // subnormal amax: below 2^-126, the clamp applies
-    int x = e - 2;
+    int x = e - EMAX;
     x = x < -127 ? -127 : (x > 127 ? 127 : x);
     return (uint32_t)(x + 127);
 }
+
 // The scale of an E8M0 byte as a float (2^-127 for code 0, a subnormal).
 __device__ __forceinline__ float e8m0_value(uint32_t e) { return __uint_as_float(e ? e << 23 : 0x00400000u); }
 // 8 E2M1 codes (4 bytes, two per byte, low nibble first, in k order) times `scale` -> 8 bf16, exact for
@@ -133,6 +136,34 @@ __device__ __forceinline__ bf16x8 e2m1x8_to_bf16(uint32_t q, float scale) {
     const bf16x2 p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, scale, 2);
     const bf16x2 p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(q, scale, 3);
     return bf16x8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+// ---- MXINT8 (OCP Microscaling: two's-complement int8 elements worth code * 2^-6, one E8M0 scale per 32) ---
+// The counterpart of bfloat8_b (7 significant bits under an exponent shared by a block).  Code of one value
+// already divided by its block scale: 64 v rounded to nearest, ties to even, saturated to [-128, 127].
+__host__ __device__ __forceinline__ int32_t i8_code(float v) {
+    const float c = rintf(v * 64.0f);
+    return (int32_t)(c < -128.f ? -128.f : (c > 127.f ? 127.f : c));
+}
+// The weight of a code step under scale byte e, 2^(e - 127) * 2^-6 = 2^(e - 133), as a float (a subnormal
+// for e < 7).
+__device__ __forceinline__ float i8_step(uint32_t e) {
+    return __uint_as_float(e >= 7u ? (e - 6u) << 23 : 1u << (e + 16u));
+}
+// 16 MXINT8 codes (bytes in k order: the 8 of k-step 0, then the 8 of k-step 1) -> 2 x 8 bf16, k-step h
+// times its step s_h.  Byte b + 128 goes through v_cvt_f32_ubyte and one fma: (b + 128) s - 128 s = b s,
+// exact (b s is a bf16 value for steps of at least 2^-126: scale bytes >= 7).
+__device__ __forceinline__ void i8x16_to_bf16(const u32x4 q, float s0, float s1, bf16x8& lo, bf16x8& hi) {
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const uint32_t u = q[i] ^ 0x80808080u;
+        const float s = i < 2 ? s0 : s1, o = -128.0f * s;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[4 * i + j] = fmaf((float)((u >> (8 * j)) & 0xffu), s, o);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) lo[j] = (__bf16)v[j], hi[j] = (__bf16)v[8 + j];
 }
 
 // Workgroup barrier for LDS traffic only: unlike __syncthreads() it does not wait for outstanding
@@ -157,7 +188,9 @@ enum OutKind { OUT_F32 = 0, OUT_BF16 = 1, OUT_F32_T = 2 };
 // Weight layouts: W_ROW = row-major bf16 [N, K]; W_FRAG = bf16 MFMA-fragment blocks; W_F8 = E4M3 fragment
 // blocks with one fp32 scale per row; W_F4 = MXFP4 fragment blocks with one E8M0 scale per row and 32
 // columns (see gdn_linear.hip).
-enum WLayout { W_ROW = 0, W_FRAG = 1, W_F8 = 2, W_F4 = 3 };
+// W_I8 = MXINT8 codes in the W_F8 block order with one E8M0 scale per row and 32 columns in the W_F4 scale order
+// (see gdn_linear.hip).
+enum WLayout { W_ROW = 0, W_FRAG = 1, W_F8 = 2, W_F4 = 3, W_I8 = 4 };
 
 // y[M, N] (row stride ldy) = x[M, K] . w[N, K]^T ; bf16 activations, fp32 accumulation; K % 128 == 0.
 // w in layout `wlayout` (W_F8: w = E4M3 codes, row n scaled by w_scale[n]; W_F4: w = E2M1 codes, w_scale
@@ -196,6 +229,10 @@ __host__ __device__ __forceinline__ size_t f8_offset(int n, int k, int K) {
 // K % 128 == 0) or row-major [N, K / 2] bytes (low nibble = even column), with their E8M0 scale codes in
 // the matching order (f4_scale_offset, or row-major [N, K / 32]).
 hipError_t launch_quantize_mxfp4(const void* w, int N, int K, u8* q, u8* scale, int to_frag, hipStream_t stream);
+// MXINT8 weights: int8 codes in W_I8 layout (to_frag != 0: the W_F8 block order, rows padded to 16 with zero codes
+// and scale code 0, K % 128 == 0) or row-major [N, K], with their E8M0 scale codes in f4_scale_offset order (or
+// row-major [N, K / 32]).
+hipError_t launch_quantize_mxint8(const void* w, int N, int K, u8* q, u8* scale, int to_frag, hipStream_t stream);
 // W_F4 layout: blocks of 16 rows x 128 columns (1 KB), lane l = 16 g + r of block holding the 32 codes
 // W[16 nt + r][128 kb + 32 h + 8 g + j] (h, j < 4, 8) in its 16 bytes at byte 4 h + j / 2, nibble j % 2 --
 // four consecutive MFMA A operands per 16-byte load.  Byte offset of (row n, column k):

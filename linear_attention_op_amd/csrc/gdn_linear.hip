@@ -119,6 +119,46 @@ __global__ __launch_bounds__(256) void quantize_mxfp4_kernel(const u16* __restri
     }
 }
 
+// MXINT8 quantizer: one workgroup per (padded) row, a thread per 32-column block: scale code 2^floor(log2 amax)
+// (the element format's largest power of two is 1), codes i8_code(w / 2^(code - 127)) (the division is exact).
+template <bool FRAG>
+__global__ __launch_bounds__(256) void quantize_mxint8_kernel(const u16* __restrict__ w, int N, int K,
+                                                              u8* __restrict__ q, u8* __restrict__ scale) {
+    const int n = blockIdx.x;
+    const bool real = n < N;
+    for (int kq = threadIdx.x; kq < (K >> 5); kq += 256) {
+        float v[32];
+        float m = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const u16x8 x = real ? *reinterpret_cast<const u16x8*>(w + (size_t)n * K + 32 * kq + 8 * i) : u16x8{};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) v[8 * i + j] = bf2f(x[j]), m = fmaxf(m, fabsf(v[8 * i + j]));
+        }
+        const uint32_t e = mx_scale_code<0>(m);
+        uint32_t wd[8];
+#pragma unroll
+        for (int g = 0; g < 8; ++g) {
+            wd[g] = 0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                wd[g] |= ((uint32_t)i8_code(ldexpf(v[4 * g + j], 127 - (int)e)) & 0xffu) << (8 * j);
+        }
+        if (FRAG) {
+            // the 8 codes of columns 32 kq + 8 g .. + 7 are 8 contiguous bytes of one lane of a W_F8-order block
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                *reinterpret_cast<uint2*>(q + f8_offset(n, 32 * kq + 8 * g, K)) = make_uint2(wd[2 * g], wd[2 * g + 1]);
+            scale[f4_scale_offset(n, kq, K)] = (u8)e;
+        } else {
+            u32x4* dst = reinterpret_cast<u32x4*>(q + (size_t)n * K + 32 * kq);
+            dst[0] = u32x4{wd[0], wd[1], wd[2], wd[3]};
+            dst[1] = u32x4{wd[4], wd[5], wd[6], wd[7]};
+            scale[(size_t)n * (K >> 5) + kq] = (u8)e;
+        }
+    }
+}
+
 // ------------------------------------------------------------------------------------------------
 // GEMV: M <= 16 MT
 // ------------------------------------------------------------------------------------------------
@@ -322,8 +362,10 @@ __device__ __forceinline__ void gemv_block_allw(const u16* __restrict__ x, const
 
 // The same on W_F8 weights: a k-step of the ring is a k-pair (64 columns), one 16-byte load per row
 // tile and two x fragments per row block; rows scaled by scale[n] at the end.  K % 64 == 0; the k range
-// is [kpb, kpb + kpn) in k-pairs.
-template <int NTS, int MT, int NW, int PD, int OUT, int XL>
+// is [kpb, kpb + kpn) in k-pairs.  On W_I8 (MXINT8) weights the same codes come with a 2-byte load of the
+// pair's two E8M0 scale bytes per row tile (`scale` is then the scale-code array in f4_scale_offset order),
+// applied as the codes are widened; K % 128 == 0.
+template <int NTS, int MT, int NW, int PD, int OUT, int XL, int WL = W_F8>
 __device__ __forceinline__ void gemv_block_f8(const u16* __restrict__ x, const u8* __restrict__ w,
                                               const float* __restrict__ scale, int M, int N, int K,
                                               void* __restrict__ y, int ldy, int n0, int kpb, int kpn, float* red) {
@@ -355,6 +397,12 @@ __device__ __forceinline__ void gemv_block_f8(const u16* __restrict__ x, const u
     constexpr size_t XSTEP = XL == W_FRAG ? 1024 : 64, XHALF = XL == W_FRAG ? 512 : 32;
 
     u32x4 wb[PD][NTS];
+    uint32_t ws[PD][NTS];  // W_I8: the k-pair's two scale bytes of this lane's row
+    const u8* s8 = reinterpret_cast<const u8*>(scale);
+    auto sload = [&](int t, int kp) -> uint32_t {
+        const int tile = min((n0 >> 4) + t, NT - 1);
+        return *reinterpret_cast<const u16*>(s8 + f4_scale_offset(16 * tile + r, 2 * kp, K));
+    };
     bf16x8 xb[PD][MT][2];
     const bf16x8 zero8 = {};
     auto xload = [&](int j, int s) {
@@ -369,7 +417,10 @@ __device__ __forceinline__ void gemv_block_f8(const u16* __restrict__ x, const u
     for (int j = 0; j < PD; ++j) {
         if (j < nsteps) {
 #pragma unroll
-            for (int t = 0; t < NTS; ++t) wb[j][t] = ldw8(wp[t] + j * 1024);
+            for (int t = 0; t < NTS; ++t) {
+                wb[j][t] = ldw8(wp[t] + j * 1024);
+                if constexpr (WL == W_I8) ws[j][t] = sload(t, kp0 + j);
+            }
             xload(j, j);
         }
     }
@@ -387,7 +438,10 @@ __device__ __forceinline__ void gemv_block_f8(const u16* __restrict__ x, const u
 #pragma unroll
                 for (int t = 0; t < NTS; ++t) {
                     bf16x8 a0, a1;
-                    e4m3x16_to_bf16(wb[j][t], a0, a1);
+                    if constexpr (WL == W_I8)
+                        i8x16_to_bf16(wb[j][t], i8_step(ws[j][t] & 0xffu), i8_step(ws[j][t] >> 8), a0, a1);
+                    else
+                        e4m3x16_to_bf16(wb[j][t], a0, a1);
 #pragma unroll
                     for (int mt = 0; mt < MT; ++mt) {
                         acc[t][mt] = mfma16(a0, xb[j][mt][0], acc[t][mt]);
@@ -396,13 +450,16 @@ __device__ __forceinline__ void gemv_block_f8(const u16* __restrict__ x, const u
                 }
                 if (s + PD < nsteps) {
 #pragma unroll
-                    for (int t = 0; t < NTS; ++t) wb[j][t] = ldw8(wp[t] + (size_t)(s + PD) * 1024);
+                    for (int t = 0; t < NTS; ++t) {
+                        wb[j][t] = ldw8(wp[t] + (size_t)(s + PD) * 1024);
+                        if constexpr (WL == W_I8) ws[j][t] = sload(t, kp0 + s + PD);
+                    }
                     xload(j, s + PD);
                 }
             }
         }
     }
-    gemv_finish<NTS, MT, NW, OUT>(acc, red, M, N, y, ldy, n0, scale);
+    gemv_finish<NTS, MT, NW, OUT>(acc, red, M, N, y, ldy, n0, WL == W_F8 ? scale : nullptr);
 }
 
 // The same on W_F4 weights: one 16-byte load per row tile covers a k-quad (4 k-steps, 128 columns) and its
@@ -504,8 +561,8 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x
     __shared__ float red[gemv_red_floats<NTS, MT, NW>()];
     if constexpr (SPW > 0)
         gemv_block_allw<MT, NW, SPW, 4, OUT, XL>(x, (const u16*)w, M, N, K, y, ldy, blockIdx.x * 16, red);
-    else if constexpr (WL == W_F8)
-        gemv_block_f8<NTS, MT, NW, PD, OUT, XL>(x, (const u8*)w, scale, M, N, K, y, ldy, blockIdx.x * NTS * 16, 0,
+    else if constexpr (WL == W_F8 || WL == W_I8)
+        gemv_block_f8<NTS, MT, NW, PD, OUT, XL, WL>(x, (const u8*)w, scale, M, N, K, y, ldy, blockIdx.x * NTS * 16, 0,
                                                 K >> 6, red);
     else if constexpr (WL == W_F4)
         gemv_block_f4<NTS, MT, NW, OUT, XL>(x, (const u8*)w, reinterpret_cast<const uint32_t*>(scale), M, N, K, y,
@@ -532,8 +589,8 @@ __global__ __launch_bounds__(NW * 64) void in_proj_decode_kernel(const u16* __re
     __shared__ float red[R1 > R2 ? R1 : R2];
     const int bid = blockIdx.x;
     if (bid < G) {
-        if constexpr (WL == W_F8)
-            gemv_block_f8<NTS, MT, NW, PD, OUT_F32, XL>(x, (const u8*)w, scale, M, N1, K, P, ldp, bid * NTS * 16, 0,
+        if constexpr (WL == W_F8 || WL == W_I8)
+            gemv_block_f8<NTS, MT, NW, PD, OUT_F32, XL, WL>(x, (const u8*)w, scale, M, N1, K, P, ldp, bid * NTS * 16, 0,
                                                        K >> 6, red);
         else if constexpr (WL == W_F4)
             gemv_block_f4<NTS, MT, NW, OUT_F32, XL>(x, (const u8*)w, reinterpret_cast<const uint32_t*>(scale), M, N1,
@@ -596,11 +653,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
 
     // global -> register staging: 1024 16-byte pieces per operand tile, 4 per thread (W_F8: 512 B pieces,
     // 2 per thread, each widened to two 16-byte bf16 pieces on the way to LDS)
-    constexpr int NB = WL == W_F8 || WL == W_F4 ? 2 : 4;
+    constexpr int NB = WL == W_F8 || WL == W_F4 || WL == W_I8 ? 2 : 4;
     const u16* w = (const u16*)wv;
     const u8* w8 = (const u8*)wv;
     u16x8 ra[4], rb[4];
     u32x4 rq[2];
+    uint32_t rs[2];  // W_I8: the k-tile's two scale bytes of a piece's row
     const u16* ag[4];
     const u16* bg[4];
     const u8* bq[2];
@@ -613,12 +671,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
         const int row = c >> 3, col = (c & 7) * 8;
         ag[j] = x + (size_t)min(m0 + row, M - 1) * K + col;
         soffa[j] = row * TLD + col;
-        if (WL == W_F8) {
+        if (WL == W_F8 || WL == W_I8) {
             // piece c (< 512) of the 8 W_F8 blocks (8 n-tiles x 1 k-pair): lane l of n-tile c / 64; its two
-            // 8-code halves are columns 8 g and 32 + 8 g of row 16 ntl + r
+            // 8-code halves are columns 8 g and 32 + 8 g of row 16 ntl + r (W_I8: and that row's scale words)
             if (j < NB) {
                 const int ntl = c >> 6, l = c & 63;
-                bq[j] = w8 + (size_t)min((n0 >> 4) + ntl, NT - 1) * (K >> 6) * 1024 + l * 16;
+                const size_t nt = (size_t)min((n0 >> 4) + ntl, NT - 1);
+                bq[j] = w8 + nt * (K >> 6) * 1024 + l * 16;
+                if (WL == W_I8) bs4[j] = reinterpret_cast<const uint32_t*>(scale) + nt * (K >> 7) * 16 + (l & 15);
                 soffb[2 * j] = (16 * ntl + (l & 15)) * TLD + 8 * (l >> 4);
                 soffb[2 * j + 1] = soffb[2 * j] + 32;
             }
@@ -647,9 +707,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
     // k advance per 64-wide step: row-major 64 elements, fragment layout 2 blocks, W_F8 one block (bytes)
     constexpr size_t BSTEP = WL == W_ROW ? TBK : 1024;
     auto bload = [&](int kt) {
-        if constexpr (WL == W_F8) {
+        if constexpr (WL == W_F8 || WL == W_I8) {
 #pragma unroll
-            for (int j = 0; j < NB; ++j) rq[j] = *reinterpret_cast<const u32x4*>(bq[j] + (size_t)kt * BSTEP);
+            for (int j = 0; j < NB; ++j) {
+                rq[j] = *reinterpret_cast<const u32x4*>(bq[j] + (size_t)kt * BSTEP);
+                if constexpr (WL == W_I8) rs[j] = bs4[j][(size_t)(kt >> 1) * 16] >> (16 * (kt & 1));
+            }
         } else if constexpr (WL == W_F4) {
             // codes, and the scale word shifted so that its bytes 0, 1 belong to this k-tile's k-steps
 #pragma unroll
@@ -663,11 +726,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(const u16* __restrict__ x, co
         }
     };
     auto bstore = [&](int buf) {
-        if constexpr (WL == W_F8) {
+        if constexpr (WL == W_F8 || WL == W_I8) {
 #pragma unroll
             for (int j = 0; j < NB; ++j) {
                 bf16x8 lo, hi;
-                e4m3x16_to_bf16(rq[j], lo, hi);
+                if constexpr (WL == W_I8)
+                    i8x16_to_bf16(rq[j], i8_step(rs[j] & 0xffu), i8_step((rs[j] >> 8) & 0xffu), lo, hi);
+                else
+                    e4m3x16_to_bf16(rq[j], lo, hi);
                 *reinterpret_cast<bf16x8*>(&Bs[buf][soffb[2 * j]]) = lo;
                 *reinterpret_cast<bf16x8*>(&Bs[buf][soffb[2 * j + 1]]) = hi;
             }
@@ -782,7 +848,7 @@ __global__ __launch_bounds__(512, 1) void gemm256_kernel(const u16* __restrict__
 
     // staging: 4 A and 4 B pieces of 16 bytes per thread and k-tile (W_F8: 2 B pieces of 16 codes, each
     // widened to two bf16 pieces on the way to LDS)
-    constexpr int NB = WL == W_F8 || WL == W_F4 ? 2 : 4;
+    constexpr int NB = WL == W_F8 || WL == W_F4 || WL == W_I8 ? 2 : 4;
     const u16* w = (const u16*)wv;
     const u8* w8 = (const u8*)wv;
     const u16* ag[4];
@@ -796,10 +862,12 @@ __global__ __launch_bounds__(512, 1) void gemm256_kernel(const u16* __restrict__
         const int row = c >> 3, ch = c & 7;
         ag[j] = x + (size_t)min(m0 + row, M - 1) * K + ch * 8;
         sa[j] = lds_off(row, ch);
-        if (WL == W_F8) {  // piece c (< 1024) of the 16 W_F8 blocks (16 n-tiles x 1 k-pair) of the tile
+        if (WL == W_F8 || WL == W_I8) {  // piece c (< 1024) of the 16 W_F8 blocks (16 n-tiles x 1 k-pair)
             if (j < NB) {
                 const int ntl = c >> 6, l = c & 63;
-                bq[j] = w8 + (size_t)min((n0 >> 4) + ntl, NT - 1) * (K >> 6) * 1024 + l * 16;
+                const size_t nt = (size_t)min((n0 >> 4) + ntl, NT - 1);
+                bq[j] = w8 + nt * (K >> 6) * 1024 + l * 16;
+                if (WL == W_I8) bs4[j] = reinterpret_cast<const uint32_t*>(scale) + nt * (K >> 7) * 16 + (l & 15);
                 sb[2 * j] = lds_off(16 * ntl + (l & 15), l >> 4);
                 sb[2 * j + 1] = lds_off(16 * ntl + (l & 15), 4 + (l >> 4));
             }
@@ -834,8 +902,10 @@ __global__ __launch_bounds__(512, 1) void gemm256_kernel(const u16* __restrict__
         for (int j = 0; j < 4; ++j) ra[j] = *reinterpret_cast<const u16x8*>(ag[j] + (size_t)k * LBK);
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            if constexpr (WL == W_F8) {
+            if constexpr (WL == W_F8 || WL == W_I8) {
                 rb[j] = __builtin_bit_cast(u16x8, *reinterpret_cast<const u32x4*>(bq[j] + (size_t)k * BSTEP));
+                // W_I8: the piece's two scale bytes for this k-tile ride in the unused third register
+                if constexpr (WL == W_I8) rb[2][j] = (u16)(bs4[j][(size_t)(k >> 1) * 16] >> (16 * (k & 1)));
             } else if constexpr (WL == W_F4) {
                 // codes, and the scale word shifted so that its bytes 0, 1 belong to this k-tile's k-steps
                 const uint2 c = *reinterpret_cast<const uint2*>(bq[j] + (size_t)(k >> 1) * 1024 + (k & 1) * 8);
@@ -849,9 +919,13 @@ __global__ __launch_bounds__(512, 1) void gemm256_kernel(const u16* __restrict__
         for (int j = 0; j < 4; ++j) *reinterpret_cast<u16x8*>(&As[buf][sa[j]]) = ra[j];
 #pragma unroll
         for (int j = 0; j < NB; ++j) {
-            if constexpr (WL == W_F8) {
+            if constexpr (WL == W_F8 || WL == W_I8) {
                 bf16x8 lo, hi;
-                e4m3x16_to_bf16(__builtin_bit_cast(u32x4, rb[j]), lo, hi);
+                if constexpr (WL == W_I8)
+                    i8x16_to_bf16(__builtin_bit_cast(u32x4, rb[j]), i8_step(rb[2][j] & 0xffu), i8_step(rb[2][j] >> 8),
+                                  lo, hi);
+                else
+                    e4m3x16_to_bf16(__builtin_bit_cast(u32x4, rb[j]), lo, hi);
                 *reinterpret_cast<bf16x8*>(&Bs[buf][sb[2 * j]]) = lo;
                 *reinterpret_cast<bf16x8*>(&Bs[buf][sb[2 * j + 1]]) = hi;
             } else if constexpr (WL == W_F4) {
@@ -966,7 +1040,7 @@ hipError_t gemv_allw(const LinArgs& a, hipStream_t stream) {
 
 template <int NTS, int MT, int NW, int WL, int XL>
 hipError_t gemv(const LinArgs& a, hipStream_t stream) {
-    constexpr int PD = WL == W_F8 ? 2 : 4;  // an E4M3 ring slot covers two k-steps
+    constexpr int PD = WL == W_F8 || WL == W_I8 ? 2 : 4;  // an E4M3 / MXINT8 ring slot covers two k-steps
     if constexpr (NTS == 1 && WL == W_FRAG) {
         // one weight tile per workgroup: every weight fragment of a wave in flight at once when its share is
         // 8 or 16 k-steps
@@ -1070,6 +1144,18 @@ hipError_t launch_quantize_mxfp4(const void* w, int N, int K, u8* q, u8* scale, 
     return hipGetLastError();
 }
 
+hipError_t launch_quantize_mxint8(const void* w, int N, int K, u8* q, u8* scale, int to_frag, hipStream_t stream) {
+    if (N <= 0 || K <= 0) return hipSuccess;
+    if (K % (to_frag ? 128 : 32)) return hipErrorInvalidValue;
+    const int rows = to_frag ? (N + 15) / 16 * 16 : N;
+    if (to_frag)
+        hipLaunchKernelGGL(quantize_mxint8_kernel<true>, dim3(rows), dim3(256), 0, stream, (const u16*)w, N, K, q, scale);
+    else
+        hipLaunchKernelGGL(quantize_mxint8_kernel<false>, dim3(rows), dim3(256), 0, stream, (const u16*)w, N, K, q,
+                           scale);
+    return hipGetLastError();
+}
+
 hipError_t launch_frag_tile(const void* w, int N, int K, void* wf, hipStream_t stream) {
     const size_t pieces = frag_elems(N, K) / 8;
     hipLaunchKernelGGL(frag_tile_kernel, dim3((unsigned)((pieces + 255) / 256)), dim3(256), 0, stream, (const u16*)w,
@@ -1139,13 +1225,14 @@ hipError_t launch_in_proj_decode(const void* x, int xlayout, const void* w, int 
                                  int ab_splits, hipStream_t stream) {
     if (M <= 0) return hipSuccess;
     if (M > 64 || N1 % 16 || ab_splits <= 0 || K % 32) return hipErrorInvalidValue;
-    if (wlayout != W_FRAG && wlayout != W_F8 && wlayout != W_F4) return hipErrorInvalidValue;
+    if (wlayout != W_FRAG && wlayout != W_F8 && wlayout != W_F4 && wlayout != W_I8) return hipErrorInvalidValue;
     if (wlayout == W_F8 && (K % 64 || !w_scale)) return hipErrorInvalidValue;
-    if (wlayout == W_F4 && (K % 128 || !w_scale)) return hipErrorInvalidValue;
+    if ((wlayout == W_F4 || wlayout == W_I8) && (K % 128 || !w_scale)) return hipErrorInvalidValue;
     if (xlayout != W_FRAG && (xlayout != W_ROW || M > 16)) return hipErrorInvalidValue;
     const DecodeArgs a{(const u16*)x, w, w_scale, (const u16*)w2, M, N1, N2, K, 0, ab_splits, P, ldp, Pab};
     if (wlayout == W_F8) return in_proj_decode_wl<W_F8>(a, xlayout, stream);
     if (wlayout == W_F4) return in_proj_decode_wl<W_F4>(a, xlayout, stream);
+    if (wlayout == W_I8) return in_proj_decode_wl<W_I8>(a, xlayout, stream);
     return in_proj_decode_wl<W_FRAG>(a, xlayout, stream);
 }
 
@@ -1170,6 +1257,10 @@ hipError_t launch_linear(const void* x, int xlayout, const void* w, int wlayout,
     if (wlayout == W_F4) {
         if (K % 128 || !w_scale) return hipErrorInvalidValue;
         return linear_wl<W_F4>(a, xlayout, stream);
+    }
+    if (wlayout == W_I8) {
+        if (K % 128 || !w_scale) return hipErrorInvalidValue;
+        return linear_wl<W_I8>(a, xlayout, stream);
     }
     if (wlayout == W_FRAG) return linear_wl<W_FRAG>(a, xlayout, stream);
     return linear_wl<W_ROW>(a, xlayout, stream);

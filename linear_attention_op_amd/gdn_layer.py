@@ -98,9 +98,10 @@ class Qwen35GatedDeltaNetHIP:
     """One GDN layer.  `weights` is an HF Qwen3_5GatedDeltaNet or a dict with keys
     w_qkv [conv_dim, H], w_z [Vd, H], w_a, w_b [nv, H], conv_w [conv_dim, 4], A_log, dt_bias [nv],
     norm_w [dv], w_out [H, Vd] (projection weights are used as bf16, the rest as fp32).
-    `weight_dtype` ("bf16", "fp8" or "mxfp4") mirrors the reference's weight_dtype (9B/gdn_layer.py:55;
+    `weight_dtype` ("bf16", "fp8", "mxfp4" or "mxint8") mirrors the reference's weight_dtype (9B/gdn_layer.py:55;
     bfloat8_b / bfloat4_b, 0.8B/gdn_l1.py:79-80): "fp8" keeps the q|k|v|z and out projections as E4M3 with
-    per-row scales (see quantize_fp8), "mxfp4" as MXFP4 with a scale per 32 (see quantize_mxfp4); a|b stay bf16."""
+    per-row scales (see quantize_fp8), "mxfp4" as MXFP4 with a scale per 32 (see quantize_mxfp4), "mxint8" as
+    MXINT8 with a scale per 32 (see quantize_mxint8; the bfloat8_b counterpart); a|b stay bf16."""
 
     def __init__(self, weights, dims=None, batch=1, max_slots=None, max_tokens=16384, device="cuda", _handle=None,
                  weight_dtype="bf16"):
@@ -300,4 +301,16 @@ def quantize_mxfp4(w):
     q = torch.empty((N, K // 2), device=w.device, dtype=torch.uint8)
     s = torch.empty((N, K // 32), device=w.device, dtype=torch.uint8)
     _lib.check(_lib.lib().gdn_quantize_mxfp4(_ptr(w), N, K, _ptr(q), _ptr(s), _stream()))
+    return q, s
+
+
+def quantize_mxint8(w):
+    """The library's MXINT8 weight quantizer (gdn_quantize_mxint8) on a CUDA matrix w [N, K] (K % 32 == 0): ->
+    (codes int8 [N, K]; scale codes uint8 [N, K / 32], E8M0).  Block j of row n dequantizes to
+    codes * 2^(scale[n, j] - 133)."""
+    w = w.to(torch.bfloat16).contiguous()
+    N, K = w.shape
+    q = torch.empty((N, K), device=w.device, dtype=torch.int8)
+    s = torch.empty((N, K // 32), device=w.device, dtype=torch.uint8)
+    _lib.check(_lib.lib().gdn_quantize_mxint8(_ptr(w), N, K, _ptr(q), _ptr(s), _stream()))
     return q, s

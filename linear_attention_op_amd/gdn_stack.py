@@ -20,7 +20,7 @@ from .gdn_layer import Qwen35GatedDeltaNetHIP, _ptr, _slots, _stream, cu_seqlens
 class Qwen35GDNStackHIP:
     """`layers`: HF Qwen3_5GatedDeltaNet modules or weight dicts (see Qwen35GatedDeltaNetHIP), one per layer.
     `norm_weights`: optional per-layer [H] weights of the RMSNorm after each layer (default 0, i.e. (1 + w) = 1).
-    `weight_dtype`: "bf16", "fp8" or "mxfp4" for every layer (wormhole_n150/qwen3.5_0.8B/gdn_l1.py:79-80)."""
+    `weight_dtype`: "bf16", "fp8", "mxfp4" or "mxint8" for every layer (wormhole_n150/qwen3.5_0.8B/gdn_l1.py:79-80)."""
 
     def __init__(self, layers, dims=None, batch=1, max_slots=None, max_tokens=None, inter_norm=False,
                  norm_weights=None, device="cuda", weight_dtype="bf16"):

@@ -72,6 +72,11 @@ def _declare(L):
     L.orc_mx_scale_code.argtypes = [ctypes.c_float]
     L.orc_mx_scale_code.restype = _I
     L.orc_quantize_mxfp4.argtypes = [_P, _I, _I, ctypes.c_void_p, ctypes.c_void_p]
+    L.orc_mx_scale_code_emax.argtypes = [ctypes.c_float, _I]
+    L.orc_mx_scale_code_emax.restype = _I
+    L.orc_mxint8_encode.argtypes = [ctypes.c_double]
+    L.orc_mxint8_encode.restype = _I
+    L.orc_quantize_mxint8.argtypes = [_P, _I, _I, ctypes.c_void_p, ctypes.c_void_p]
 
 
 def _f(a):
@@ -286,3 +291,32 @@ def dequantize_mxfp4(q, sc):
     """codes [N, K], scale codes [N, K / 32] -> float32 [N, K] = value(code) * 2^(scale code - 127)."""
     scale = np.ldexp(np.float32(1.0), np.asarray(sc, np.int32) - 127).astype(np.float32)
     return e2m1_table()[np.asarray(q)] * np.repeat(scale, 32, axis=1)
+
+
+# ---- low-precision weights (MXINT8: int8 codes worth code * 2^-6, one E8M0 scale per 32 along K) -------
+def mxint8_scale_code(amax):
+    """E8M0 exponent byte of the MXINT8 scale 2^floor(log2 amax) of a block with largest magnitude amax."""
+    return lib().orc_mx_scale_code_emax(float(amax), 0)
+
+
+def mxint8_encode(v):
+    """MXINT8 code of one value already divided by its block scale (nearest code / 64, ties to even, saturated)."""
+    return lib().orc_mxint8_encode(float(v))
+
+
+def quantize_mxint8(w):
+    """w [N, K] (K % 32 == 0) -> (codes int8 [N, K]; scale codes uint8 [N, K / 32])."""
+    w, pw = _f(w)
+    N, K = w.shape
+    if K % 32:
+        raise ValueError("K must be a multiple of 32")
+    q = np.empty((N, K), np.int8)
+    sc = np.empty((N, K // 32), np.uint8)
+    lib().orc_quantize_mxint8(pw, N, K, q.ctypes.data_as(ctypes.c_void_p), sc.ctypes.data_as(ctypes.c_void_p))
+    return q, sc
+
+
+def dequantize_mxint8(q, sc):
+    """codes [N, K], scale codes [N, K / 32] -> float32 [N, K] = code * 2^(scale code - 133)."""
+    step = np.ldexp(np.float64(1.0), np.asarray(sc, np.int32) - 133)
+    return (np.asarray(q, np.float64) * np.repeat(step, 32, axis=1)).astype(np.float32)

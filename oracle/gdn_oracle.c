@@ -692,3 +692,51 @@ EXPORT void orc_quantize_mxfp4(const float* w, int N, int K, uint8_t* q, uint8_t
             for (int j = 0; j < 32; ++j) q[(size_t)n * K + 32 * kb + j] = (uint8_t)orc_e2m1_encode((float)(b[j] / X));
         }
 }
+
+/* ---- low-precision weights: MXINT8 (int8 elements worth code * 2^-6, one E8M0 scale per 32 along K) ------
+ * The counterpart of the reference's ttnn.bfloat8_b (9B/gdn_layer.py:55,115-120; the default weight_dtype of
+ * the 0.8B stack, 0.8B/gdn_l1.py:153), a shared-exponent tile format that keeps 7 significant bits per value.
+ * The HIP path stores w_in (q|k|v|z rows) and w_out as OCP MXINT8 (OCP Microscaling Formats Specification
+ * v1.0, 2023): blocks of 32 consecutive values of a row share the scale X = 2^(floor(log2(amax)) - emax) with
+ * emax = 0 (the largest power of two of the element format, whose values are code * 2^-6 for two's-complement
+ * codes in [-128, 127]); X is stored as its E8M0 exponent byte (bias 127, exponent clamped to [-127, 127], code
+ * 0 for an all-zero block) and each value as the code nearest to w / X, ties to the even code, saturated to
+ * [-128, 127].  Dequantized weight = code * 2^-6 * X.  Restated from the specification: the exponent by frexp,
+ * the code by a nearest search over the candidate codes around 64 w / X with explicit tie-breaking. */
+EXPORT int orc_mx_scale_code_emax(float amax, int emax) {
+    if (!(amax > 0.f)) return 0;
+    int e2;
+    frexp((double)amax, &e2);   /* amax = f 2^e2, f in [0.5, 1): floor(log2 amax) = e2 - 1 */
+    int x = e2 - 1 - emax;
+    if (x < -127) x = -127;
+    if (x > 127) x = 127;
+    return x + 127;
+}
+
+EXPORT int orc_mxint8_encode(double v) {
+    /* v is already divided by the block scale; the element value of code c is c / 64 */
+    const double t = fmin(fmax(v * 64.0, -256.0), 256.0);  /* beyond the codes: saturates either way */
+    int lo = (int)floor(t) - 1, best = 0;
+    double dbest = INFINITY;
+    for (int c = lo; c <= lo + 3; ++c) {
+        const int cc = c < -128 ? -128 : (c > 127 ? 127 : c);
+        const double d = fabs(cc / 64.0 - v);
+        if (d < dbest || (d == dbest && (cc & 1) == 0 && (best & 1) != 0)) best = cc, dbest = d;
+    }
+    return best;
+}
+
+/* w [N, K] (K % 32 == 0) -> codes [N, K] (int8) and scale codes [N, K / 32] */
+EXPORT void orc_quantize_mxint8(const float* w, int N, int K, int8_t* q, uint8_t* sc) {
+#pragma omp parallel for schedule(static)
+    for (int n = 0; n < N; ++n)
+        for (int kb = 0; kb < K / 32; ++kb) {
+            const float* b = w + (size_t)n * K + 32 * kb;
+            float m = 0.f;
+            for (int j = 0; j < 32; ++j) m = fmaxf(m, fabsf(b[j]));
+            const int code = orc_mx_scale_code_emax(m, 0);
+            sc[(size_t)n * (K / 32) + kb] = (uint8_t)code;
+            const double X = ldexp(1.0, code - 127);
+            for (int j = 0; j < 32; ++j) q[(size_t)n * K + 32 * kb + j] = (int8_t)orc_mxint8_encode(b[j] / X);
+        }
+}
