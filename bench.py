@@ -674,8 +674,11 @@ def main():
 
     prefill = None
     prefill_lowp = None
+    prefill_4k = None
     if not args.no_prefill:
         prefill = prefill_bench(w0, d, args.prefill_len, args.prefill_steps)
+        # the other prefill length of the 9B prefill configuration (one sequence of 4096 tokens)
+        prefill_4k = prefill_bench(w0, d, 4096, 2 * args.prefill_steps)
         if not args.no_fp8:
             prefill_lowp = [prefill_bench(w0, d, args.prefill_len, args.prefill_steps, wd)
                             for wd in ("fp8", "mxfp4", "mxint8")]
@@ -715,6 +718,7 @@ def main():
                    "hidden": d["hidden"], "num_k_heads": d["num_k_heads"], "num_v_heads": d["num_v_heads"],
                    "head_dim": 128, "batch": B, "state_dtype": "fp32", "weights": "bf16 N(0,0.02) seed 2"},
         "roofline": roofline, "layer_roofline": layer_roof, "stream_ceiling": ceiling, "prefill": prefill,
+        "prefill_t4096": prefill_4k,
         "prefill_lowp_weights": prefill_lowp, "stack": stack, "fp8_decode": lowp.get("fp8"),
         "mxfp4_decode": lowp.get("mxfp4"), "mxint8_decode": lowp.get("mxint8"),
         "small_batch_decode": small,
