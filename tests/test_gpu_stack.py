@@ -7,7 +7,7 @@ own state" (0.8B/test_gdn_l1.py:55-69).  Here:
     a subset `layers=[i]` equals layer i alone;
   * a short decode through 0.8B stacks matches the CPU oracle chained the same way (bf16 activations
     between layers), output rel-L2 <= 1e-2 and states <= 1e-3 per step, in the reference's resident-layer
-    cases (2, 1, bf16), (3, 1 and 4, bfloat8_b -> E4M3), (6, 1, bfloat4_b -> MXFP4);
+    cases (2, 1, bf16), (3, 1 and 4, bfloat8_b -> MXINT8 and E4M3), (6, 1, bfloat4_b -> MXFP4);
   * the decoder RMSNorm between layers matches a float32 torch restatement on the CPU;
   * a decode step of the stack captured in a HIP graph replays bit-exactly;
   * a varlen launch mixing prefills (chunked path) and decode streams equals per-sequence launches up
@@ -67,26 +67,27 @@ def test_stack_equals_chained_layers():
 
 
 def _dequantized(w, weight_dtype):
-    """numpy weights as the stack stores them (the oracle's quantizer for fp8 / mxfp4)"""
+    """numpy weights as the stack stores them (the oracle's quantizer for fp8 / mxfp4 / mxint8)"""
     wn = syn.to_numpy(w)
     if weight_dtype != "bf16":
-        q, dq = ((oracle.quantize_e4m3, oracle.dequantize_e4m3) if weight_dtype == "fp8"
-                 else (oracle.quantize_mxfp4, oracle.dequantize_mxfp4))
+        q, dq = {"fp8": (oracle.quantize_e4m3, oracle.dequantize_e4m3),
+                 "mxfp4": (oracle.quantize_mxfp4, oracle.dequantize_mxfp4),
+                 "mxint8": (oracle.quantize_mxint8, oracle.dequantize_mxint8)}[weight_dtype]
         for k in ("w_qkv", "w_z", "w_out"):
             wn[k] = dq(*q(wn[k]))
     return wn
 
 
 # the reference's resident-layer decode cases (0.8B/test_gdn_l1.py:88-92): (layers, B, dtype) with bfloat8_b
-# and bfloat4_b as E4M3 and MXFP4; compared, as there, against the truth run on the quantized weights.  Up to
+# as MXINT8 (and E4M3) and bfloat4_b as MXFP4; compared, as there, against the truth run on the quantized weights.  Up to
 # 3 layers the stack runs whole against an independent oracle chain.  Random GDN layers chained with no
 # residual or norm shrink the activations ~10-100x per layer (1e-20 by the sixth, where the l2norm's 1e-6
 # and fp32 underflow decide the result), so the 6-layer case runs the stack one layer at a time
 # (stack(x, layers=[i]), every layer on its own slots), puts the decoder RMSNorm between layers as the model
 # does (float32 on the CPU, bf16 at the boundary) and gives each oracle layer the bf16 input the GPU layer
 # saw: every layer within 1e-2, every state within 1e-3, every step.
-@pytest.mark.parametrize("n_layers, B, weight_dtype", [(2, 1, "bf16"), (2, 2, "bf16"), (3, 1, "fp8"), (3, 4, "fp8"),
-                                                       (6, 1, "mxfp4")])
+@pytest.mark.parametrize("n_layers, B, weight_dtype", [(2, 1, "bf16"), (2, 2, "bf16"), (3, 1, "mxint8"), (3, 4, "mxint8"),
+                                                       (3, 1, "fp8"), (3, 4, "fp8"), (6, 1, "mxfp4")])
 def test_stack_decode_against_oracle(n_layers, B, weight_dtype):
     print(f"stack decode vs oracle 0.8b: {n_layers} layers, B={B}, {weight_dtype}", flush=True)
     d = syn.SHAPES["0.8b"]
