@@ -245,6 +245,26 @@ def test_config_08b_decode_b32_256_steps():
     assert worst_state < STATE_TOL
 
 
+@pytest.mark.parametrize("B", [1, 3, 4, 8, 16])
+def test_08b_decode_batches_from_zero_state(B):
+    """The reference's one-layer decode grid (0.8B/test_gdn_l1.py:82-85): 0.8B shape, batch 1 / 3 / 4 / 8 / 16,
+    8 single-token steps from a zero state, every step against the oracle."""
+    print(f"0.8B decode B={B}, 8 steps", flush=True)
+    d = syn.SHAPES["0.8b"]
+    w, gen = syn.make_weights(d, seed=5)
+    wn = syn.to_numpy(w)
+    x, _ = syn.make_inputs(d, B, 8, gen)
+    layer = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B)
+    rec_o = np.zeros((B, d["num_v_heads"], d["head_k_dim"], d["head_v_dim"]), np.float32)
+    conv_o = np.zeros((B, syn.conv_dim(d), 3), np.float32)
+    xg = x.cuda()
+    for t in range(8):
+        out = layer(xg[:, t:t + 1])
+        want = oracle.layer_forward(odims(d), wn, x[:, t:t + 1].numpy(), rec_o, conv_o)
+        assert rel(out, want) < OUT_TOL, f"step {t}"
+        assert rel(layer.get_recurrent_state(), rec_o) < STATE_TOL, f"step {t}"
+
+
 @pytest.fixture(scope="module")
 def layer9b():
     d = syn.SHAPES["9b"]

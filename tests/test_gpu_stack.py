@@ -79,15 +79,16 @@ def _dequantized(w, weight_dtype):
 
 
 # the reference's resident-layer decode cases (0.8B/test_gdn_l1.py:88-92): (layers, B, dtype) with bfloat8_b
-# as MXINT8 (and E4M3) and bfloat4_b as MXFP4; compared, as there, against the truth run on the quantized weights.  Up to
+# as MXINT8 (and E4M3) and bfloat4_b as MXFP4, and its weights-in-DRAM comparison (0.8B/test_gdn_l1.py:95-100: 2
+# layers, B = 2, bf16 and bfloat8_b; this stack always streams its weights from HBM); compared, as there, against the truth run on the quantized weights.  Up to
 # 3 layers the stack runs whole against an independent oracle chain.  Random GDN layers chained with no
 # residual or norm shrink the activations ~10-100x per layer (1e-20 by the sixth, where the l2norm's 1e-6
 # and fp32 underflow decide the result), so the 6-layer case runs the stack one layer at a time
 # (stack(x, layers=[i]), every layer on its own slots), puts the decoder RMSNorm between layers as the model
 # does (float32 on the CPU, bf16 at the boundary) and gives each oracle layer the bf16 input the GPU layer
 # saw: every layer within 1e-2, every state within 1e-3, every step.
-@pytest.mark.parametrize("n_layers, B, weight_dtype", [(2, 1, "bf16"), (2, 2, "bf16"), (3, 1, "mxint8"), (3, 4, "mxint8"),
-                                                       (3, 1, "fp8"), (3, 4, "fp8"), (6, 1, "mxfp4")])
+@pytest.mark.parametrize("n_layers, B, weight_dtype", [(2, 1, "bf16"), (2, 2, "bf16"), (2, 2, "mxint8"), (3, 1, "mxint8"),
+                                                       (3, 4, "mxint8"), (3, 1, "fp8"), (3, 4, "fp8"), (6, 1, "mxfp4")])
 def test_stack_decode_against_oracle(n_layers, B, weight_dtype):
     print(f"stack decode vs oracle 0.8b: {n_layers} layers, B={B}, {weight_dtype}", flush=True)
     d = syn.SHAPES["0.8b"]
