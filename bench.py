@@ -24,6 +24,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "GDN-layer decode tok/s + prefill tok/s at 9B shape; % HBM / MFMA roofline"
 HBM_PEAK = 8.0e12        # B/s, MI355X HBM3E
+LAYER_OUT = "bf16"       # layer / stack output element type: bf16 activations, as in a bf16 model
 BF16_PEAK = 2.5e15       # FLOP/s, MI355X dense bf16 MFMA
 
 
@@ -209,7 +210,7 @@ def pmc_child(steps=4):
     del src, dst
     d = syn.SHAPES["9b"]
     w, _ = syn.make_weights(d, seed=2)
-    lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=64, max_tokens=64)
+    lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=64, max_tokens=64, out_dtype=LAYER_OUT)
     lay.set_state(rec=torch.randn(64, d["num_v_heads"], 128, 128, device=dev) * 0.01)
     x = torch.randn(64, 1, d["hidden"], device=dev).to(torch.bfloat16)
     for _ in range(steps):
@@ -241,7 +242,7 @@ def profile_child(which):
                 gg = torch.Generator(device=dev).manual_seed(200 + i)
                 wi = {k: (torch.randn(v.shape, generator=gg, device=dev) * v.float().std()).to(v.dtype)
                       if k.startswith("w_") or k == "conv_w" else v for k, v in ws.items()}
-                lay = Qwen35GatedDeltaNetHIP(wi, dims=ds, batch=B, max_tokens=64)
+                lay = Qwen35GatedDeltaNetHIP(wi, dims=ds, batch=B, max_tokens=64, out_dtype=LAYER_OUT)
                 lay.set_state(rec=torch.randn(B, ds["num_v_heads"], 128, 128, device=dev) * 0.01)
                 layers.append(lay)
             x = torch.randn(B, 1, ds["hidden"], device=dev).to(torch.bfloat16)
@@ -256,14 +257,14 @@ def profile_child(which):
             gg = torch.Generator(device=dev).manual_seed(100 + i)
             wi = w if i == 0 else {k: (torch.randn(v.shape, generator=gg, device=dev) * v.float().std()).to(v.dtype)
                                    if k.startswith("w_") or k == "conv_w" else v for k, v in w.items()}
-            lay = Qwen35GatedDeltaNetHIP(wi, dims=d, batch=64, max_tokens=64)
+            lay = Qwen35GatedDeltaNetHIP(wi, dims=d, batch=64, max_tokens=64, out_dtype=LAYER_OUT)
             lay.set_state(rec=torch.randn(64, d["num_v_heads"], 128, 128, device=dev) * 0.01)
             layers.append(lay)
         x = torch.randn(64, 1, d["hidden"], device=dev).to(torch.bfloat16)
         for i in range(15):
             layers[i % 4](x)
     else:
-        lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=1, max_tokens=16384)
+        lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=1, max_tokens=16384, out_dtype=LAYER_OUT)
         x = torch.randn(1, 16384, d["hidden"], device=dev).to(torch.bfloat16)
         for _ in range(4):
             lay.reset_state()
@@ -383,7 +384,7 @@ def prefill_bench(w, d, T, steps, weight_dtype="bf16"):
     from linear_attention_op_amd import Qwen35GatedDeltaNetHIP
 
     dev = torch.device("cuda", 0)
-    lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=1, max_tokens=T, weight_dtype=weight_dtype)
+    lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=1, max_tokens=T, weight_dtype=weight_dtype, out_dtype=LAYER_OUT)
     x = torch.randn(1, T, d["hidden"], device=dev).to(torch.bfloat16)
     lay.reset_state()
     lay(x)
@@ -424,7 +425,7 @@ def small_batch_decode(shape, B, copies=8, steps=400, warmup=40, weight_dtype="b
         gg = torch.Generator(device=dev).manual_seed(200 + i)
         w = {k: (torch.randn(v.shape, generator=gg, device=dev) * v.float().std()).to(v.dtype)
              if k.startswith("w_") or k == "conv_w" else v for k, v in w0.items()}
-        lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B, max_tokens=64, weight_dtype=weight_dtype)
+        lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=B, max_tokens=64, weight_dtype=weight_dtype, out_dtype=LAYER_OUT)
         lay.set_state(rec=torch.randn(B, d["num_v_heads"], d["head_k_dim"], d["head_v_dim"], device=dev) * 0.01)
         layers.append(lay)
         xin.append(torch.randn(B, 1, d["hidden"], device=dev).to(torch.bfloat16))
@@ -470,7 +471,8 @@ def stack_bench(d, n_layers=24, n_prefill=8, prefill_len=2048, n_decode=56, step
     layers, cu, x, s0 = syn.continuous_batch(d, n_layers=n_layers, n_prefill=n_prefill, prefill_len=prefill_len,
                                              n_decode=n_decode, seed=seed)
     n_seq, rows = n_prefill + n_decode, cu[-1]
-    stack = Qwen35GDNStackHIP(layers, dims=d, batch=n_seq, max_slots=n_seq, max_tokens=rows, inter_norm=True)
+    stack = Qwen35GDNStackHIP(layers, dims=d, batch=n_seq, max_slots=n_seq, max_tokens=rows,
+                              inter_norm=True, out_dtype=LAYER_OUT)
     del layers
     slots = torch.arange(n_seq, dtype=torch.int32, device="cuda")
     for L, s in zip(stack.layers, s0):
@@ -554,7 +556,7 @@ def main():
 
     layers = []
     for i in range(L):
-        lay = Qwen35GatedDeltaNetHIP(copy_weights(i), dims=d, batch=B, max_tokens=max(B, 64))
+        lay = Qwen35GatedDeltaNetHIP(copy_weights(i), dims=d, batch=B, max_tokens=max(B, 64), out_dtype=LAYER_OUT)
         s0 = torch.randn(B, d["num_v_heads"], 128, 128, device=dev) * 0.01
         lay.set_state(rec=s0)
         layers.append(lay)
@@ -653,7 +655,8 @@ def main():
             print(f"[bench] {wd}-weight decode, {L} copies", file=sys.stderr, flush=True)
             lays = []
             for i in range(L):
-                lay = Qwen35GatedDeltaNetHIP(copy_weights(i), dims=d, batch=B, max_tokens=max(B, 64), weight_dtype=wd)
+                lay = Qwen35GatedDeltaNetHIP(copy_weights(i), dims=d, batch=B, max_tokens=max(B, 64),
+                                             weight_dtype=wd, out_dtype=LAYER_OUT)
                 lay.set_state(rec=torch.randn(B, d["num_v_heads"], 128, 128, device=dev) * 0.01)
                 lays.append(lay)
             wall, st = eager_decode(lays, xs, args.steps, args.warmup)

@@ -106,18 +106,37 @@ int gdn_layer_create_ex(const gdn_dims* dims, const gdn_weights* weights, int ma
 /* The gdn_weight_format of a layer. */
 int gdn_layer_weight_format(const gdn_layer* layer);
 
+/* Element type of a layer's or a stack's output. */
+typedef enum {
+    GDN_OUT_BF16 = 0, /* bf16 (the default of a new handle) */
+    GDN_OUT_FP32 = 1  /* fp32: the reference's layer output (9B/gdn_layer.py:272-276, ttnn.linear with
+                       * dtype=ttnn.float32) and stack output (0.8B/gdn_l1.py:300, 336-339, fp32 rows) */
+} gdn_out_dtype;
+
+/* The element type (a gdn_out_dtype) of `out` in gdn_layer_forward, gdn_layer_forward_varlen and
+ * gdn_out_proj of this layer, for calls issued after it.  Both types store the same fp32 sums of the
+ * out_proj; the bf16 output is the fp32 one rounded to nearest even.  The state, the workspace and the
+ * activations inside the layer are the same for both.  A split launch (B > 1 and T > max_tokens / B) with
+ * fp32 output needs gdn_layer_proj_width() >= hidden (true of every Qwen3.5 shape), else it fails with
+ * GDN_ERR_UNSUPPORTED. */
+int gdn_layer_set_output_dtype(gdn_layer* layer, int out_dtype);
+
+/* The gdn_out_dtype of a layer's output. */
+int gdn_layer_output_dtype(const gdn_layer* layer);
+
 int gdn_layer_destroy(gdn_layer* layer);
 
 /* 9B/gdn_layer.py:282-292 (__call__) and 244-280 (_forward_rows).
- * x: bf16 [B*T, H]; out: bf16 [B*T, H].  slot_ids: device int32 [B] (state slot of sequence b), or NULL
- * for slots 0..B-1.  Continues every sequence from its slot's conv and recurrent state. */
+ * x: bf16 [B*T, H]; out: [B*T, H] of the layer's output type (bf16 unless gdn_layer_set_output_dtype).
+ * slot_ids: device int32 [B] (state slot of sequence b), or NULL for slots 0..B-1.  Continues every
+ * sequence from its slot's conv and recurrent state. */
 int gdn_layer_forward(gdn_layer* layer, const void* x, int B, int T, const int* slot_ids, void* out,
                       void* stream);
 
 /* Variable-length launch (no counterpart in the reference, which fixes one batch geometry per handle and
  * maps row -> slot as m / T, 9B/kernels/layer_compute.cpp:231): n_seqs sequences of different lengths in
- * one call, e.g. prefills and decode streams of a continuous batch.  x, out: bf16 [cu_seqlens[n_seqs], H];
- * sequence i is rows [cu_seqlens[i], cu_seqlens[i+1]) (host int32 [n_seqs + 1], cu_seqlens[0] = 0, at most
+ * one call, e.g. prefills and decode streams of a continuous batch.  x: bf16 [cu_seqlens[n_seqs], H], out: the
+ * same rows of the layer's output type; sequence i is rows [cu_seqlens[i], cu_seqlens[i+1]) (host int32 [n_seqs + 1], cu_seqlens[0] = 0, at most
  * max_tokens rows) and continues slot slot_ids[i] (device int32 [n_seqs], or NULL for slots 0..n_seqs-1).
  * The in_proj and out_proj run once over all rows; runs of consecutive equal-length sequences share one
  * launch of the middle of the layer.  The result of each sequence equals its own gdn_layer_forward up to
@@ -185,7 +204,8 @@ int gdn_delta_rule(gdn_layer* layer, const float* qn, const float* kn, const flo
 int gdn_gated_rmsnorm(gdn_layer* layer, const float* o, const float* z, int z_stride, int M, void* y,
                       void* stream);
 
-/* out_proj: 9B/gdn_layer.py:272-276.  y bf16 [M, nv*dv] -> out bf16 [M, H]. */
+/* out_proj: 9B/gdn_layer.py:272-276.  y bf16 [M, nv*dv] -> out [M, H] of the layer's output type
+ * (gdn_layer_set_output_dtype). */
 int gdn_out_proj(gdn_layer* layer, const void* y, int M, void* out, void* stream);
 
 /* ---- layer stack: mirrors Qwen35_08B_GDNStackL1 (wormhole_n150/qwen3.5_0.8B/gdn_l1.py:207-341) ---- */
@@ -207,9 +227,18 @@ int gdn_stack_destroy(gdn_stack* stack);
 /* The handle of layer i, for the state calls (gdn_state_*) and per-op entries.  Owned by the stack. */
 int gdn_stack_layer(gdn_stack* stack, int i, gdn_layer** layer);
 
+/* The element type (a gdn_out_dtype, bf16 for a new stack) of the output of gdn_stack_forward(_varlen)
+ * calls that run the stack's last layer; gdn_l1.py:300, 336-339 returns fp32 rows (GDN_OUT_FP32).  The
+ * activations between layers stay bf16, and so does the output of a call that ends before the last layer
+ * (the input of the next call).  A layer's own setting (gdn_layer_set_output_dtype) does not apply inside
+ * the stack. */
+int gdn_stack_set_output_dtype(gdn_stack* stack, int out_dtype);
+
 /* gdn_l1.py:294-341 (forward_device / __call__(hidden_states, layers)): layers [first, first + count) on
- * x bf16 [B*T, H] -> out bf16 [B*T, H]; slot_ids as in gdn_layer_forward.  Launches of more than max_tokens
- * rows run token blocks of at most max_tokens rows through all the layers in turn (B <= max_tokens). */
+ * x bf16 [B*T, H] -> out [B*T, H], of the stack's output type (gdn_stack_set_output_dtype) when the call
+ * runs the stack's last layer and bf16 otherwise; slot_ids as in gdn_layer_forward.  Launches of more than
+ * max_tokens rows run token blocks of at most max_tokens rows through all the layers in turn
+ * (B <= max_tokens). */
 int gdn_stack_forward(gdn_stack* stack, const void* x, int B, int T, const int* slot_ids, int first, int count,
                       void* out, void* stream);
 

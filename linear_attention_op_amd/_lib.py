@@ -31,6 +31,34 @@ WEIGHT_NAMES = {GDN_WEIGHTS_BF16: "bf16", GDN_WEIGHTS_FP8_E4M3: "fp8", GDN_WEIGH
                 GDN_WEIGHTS_MXINT8: "mxint8"}
 
 
+GDN_OUT_BF16 = 0
+GDN_OUT_FP32 = 1
+
+
+_OUT_NAMES = {"fp32": GDN_OUT_FP32, "float32": GDN_OUT_FP32, "bf16": GDN_OUT_BF16, "bfloat16": GDN_OUT_BF16}
+
+
+def out_dtype_code(dtype):
+    """torch.float32 or "fp32" (the reference's layer and stack output), torch.bfloat16 or "bf16" -> a
+    gdn_out_dtype."""
+    import torch
+
+    if isinstance(dtype, str) and dtype.lower() in _OUT_NAMES:
+        return _OUT_NAMES[dtype.lower()]
+    if dtype == torch.float32:
+        return GDN_OUT_FP32
+    if dtype == torch.bfloat16:
+        return GDN_OUT_BF16
+    raise ValueError(f"output dtype {dtype}: torch.float32 / 'fp32' or torch.bfloat16 / 'bf16'")
+
+
+def out_torch_dtype(dtype):
+    """The torch dtype of an output dtype name or torch dtype."""
+    import torch
+
+    return torch.float32 if out_dtype_code(dtype) == GDN_OUT_FP32 else torch.bfloat16
+
+
 def weight_format(weight_dtype):
     """gdn_weight_format of a weight_dtype name ("bf16", "fp8", "mxfp4" or "mxint8")."""
     try:
@@ -74,6 +102,8 @@ SIGNATURES = {
     "gdn_layer_create_ex": (_I, [ctypes.POINTER(GdnDims), ctypes.POINTER(GdnWeights), _I, _I, _I,
                                  ctypes.POINTER(_V)]),
     "gdn_layer_weight_format": (_I, [_V]),
+    "gdn_layer_set_output_dtype": (_I, [_V, _I]),
+    "gdn_layer_output_dtype": (_I, [_V]),
     "gdn_layer_destroy": (_I, [_V]),
     "gdn_layer_forward": (_I, [_V, _V, _I, _I, _V, _V, _V]),
     "gdn_layer_forward_varlen": (_I, [_V, _V, _I, ctypes.POINTER(_I), _V, _V, _V]),
@@ -83,6 +113,7 @@ SIGNATURES = {
                                  ctypes.POINTER(ctypes.c_void_p), _I, _I, _I, ctypes.POINTER(_V)]),
     "gdn_stack_destroy": (_I, [_V]),
     "gdn_stack_layer": (_I, [_V, _I, ctypes.POINTER(_V)]),
+    "gdn_stack_set_output_dtype": (_I, [_V, _I]),
     "gdn_stack_forward": (_I, [_V, _V, _I, _I, _V, _I, _I, _V, _V]),
     "gdn_stack_forward_varlen": (_I, [_V, _V, _I, ctypes.POINTER(_I), _V, _I, _I, _V, _V]),
     "gdn_state_reset": (_I, [_V, _V, _I, _V]),

@@ -58,6 +58,7 @@ struct gdn_layer {
     std::vector<void*> allocs;
 
     int wfmt = GDN_WEIGHTS_BF16;
+    int out_kind = gdn::OUT_BF16;  // element type of the layer's output (gdn_layer_set_output_dtype)
     u16* w_in = nullptr;      // bf16: [NP, H]  rows q | k | v | z | a | b, W_FRAG layout
     u16* w_out = nullptr;     // bf16: [H, Vd] W_FRAG layout
     u16* w_ab = nullptr;      // [2 nv, H] a | b rows, W_FRAG (bf16: inside w_in)
@@ -202,12 +203,17 @@ hipError_t in_proj_rows(const gdn_layer* L, const void* x, int xl, int M, float*
     return gdn::launch_linear(x, xl, L->w_ab, gdn::W_FRAG, nullptr, M, nab, H, P + N1, L->NP, gdn::OUT_F32, st);
 }
 
-// out_proj of M rows of y (row-major, or W_FRAG for M <= 64) into out bf16 [M, H] (9B/gdn_layer.py:272-276).
-hipError_t out_proj_rows(const gdn_layer* L, const void* y, int yl, int M, void* out, hipStream_t st) {
+// out_proj of M rows of y (row-major, or W_FRAG for M <= 64) into out [M, H], bf16 or fp32 by out_kind
+// (9B/gdn_layer.py:272-276).  Both kinds store the same fp32 sums; bf16 rounds them to nearest even.
+hipError_t out_proj_rows(const gdn_layer* L, const void* y, int yl, int M, void* out, int out_kind,
+                         hipStream_t st) {
     const int H = L->d.hidden;
     const QW q = w_out_q(L);
-    return gdn::launch_linear(y, yl, q.w, q.layout, q.scale, M, H, L->Vd, out, H, gdn::OUT_BF16, st);
+    return gdn::launch_linear(y, yl, q.w, q.layout, q.scale, M, H, L->Vd, out, H, out_kind, st);
 }
+
+// bytes of one output element of an out_kind
+size_t out_elem_bytes(int out_kind) { return out_kind == gdn::OUT_F32 ? sizeof(float) : sizeof(u16); }
 
 // A group of sequences of one launch with the same length: rows [row0, row0 + B T) of the launch,
 // sequence b of the group on state slot slots[b].
@@ -219,7 +225,7 @@ struct Group {
 // One launch over M rows made of row groups (9B/gdn_layer.py:244-280 for a single group): the in_proj over
 // all M rows, the middle of the layer per group (fused mixer for groups of <= kFusedMaxT tokens per
 // sequence, front end + chunked recurrence + gated RMSNorm otherwise), the out_proj over all M rows.
-int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, u16* out, hipStream_t st) {
+int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, void* out, int out_kind, hipStream_t st) {
     const gdn_dims& d = L->d;
     const int Kd = L->Kd, Vd = L->Vd, nv = d.num_v_heads;
     hipEvent_t ev[4] = {L->prof_event(0), L->prof_event(1), L->prof_event(2), L->prof_event(3)};
@@ -290,7 +296,7 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, u16* o
         }
     }
     if (ev[2]) HIP_OK(hipEventRecord(ev[2], st));
-    HIP_OK(out_proj_rows(L, L->y, y_frag ? gdn::W_FRAG : gdn::W_ROW, M, out, st));
+    HIP_OK(out_proj_rows(L, L->y, y_frag ? gdn::W_FRAG : gdn::W_ROW, M, out, out_kind, st));
     if (ev[3]) {
         HIP_OK(hipEventRecord(ev[3], st));
         ++L->prof_calls;
@@ -298,30 +304,46 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, u16* o
     return GDN_OK;
 }
 
-int run_chunk(gdn_layer* L, const u16* x, int B, int T, const int* slot_ids, u16* out, hipStream_t st) {
+int run_chunk(gdn_layer* L, const u16* x, int B, int T, const int* slot_ids, void* out, int out_kind,
+              hipStream_t st) {
     const Group g{0, B, T, slot_ids ? slot_ids : L->iota};
-    return run_rows(L, x, B * T, &g, 1, out, st);
+    return run_rows(L, x, B * T, &g, 1, out, out_kind, st);
+}
+
+// Where the output rows of a split launch over several sequences are gathered before they are scattered to
+// their sequences: the bf16 output workspace, or for fp32 rows the projection workspace P ([max_tokens, NP]
+// fp32), which the out_proj neither reads nor is followed by a reader of; NULL when P rows are narrower
+// than the hidden size.
+void* split_out_stage(gdn_layer* L, int out_kind) {
+    if (out_kind != gdn::OUT_F32) return L->out_ws;
+    return L->NP >= L->d.hidden ? (void*)L->P : nullptr;
 }
 
 // gdn_layer_forward without the argument checks: launches longer than the workspace are split by tokens.
-int layer_forward(gdn_layer* L, const u16* x, int B, int T, const int* slot_ids, u16* out, hipStream_t st) {
+int layer_forward(gdn_layer* L, const u16* x, int B, int T, const int* slot_ids, void* out, int out_kind,
+                  hipStream_t st) {
     const int H = L->d.hidden;
     const int tc_max = L->max_tokens / B;
-    if (T <= tc_max) return run_chunk(L, x, B, T, slot_ids, out, st);
+    if (T <= tc_max) return run_chunk(L, x, B, T, slot_ids, out, out_kind, st);
+    char* o = (char*)out;
+    const size_t rb = (size_t)H * sizeof(u16), ob = (size_t)H * out_elem_bytes(out_kind);
+    void* stage = split_out_stage(L, out_kind);
+    if (B > 1 && !stage)
+        return fail(GDN_ERR_UNSUPPORTED, "fp32 output of a split launch of %d sequences needs proj width %d >= "
+                    "hidden %d", B, L->NP, H);
     for (int t0 = 0; t0 < T; t0 += tc_max) {
         const int tc = T - t0 < tc_max ? T - t0 : tc_max;
-        const size_t rb = (size_t)H * sizeof(u16);
         if (B == 1) {
-            int rc = run_chunk(L, x + (size_t)t0 * H, 1, tc, slot_ids, out + (size_t)t0 * H, st);
+            int rc = run_chunk(L, x + (size_t)t0 * H, 1, tc, slot_ids, o + (size_t)t0 * ob, out_kind, st);
             if (rc) return rc;
             continue;
         }
         // gather rows [b, t0:t0+tc) of every sequence into one sequence-major block, and scatter back
         HIP_OK(hipMemcpy2DAsync(L->x_ws, tc * rb, x + (size_t)t0 * H, (size_t)T * rb, tc * rb, B,
                                 hipMemcpyDeviceToDevice, st));
-        int rc = run_chunk(L, L->x_ws, B, tc, slot_ids, L->out_ws, st);
+        int rc = run_chunk(L, L->x_ws, B, tc, slot_ids, stage, out_kind, st);
         if (rc) return rc;
-        HIP_OK(hipMemcpy2DAsync(out + (size_t)t0 * H, (size_t)T * rb, L->out_ws, tc * rb, tc * rb, B,
+        HIP_OK(hipMemcpy2DAsync(o + (size_t)t0 * ob, (size_t)T * ob, stage, tc * ob, tc * ob, B,
                                 hipMemcpyDeviceToDevice, st));
     }
     return GDN_OK;
@@ -551,7 +573,7 @@ int gdn_layer_forward(gdn_layer* L, const void* x, int B, int T, const int* slot
     if (B <= 0 || T <= 0) return fail(GDN_ERR_SHAPE, "gdn_layer_forward: B=%d T=%d must be > 0", B, T);
     if (B > L->max_tokens) return fail(GDN_ERR_SHAPE, "B=%d exceeds max_tokens=%d", B, L->max_tokens);
     if (!slot_ids && B > L->max_slots) return fail(GDN_ERR_SLOT, "B=%d exceeds max_slots=%d", B, L->max_slots);
-    return layer_forward(L, (const u16*)x, B, T, slot_ids, (u16*)out, as_stream(stream));
+    return layer_forward(L, (const u16*)x, B, T, slot_ids, out, L->out_kind, as_stream(stream));
 }
 
 int gdn_layer_forward_varlen(gdn_layer* L, const void* x, int n_seqs, const int* cu_seqlens, const int* slot_ids,
@@ -560,8 +582,21 @@ int gdn_layer_forward_varlen(gdn_layer* L, const void* x, int n_seqs, const int*
     std::vector<Group> groups;
     int rc = varlen_groups(L, n_seqs, cu_seqlens, slot_ids, &groups);
     if (rc) return rc;
-    return run_rows(L, (const u16*)x, cu_seqlens[n_seqs], groups.data(), (int)groups.size(), (u16*)out,
+    return run_rows(L, (const u16*)x, cu_seqlens[n_seqs], groups.data(), (int)groups.size(), out, L->out_kind,
                     as_stream(stream));
+}
+
+int gdn_layer_set_output_dtype(gdn_layer* L, int out_dtype) {
+    if (!L) return fail(GDN_ERR_INVALID_ARG, "layer is NULL");
+    if (out_dtype != GDN_OUT_BF16 && out_dtype != GDN_OUT_FP32)
+        return fail(GDN_ERR_INVALID_ARG, "output dtype %d (GDN_OUT_BF16 = 0 or GDN_OUT_FP32 = 1)", out_dtype);
+    L->out_kind = out_dtype == GDN_OUT_FP32 ? gdn::OUT_F32 : gdn::OUT_BF16;
+    return GDN_OK;
+}
+
+int gdn_layer_output_dtype(const gdn_layer* L) {
+    if (!L) return fail(GDN_ERR_INVALID_ARG, "layer is NULL");
+    return L->out_kind == gdn::OUT_F32 ? GDN_OUT_FP32 : GDN_OUT_BF16;
 }
 
 int gdn_state_reset(gdn_layer* L, const int* slot_ids, int n, void* stream) {
@@ -682,7 +717,7 @@ int gdn_gated_rmsnorm(gdn_layer* L, const float* o, const float* z, int z_stride
 int gdn_out_proj(gdn_layer* L, const void* y, int M, void* out, void* stream) {
     if (!L || !y || !out) return fail(GDN_ERR_INVALID_ARG, "gdn_out_proj: NULL argument");
     if (M <= 0) return fail(GDN_ERR_SHAPE, "M=%d", M);
-    HIP_OK(out_proj_rows(L, y, gdn::W_ROW, M, out, as_stream(stream)));
+    HIP_OK(out_proj_rows(L, y, gdn::W_ROW, M, out, L->out_kind, as_stream(stream)));
     return GDN_OK;
 }
 
@@ -822,6 +857,7 @@ struct gdn_stack {
     float* norm_w = nullptr;  // [n_layers, H] decoder RMSNorm weights (y = x rstd (1 + w))
     u16* act[2] = {nullptr, nullptr};
     int H = 0, max_tokens = 0;
+    int out_kind = gdn::OUT_BF16;  // element type of the output of calls that run the last layer
     float eps = 1e-6f;
     ~gdn_stack() {
         for (size_t i = layers.size(); i-- > 0;) delete layers[i];  // borrowers before the workspace owner
@@ -833,13 +869,21 @@ struct gdn_stack {
 
 namespace {
 
+// Element type of `out` of a call over layers [first, first + count): the stack's output type when the call
+// runs the last layer, else bf16 (the activations between layers, and the next call's input).
+int stack_out_kind(const gdn_stack* S, int first, int count) {
+    return first + count == (int)S->layers.size() ? S->out_kind : gdn::OUT_BF16;
+}
+
 // Layers [first, first + count) on rows made of `groups`; norms after every layer but the stack's last.
-int stack_run(gdn_stack* S, const u16* x, int M, const Group* groups, int ng, int first, int count, u16* out,
+int stack_run(gdn_stack* S, const u16* x, int M, const Group* groups, int ng, int first, int count, void* out,
               hipStream_t st) {
     const u16* in = x;
     for (int i = first; i < first + count; ++i) {
-        u16* dst = i + 1 == first + count ? out : S->act[(i - first) & 1];
-        int rc = run_rows(S->layers[i], in, M, groups, ng, dst, st);
+        const bool last = i + 1 == first + count;
+        u16* dst = last ? (u16*)out : S->act[(i - first) & 1];
+        int rc = run_rows(S->layers[i], in, M, groups, ng, dst, last ? stack_out_kind(S, first, count) : gdn::OUT_BF16,
+                          st);
         if (rc) return rc;
         if (S->inter_norm && i + 1 < (int)S->layers.size())
             HIP_OK(gdn::launch_rmsnorm_rows(dst, M, S->H, S->norm_w + (size_t)i * S->H, S->eps, dst, st));
@@ -924,7 +968,8 @@ int gdn_stack_forward(gdn_stack* S, const void* x, int B, int T, const int* slot
     const int* slots = slot_ids ? slot_ids : S->layers[0]->iota;
     const hipStream_t st = as_stream(stream);
     const u16* xin = (const u16*)x;
-    u16* xout = (u16*)out;
+    char* xout = (char*)out;
+    const int okind = stack_out_kind(S, first, count);
     const int tc_max = S->max_tokens / B;
     if (T <= tc_max) {
         const Group g{0, B, T, slots};
@@ -935,20 +980,24 @@ int gdn_stack_forward(gdn_stack* S, const void* x, int B, int T, const int* slot
     // splits one layer the same way).  Rows of several sequences are gathered into the workspace of layer 0
     // (not used by the layers' own launches) and scattered back.
     gdn_layer* L0 = S->layers[0];
-    const size_t rb = (size_t)S->H * sizeof(u16);
+    const size_t rb = (size_t)S->H * sizeof(u16), ob = (size_t)S->H * out_elem_bytes(okind);
+    void* stage = split_out_stage(L0, okind);  // the layers share L0's workspaces
+    if (B > 1 && !stage)
+        return fail(GDN_ERR_UNSUPPORTED, "fp32 output of a split launch of %d sequences needs proj width %d >= "
+                    "hidden %d", B, L0->NP, S->H);
     for (int t0 = 0; t0 < T; t0 += tc_max) {
         const int tc = T - t0 < tc_max ? T - t0 : tc_max;
         const Group g{0, B, tc, slots};
         if (B == 1) {
-            int rc = stack_run(S, xin + (size_t)t0 * S->H, tc, &g, 1, first, count, xout + (size_t)t0 * S->H, st);
+            int rc = stack_run(S, xin + (size_t)t0 * S->H, tc, &g, 1, first, count, xout + (size_t)t0 * ob, st);
             if (rc) return rc;
             continue;
         }
         HIP_OK(hipMemcpy2DAsync(L0->x_ws, tc * rb, xin + (size_t)t0 * S->H, (size_t)T * rb, tc * rb, B,
                                 hipMemcpyDeviceToDevice, st));
-        int rc = stack_run(S, L0->x_ws, B * tc, &g, 1, first, count, L0->out_ws, st);
+        int rc = stack_run(S, L0->x_ws, B * tc, &g, 1, first, count, stage, st);
         if (rc) return rc;
-        HIP_OK(hipMemcpy2DAsync(xout + (size_t)t0 * S->H, (size_t)T * rb, L0->out_ws, tc * rb, tc * rb, B,
+        HIP_OK(hipMemcpy2DAsync(xout + (size_t)t0 * ob, (size_t)T * ob, stage, tc * ob, tc * ob, B,
                                 hipMemcpyDeviceToDevice, st));
     }
     return GDN_OK;
@@ -962,8 +1011,16 @@ int gdn_stack_forward_varlen(gdn_stack* S, const void* x, int n_seqs, const int*
     std::vector<Group> groups;
     int rc = varlen_groups(S->layers[0], n_seqs, cu_seqlens, slot_ids, &groups);
     if (rc) return rc;
-    return stack_run(S, (const u16*)x, cu_seqlens[n_seqs], groups.data(), (int)groups.size(), first, count, (u16*)out,
+    return stack_run(S, (const u16*)x, cu_seqlens[n_seqs], groups.data(), (int)groups.size(), first, count, out,
                      as_stream(stream));
+}
+
+int gdn_stack_set_output_dtype(gdn_stack* S, int out_dtype) {
+    if (!S) return fail(GDN_ERR_INVALID_ARG, "stack is NULL");
+    if (out_dtype != GDN_OUT_BF16 && out_dtype != GDN_OUT_FP32)
+        return fail(GDN_ERR_INVALID_ARG, "output dtype %d (GDN_OUT_BF16 = 0 or GDN_OUT_FP32 = 1)", out_dtype);
+    S->out_kind = out_dtype == GDN_OUT_FP32 ? gdn::OUT_F32 : gdn::OUT_BF16;
+    return GDN_OK;
 }
 
 }  // extern "C"

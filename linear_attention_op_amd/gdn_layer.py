@@ -101,10 +101,12 @@ class Qwen35GatedDeltaNetHIP:
     `weight_dtype` ("bf16", "fp8", "mxfp4" or "mxint8") mirrors the reference's weight_dtype (9B/gdn_layer.py:55;
     bfloat8_b / bfloat4_b, 0.8B/gdn_l1.py:79-80): "fp8" keeps the q|k|v|z and out projections as E4M3 with
     per-row scales (see quantize_fp8), "mxfp4" as MXFP4 with a scale per 32 (see quantize_mxfp4), "mxint8" as
-    MXINT8 with a scale per 32 (see quantize_mxint8; the bfloat8_b counterpart); a|b stay bf16."""
+    MXINT8 with a scale per 32 (see quantize_mxint8; the bfloat8_b counterpart); a|b stay bf16.
+    `out_dtype` is the element type of the layer's output: torch.float32, the reference's (9B/gdn_layer.py:272-276
+    computes out_proj with dtype=ttnn.float32), or torch.bfloat16, the same sums rounded to nearest even."""
 
     def __init__(self, weights, dims=None, batch=1, max_slots=None, max_tokens=16384, device="cuda", _handle=None,
-                 weight_dtype="bf16"):
+                 weight_dtype="bf16", out_dtype=torch.float32):
         self.device = torch.device(device)
         self.batch = batch
         self.max_slots = max_slots or batch
@@ -127,6 +129,8 @@ class Qwen35GatedDeltaNetHIP:
         self.proj_width = _lib.lib().gdn_layer_proj_width(self._h)
         fmt = _lib.lib().gdn_layer_weight_format(self._h)
         self.weight_dtype = _lib.WEIGHT_NAMES[fmt]
+        _lib.check(_lib.lib().gdn_layer_set_output_dtype(self._h, _lib.out_dtype_code(out_dtype)))
+        self.out_dtype = _lib.out_torch_dtype(out_dtype)
 
     @classmethod
     def from_checkpoint(cls, path, layer_idx, prefix=None, **kwargs):
@@ -151,23 +155,23 @@ class Qwen35GatedDeltaNetHIP:
 
     # ---- layer ------------------------------------------------------------------------------------
     def __call__(self, hidden_states, slot_ids=None):
-        """hidden_states [B, T, H] (any float dtype, used as bf16) -> [B, T, H] bf16, continuing the states
-        of slots `slot_ids` (default 0..B-1).  9B/gdn_layer.py:282-292."""
+        """hidden_states [B, T, H] (any float dtype, used as bf16) -> [B, T, H] of out_dtype, continuing the
+        states of slots `slot_ids` (default 0..B-1).  9B/gdn_layer.py:282-292."""
         B, T, H = hidden_states.shape
         if H != self.hidden:
             raise ValueError(f"hidden {H} != {self.hidden}")
         x = hidden_states.to(device=self.device, dtype=torch.bfloat16).contiguous()
-        out = torch.empty_like(x)
+        out = torch.empty(x.shape, device=self.device, dtype=self.out_dtype)
         s = _slots(slot_ids, self.device, self.max_slots, unique=True)
         _lib.check(_lib.lib().gdn_layer_forward(self._h, _ptr(x), B, T, _ptr(s), _ptr(out), _stream()))
         return out
 
     def forward_varlen(self, x, cu_seqlens, slot_ids=None):
         """x [total, H]: sequences of different lengths (rows cu_seqlens[i]..cu_seqlens[i+1]) in one launch,
-        sequence i continuing slot slot_ids[i] (default i) -> [total, H] bf16."""
+        sequence i continuing slot slot_ids[i] (default i) -> [total, H] of out_dtype."""
         n = len(cu_seqlens) - 1
         x = x.to(device=self.device, dtype=torch.bfloat16).reshape(-1, self.hidden).contiguous()
-        out = torch.empty_like(x)
+        out = torch.empty(x.shape, device=self.device, dtype=self.out_dtype)
         s = _slots(slot_ids, self.device, self.max_slots, unique=True)
         _lib.check(_lib.lib().gdn_layer_forward_varlen(self._h, _ptr(x), n, cu_seqlens_arg(cu_seqlens, n), _ptr(s),
                                                        _ptr(out), _stream()))
@@ -265,9 +269,9 @@ class Qwen35GatedDeltaNetHIP:
         return y
 
     def out_proj(self, y):
-        """y [M, nv*dv] -> out [M, H] bf16."""
+        """y [M, nv*dv] -> out [M, H] of out_dtype."""
         y = y.to(device=self.device, dtype=torch.bfloat16).contiguous()
-        out = torch.empty(y.shape[0], self.hidden, device=self.device, dtype=torch.bfloat16)
+        out = torch.empty(y.shape[0], self.hidden, device=self.device, dtype=self.out_dtype)
         _lib.check(_lib.lib().gdn_out_proj(self._h, _ptr(y), y.shape[0], _ptr(out), _stream()))
         return out
 

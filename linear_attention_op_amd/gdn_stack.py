@@ -20,10 +20,12 @@ from .gdn_layer import Qwen35GatedDeltaNetHIP, _ptr, _slots, _stream, cu_seqlens
 class Qwen35GDNStackHIP:
     """`layers`: HF Qwen3_5GatedDeltaNet modules or weight dicts (see Qwen35GatedDeltaNetHIP), one per layer.
     `norm_weights`: optional per-layer [H] weights of the RMSNorm after each layer (default 0, i.e. (1 + w) = 1).
-    `weight_dtype`: "bf16", "fp8", "mxfp4" or "mxint8" for every layer (wormhole_n150/qwen3.5_0.8B/gdn_l1.py:79-80)."""
+    `weight_dtype`: "bf16", "fp8", "mxfp4" or "mxint8" for every layer (wormhole_n150/qwen3.5_0.8B/gdn_l1.py:79-80).
+    `out_dtype`: element type of the stack's output, torch.float32 as the reference's (gdn_l1.py:336-339 returns
+    fp32 rows) or torch.bfloat16; the activations between layers are bf16 either way."""
 
     def __init__(self, layers, dims=None, batch=1, max_slots=None, max_tokens=None, inter_norm=False,
-                 norm_weights=None, device="cuda", weight_dtype="bf16"):
+                 norm_weights=None, device="cuda", weight_dtype="bf16", out_dtype=torch.float32):
         self.device = torch.device(device)
         self.batch = batch
         self.max_slots = max_slots or batch
@@ -49,12 +51,15 @@ class Qwen35GDNStackHIP:
         _lib.check(_lib.lib().gdn_stack_create_ex(ctypes.byref(prepared[0][1]), cw, self.n_layers, int(inter_norm),
                                                   nw, self.max_slots, self.max_tokens,
                                                   _lib.weight_format(weight_dtype), ctypes.byref(self._h)))
+        _lib.check(_lib.lib().gdn_stack_set_output_dtype(self._h, _lib.out_dtype_code(out_dtype)))
+        self.out_dtype = _lib.out_torch_dtype(out_dtype)
         self.layers = []
         for i in range(self.n_layers):
             h = ctypes.c_void_p()
             _lib.check(_lib.lib().gdn_stack_layer(self._h, i, ctypes.byref(h)))
             self.layers.append(Qwen35GatedDeltaNetHIP(None, dims=self.dims, batch=batch, max_slots=self.max_slots,
-                                                      max_tokens=self.max_tokens, device=device, _handle=h))
+                                                      max_tokens=self.max_tokens, device=device, _handle=h,
+                                                      out_dtype=out_dtype))
 
     @classmethod
     def from_checkpoint(cls, path, layers=None, prefix=None, **kwargs):
@@ -93,9 +98,16 @@ class Qwen35GDNStackHIP:
                 runs.append([i, 1])
         return runs
 
+    def _run_dtype(self, first, count):
+        """Element type of the output of the C call over layers [first, first + count): the stack's output type
+        when it runs the last layer, else bf16 (activations)."""
+        return self.out_dtype if first + count == self.n_layers else torch.bfloat16
+
     def __call__(self, hidden_states, layers=None, slot_ids=None):
-        """hidden_states [B, H] (one decode step) or [B, T, H] -> same shape, bf16, through `layers` (default
-        all) in order, continuing the states of slots `slot_ids` (default 0..B-1).  gdn_l1.py:330-341."""
+        """hidden_states [B, H] (one decode step) or [B, T, H] -> same shape, of out_dtype, through `layers`
+        (default all) in order, continuing the states of slots `slot_ids` (default 0..B-1).  gdn_l1.py:330-341.
+        A list that does not end with the last layer returns the bf16 activations after its last layer, widened
+        to out_dtype."""
         shape = hidden_states.shape
         x = hidden_states.to(device=self.device, dtype=torch.bfloat16)
         if x.dim() == 2:
@@ -106,11 +118,12 @@ class Qwen35GDNStackHIP:
         x = x.contiguous()
         s = _slots(slot_ids, self.device, self.max_slots, unique=True)
         for first, count in self._runs(layers, self.n_layers):
-            out = torch.empty_like(x)
+            x = x.to(torch.bfloat16)  # the fp32 output of an earlier run that ended at the last layer
+            out = torch.empty(x.shape, device=self.device, dtype=self._run_dtype(first, count))
             _lib.check(_lib.lib().gdn_stack_forward(self._h, _ptr(x), B, T, _ptr(s), first, count, _ptr(out),
                                                     _stream()))
             x = out
-        return x.reshape(shape)
+        return x.to(self.out_dtype).reshape(shape)
 
     def forward_varlen(self, x, cu_seqlens, slot_ids=None, layers=None):
         """x [total, H]: a continuous batch -- sequence i is rows cu_seqlens[i]..cu_seqlens[i+1] and continues
@@ -120,11 +133,12 @@ class Qwen35GDNStackHIP:
         cu = cu_seqlens_arg(cu_seqlens, n)
         s = _slots(slot_ids, self.device, self.max_slots, unique=True)
         for first, count in self._runs(layers, self.n_layers):
-            out = torch.empty_like(x)
+            x = x.to(torch.bfloat16)
+            out = torch.empty(x.shape, device=self.device, dtype=self._run_dtype(first, count))
             _lib.check(_lib.lib().gdn_stack_forward_varlen(self._h, _ptr(x), n, cu, _ptr(s), first, count,
                                                            _ptr(out), _stream()))
             x = out
-        return x
+        return x.to(self.out_dtype)
 
     def reset_state(self, slot_ids=None):
         """Zero every layer's states (gdn_l1.py:203-205)."""

@@ -56,6 +56,18 @@ def test_null_arguments_are_errors_not_crashes():
     assert L.gdn_layer_forward(None, None, 1, 1, None, None, None) == _lib.GDN_ERR_INVALID_ARG
     assert L.gdn_state_get(None, None, 1, None, None, None) == _lib.GDN_ERR_INVALID_ARG
     assert L.gdn_layer_destroy(None) == _lib.GDN_OK
+    assert L.gdn_layer_set_output_dtype(None, _lib.GDN_OUT_FP32) == _lib.GDN_ERR_INVALID_ARG
+    assert L.gdn_layer_output_dtype(None) == _lib.GDN_ERR_INVALID_ARG
+    assert L.gdn_stack_set_output_dtype(None, _lib.GDN_OUT_BF16) == _lib.GDN_ERR_INVALID_ARG
+
+
+def test_output_dtype_names():
+    import torch
+
+    assert _lib.out_dtype_code(torch.float32) == _lib.GDN_OUT_FP32 == 1
+    assert _lib.out_dtype_code(torch.bfloat16) == _lib.GDN_OUT_BF16 == 0
+    with pytest.raises(ValueError):
+        _lib.out_dtype_code(torch.float16)
 
 
 def test_linear_and_recurrence_shape_checks():

@@ -120,7 +120,8 @@ def test_out_proj_one_hot_rows_exact(M):
     print(f"mxint8 out_proj one-hot M={M}", flush=True)
     d = syn.SHAPES["0.8b"]
     w = representable_weights(d, seed=4)
-    layer = Qwen35GatedDeltaNetHIP(w, dims=d, batch=1, max_tokens=64, weight_dtype="mxint8")
+    layer = Qwen35GatedDeltaNetHIP(w, dims=d, batch=1, max_tokens=64, weight_dtype="mxint8",
+                                  out_dtype=torch.bfloat16)
     Vd = d["num_v_heads"] * d["head_v_dim"]
     cols = (torch.arange(M) * 101) % Vd
     y = torch.zeros(M, Vd)

@@ -59,11 +59,12 @@ def test_stack_equals_chained_layers():
     for i, L in enumerate(layers):
         assert torch.equal(stack.get_recurrent_state(i), L.get_recurrent_state()), f"layer {i}"
         assert torch.equal(stack.layers[i].get_conv_state(), L.get_conv_state()), f"layer {i}"
-    # a subset runs only those layers: layer 1 alone on the same input as a lone layer 1
+    # a subset runs only those layers: layer 1 alone on the same input as a lone layer 1 (a call that ends
+    # before the last layer returns the bf16 activations, widened to the stack's fp32 output type)
     xt = x[:, 0].cuda()
     got = stack(xt, layers=[1])
     want = layers[1](xt.to(torch.bfloat16).unsqueeze(1)).squeeze(1)
-    assert torch.equal(got, want)
+    assert torch.equal(got, want.bfloat16().float())
 
 
 def _dequantized(w, weight_dtype):
@@ -140,8 +141,9 @@ def test_stack_inter_norm():
     stack = Qwen35GDNStackHIP(ws, dims=d, batch=B, inter_norm=True, norm_weights=nw)
     lone = [Qwen35GatedDeltaNetHIP(w, dims=d, batch=B, max_tokens=64) for w in ws]
     got = stack(x[:, 0].cuda()).float().cpu()
-    h0 = lone[0](x[:, :1].cuda()).float().cpu()[:, 0]
-    # decoder RMSNorm in float32 on the CPU, rounded to bf16 at the layer boundary
+    # the stack's activations between layers are bf16: layer 0's output rounded to bf16, the decoder RMSNorm
+    # in float32 on the CPU, rounded to bf16 at the layer boundary
+    h0 = lone[0](x[:, :1].cuda()).bfloat16().float().cpu()[:, 0]
     hn = (h0 * torch.rsqrt(h0.pow(2).mean(-1, keepdim=True) + 1e-6) * (1.0 + nw[0])).bfloat16()
     want = lone[1](hn.unsqueeze(1).cuda()).float().cpu()[:, 0]
     r = rel(got, want)
