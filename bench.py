@@ -24,8 +24,30 @@ sys.path.insert(0, ROOT)
 
 METRIC = "GDN-layer decode tok/s + prefill tok/s at 9B shape; % HBM / MFMA roofline"
 HBM_PEAK = 8.0e12        # B/s, MI355X HBM3E
-LAYER_OUT = "bf16"       # layer / stack output element type: bf16 activations, as in a bf16 model
 BF16_PEAK = 2.5e15       # FLOP/s, MI355X dense bf16 MFMA
+LAYER_OUT = "bf16"       # layer / stack output element type: bf16 activations, as in a bf16 model
+# Every measured workload first runs untimed for SETTLE_S seconds, then its warm-up steps, then the timed
+# steps.  From idle the clocks take tens of milliseconds to rise: the 16k prefill measured 3.33 ms per call
+# after one warm-up call against 2.90-2.92 ms after 200 ms of calls (in_proj GEMM 1.64 -> 1.40 ms), the
+# batch-64 decode 90 against 88-89 us per step.
+SETTLE_S = 0.3
+
+
+def settle(fn, seconds=SETTLE_S):
+    """Run fn() untimed until `seconds` have passed, synchronising about every 20 ms; returns the call count."""
+    import torch
+
+    t0 = time.perf_counter()
+    fn()
+    torch.cuda.synchronize()
+    k = max(1, int(0.02 / max(time.perf_counter() - t0, 1e-6)))
+    n = 1
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(k):
+            fn()
+        n += k
+        torch.cuda.synchronize()
+    return n
 
 
 def decode_bytes(d, B, weights="bf16"):
@@ -54,6 +76,8 @@ def eager_decode(layers, xs, steps, warmup):
     import torch
 
     L = len(layers)
+    it = iter(range(1 << 62))
+    settle(lambda: (lambda i: layers[i % L](xs[i % len(xs)]))(next(it)))
     for i in range(warmup):
         layers[i % L](xs[i % len(xs)])
     torch.cuda.synchronize()
@@ -221,10 +245,12 @@ def pmc_child(steps=4):
 
 def profile_child(which):
     """Workload for an external profiler (rocprofv3 --kernel-trace / --pmc put this process after `--`):
-    `decode`: 9B decode at batch 64, 4 layer copies rotated as in the benchmark, 3 warm-up + 12 steps;
-    `prefill`: one 16384-token prefill of a 9B layer, 1 warm-up + 3 runs;
+    `decode`: 9B decode at batch 64, 4 layer copies rotated as in the benchmark, SETTLE_S seconds of steps then
+    16 more;
+    `prefill`: one 16384-token prefill of a 9B layer, SETTLE_S seconds of prefills then 4 more;
     `small`: 9B decode at batch 1 and at batch 8, then the 0.8B shape at batch 1, 8 layer copies each rotated,
-    3 warm-up + 12 steps each."""
+    SETTLE_S seconds of steps then 16 more each.
+    A kernel trace of these averages over every call: almost all of them run at settled clocks."""
     import torch
 
     from linear_attention_op_amd import Qwen35GatedDeltaNetHIP
@@ -246,7 +272,9 @@ def profile_child(which):
                 lay.set_state(rec=torch.randn(B, ds["num_v_heads"], 128, 128, device=dev) * 0.01)
                 layers.append(lay)
             x = torch.randn(B, 1, ds["hidden"], device=dev).to(torch.bfloat16)
-            for i in range(15):
+            it = iter(range(1 << 62))
+            settle(lambda: layers[next(it) % 8](x))
+            for i in range(16):
                 layers[i % 8](x)
             torch.cuda.synchronize()
             for lay in layers:
@@ -261,14 +289,21 @@ def profile_child(which):
             lay.set_state(rec=torch.randn(64, d["num_v_heads"], 128, 128, device=dev) * 0.01)
             layers.append(lay)
         x = torch.randn(64, 1, d["hidden"], device=dev).to(torch.bfloat16)
-        for i in range(15):
+        it = iter(range(1 << 62))
+        settle(lambda: layers[next(it) % 4](x))
+        for i in range(16):
             layers[i % 4](x)
     else:
         lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=1, max_tokens=16384, out_dtype=LAYER_OUT)
         x = torch.randn(1, 16384, d["hidden"], device=dev).to(torch.bfloat16)
-        for _ in range(4):
+
+        def once():
             lay.reset_state()
             lay(x)
+
+        settle(once)
+        for _ in range(4):
+            once()
     torch.cuda.synchronize()
     print(f"profile child {which}: done", flush=True)
 
@@ -386,8 +421,12 @@ def prefill_bench(w, d, T, steps, weight_dtype="bf16"):
     dev = torch.device("cuda", 0)
     lay = Qwen35GatedDeltaNetHIP(w, dims=d, batch=1, max_tokens=T, weight_dtype=weight_dtype, out_dtype=LAYER_OUT)
     x = torch.randn(1, T, d["hidden"], device=dev).to(torch.bfloat16)
-    lay.reset_state()
-    lay(x)
+
+    def once():
+        lay.reset_state()
+        lay(x)
+
+    settle(once)
     torch.cuda.synchronize()
     lay.profile(steps)
     t0 = time.perf_counter()
@@ -441,6 +480,8 @@ def small_batch_decode(shape, B, copies=8, steps=400, warmup=40, weight_dtype="b
         with torch.cuda.graph(g):
             lay(x)
         graphs.append(g)
+    it = iter(range(1 << 62))
+    settle(lambda: graphs[next(it) % copies].replay())
     for i in range(warmup):
         graphs[i % copies].replay()
     torch.cuda.synchronize()
@@ -479,6 +520,8 @@ def stack_bench(d, n_layers=24, n_prefill=8, prefill_len=2048, n_decode=56, step
         L.set_state(rec=s, slot_ids=slots[n_prefill:])
     del s0
     xs = [x, torch.roll(x, 1, 0)]
+    it = iter(range(1 << 62))
+    settle(lambda: stack.forward_varlen(xs[next(it) % 2], cu, slots))
     for i in range(warmup):
         stack.forward_varlen(xs[i % 2], cu, slots)
     torch.cuda.synchronize()
@@ -510,7 +553,7 @@ def main():
     ap.add_argument("--batch", type=int, default=64)
     ap.add_argument("--copies", type=int, default=4, help="independent layers rotated through (defeats MALL)")
     ap.add_argument("--prefill-len", type=int, default=16384)
-    ap.add_argument("--prefill-steps", type=int, default=3)
+    ap.add_argument("--prefill-steps", type=int, default=10)
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--graph", type=int, default=0,
                     help="1: replay the decode step from HIP graphs; 0: launch eagerly (faster here: 104 vs 112 us)")
@@ -565,6 +608,8 @@ def main():
 
     # eager warm-up, then one HIP graph per layer copy for the decode step (the counterpart of the
     # reference's traced decode, wormhole_n150/qwen3.5_0.8B/bench_decode.py:44-60)
+    it = iter(range(1 << 62))
+    settle(lambda: (lambda i: layers[i % L](xs[i % 4]))(next(it)))
     for i in range(args.warmup):
         layers[i % L](xs[i % 4])
     torch.cuda.synchronize()
@@ -726,6 +771,8 @@ def main():
         "mxfp4_decode": lowp.get("mxfp4"), "mxint8_decode": lowp.get("mxint8"),
         "small_batch_decode": small,
         "cpu_baseline": cpu,
+        "settle": {"seconds": SETTLE_S, "what": "untimed runs of each measured workload before its warm-up steps, "
+                                                "so that the clocks have left their idle state"},
     }
     print(json.dumps(line))
 
