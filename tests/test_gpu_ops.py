@@ -132,6 +132,35 @@ def test_chunked_recurrence_matches_oracle(B, Hk, Hv, T, l2):
     assert rel(op.get_state(), want_s.reshape(B * Hv, dk, dv)) < STATE_TOL
 
 
+def test_chunked_recurrence_mixed_decay():
+    """Chunk decays from ~1 to below 2^-8 within one launch and within one head (the chunked form's W S error
+    reaches the state scaled by the chunk's decay): eight v-heads with per-token log decays from -0.004 to -0.3
+    and per-token noise, so that 64-token sums fall on both sides of -8 ln 2; against the oracle."""
+    print("chunked recurrence, mixed chunk decays", flush=True)
+    B, Hk, Hv, dk, dv, T = 1, 4, 8, 128, 128, 640
+    gen = torch.Generator().manual_seed(61)
+    q = torch.randn(B, T, Hk, dk, generator=gen)
+    k = torch.randn(B, T, Hk, dk, generator=gen)
+    v = torch.randn(B, T, Hv, dv, generator=gen)
+    rate = torch.logspace(np.log10(0.004), np.log10(0.3), Hv)
+    g = -rate * (0.2 + 1.6 * torch.rand(B, T, Hv, generator=gen))
+    beta = torch.sigmoid(torch.randn(B, T, Hv, generator=gen))
+    G = g[0].reshape(-1, 64, Hv).sum(1)
+    lim = -8 * np.log(2.0)
+    # fast and slow chunks overall, and both within one head
+    assert (G > lim).any() and (G <= lim).any() and ((G > lim).any(0) & (G <= lim).any(0)).any()
+    init = torch.randn(B, Hv, dk, dv, generator=gen) * 0.1
+    want_o, want_s = oracle.recurrent_gated_delta_rule(q.numpy(), k.numpy(), v.numpy(), g.numpy(), beta.numpy(),
+                                                       init.numpy())
+    op = GatedDeltaRuleHIP(B * Hv, dk, dv, initial_state=init.reshape(B * Hv, dk, dv).cuda())
+    got_o = op(q, k, v, g, beta)
+    torch.cuda.synchronize()
+    assert op.workspace is not None  # the chunked form ran
+    r_o, r_s = rel(got_o, want_o), rel(op.get_state(), want_s.reshape(B * Hv, dk, dv))
+    print(f"  output {r_o:.2e} state {r_s:.2e}", flush=True)
+    assert r_o < STATE_TOL and r_s < STATE_TOL
+
+
 def test_chunked_recurrence_matches_token_loop():
     """9B heads, T = 2048 then T = 100 on the same object (the workspace is kept, the state carried): the
     chunked form against the token loop on the same inputs."""
