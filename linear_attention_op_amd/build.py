@@ -4,6 +4,8 @@
 
 Objects go to linear_attention_op_amd/_build/, the library to linear_attention_op_amd/libgdn_hip.so.  The HBM
 stream probe (csrc/hbm_stream.hip), a measurement yardstick that only bench.py loads, becomes libgdn_stream.so.
+The C host driver of the ABI (csrc/gdn_driver.c, plain C against include/gdn.h and the HIP runtime) becomes
+linear_attention_op_amd/gdn_driver, linked to libgdn_hip.so beside it.
 """
 
 import os
@@ -21,6 +23,9 @@ ARCH = "gfx950"
 SOURCES = ["gdn_linear.hip", "gdn_mixer.hip", "gdn_delta.hip", "gdn_chunk.hip", "gdn_api.cpp"]
 STREAM_SOURCES = ["hbm_stream.hip"]
 STREAM_LIB = os.path.join(HERE, "libgdn_stream.so")
+DRIVER_SRC = os.path.join(CSRC, "gdn_driver.c")
+DRIVER = os.path.join(HERE, "gdn_driver")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-result",
@@ -55,6 +60,21 @@ def _link(objs, lib, verbose):
         print(f"built {lib}", file=sys.stderr)
 
 
+def _driver(verbose):
+    tmp = DRIVER + ".tmp"
+    cmd = ["gcc", "-O2", "-std=c11", "-Wall", "-Wextra", "-D__HIP_PLATFORM_AMD__", f"-I{ROCM}/include", DRIVER_SRC,
+           "-o", tmp, f"-L{HERE}", "-lgdn_hip", f"-L{ROCM}/lib", "-lamdhip64", "-lm", "-Wl,-rpath,$ORIGIN",
+           f"-Wl,-rpath,{ROCM}/lib"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"gcc failed for gdn_driver.c:\n{r.stderr}")
+    if r.stderr.strip():
+        print(r.stderr, file=sys.stderr)
+    os.replace(tmp, DRIVER)
+    if verbose:
+        print(f"built {DRIVER}", file=sys.stderr)
+
+
 def build(verbose=True):
     os.makedirs(BUILD, exist_ok=True)
     srcs = SOURCES + STREAM_SOURCES
@@ -62,6 +82,7 @@ def build(verbose=True):
         objs = list(ex.map(_compile, srcs))
     _link(objs[:len(SOURCES)], LIB, verbose)
     _link(objs[len(SOURCES):], STREAM_LIB, verbose)
+    _driver(verbose)
     return LIB
 
 

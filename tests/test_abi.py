@@ -152,3 +152,18 @@ def test_host_slot_ids_are_checked_before_upload():
     with pytest.raises(_lib.GdnValueError):
         _slots([1, 1], cpu, 4, unique=True)
     assert _slots([1, 1], cpu, 4).tolist() == [1, 1]  # state reads may name a slot twice
+
+
+def test_c_driver_links_and_parses_arguments():
+    """The C host driver (csrc/gdn_driver.c, built beside the library) links against libgdn_hip.so and the HIP
+    runtime and rejects a bad argument before it touches a device."""
+    import os
+    import subprocess
+
+    exe = os.path.join(os.path.dirname(_lib.LIB_PATH), "gdn_driver")
+    if not os.path.exists(exe):
+        pytest.skip("gdn_driver not built (run __graft_entry__.build())")
+    r = subprocess.run([exe, "--no-such-option"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2 and "usage: gdn_driver" in r.stderr
+    r = subprocess.run([exe, "--shape", "7b"], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2 and "shape 7b" in r.stderr
