@@ -19,11 +19,12 @@
 //    workspace, laid out as U).
 //  * chunk_state_kernel: the sequential pass over chunks.  A workgroup owns 16 value columns of one
 //    (sequence, v-head) state; its eight waves own 16 state rows each, held in MFMA accumulators for the
-//    whole launch (state read once, written once).  Per chunk: W S and Q' S (partials over the waves'
-//    rows, summed through LDS), Vn, O += Q' S, S update.  The operands of the next two chunks are in
-//    flight while the current one is computed; each step issues the loads of the chunk two ahead in four
-//    parts spread over its own work.  Workgroup ids put the 8 column blocks of a head on one XCD so that they
-//    share that XCD's L2 copy of W, Q' and the keys.
+//    whole launch (state read once, written once).  Per chunk: the state goes through LDS as a bf16 hi|lo
+//    MFMA operand; four waves form W S and Vn for one 16-token tile each, four form Q' S and O for one tile
+//    each; then every wave updates its rows from Vn.  The operands of the next two chunks are in flight while
+//    the current one is computed; each step issues the loads of the chunk two ahead in four parts spread
+//    over its own work.  Workgroup ids put the 8 column blocks of a head on one XCD so that they share that
+//    XCD's L2 copy of W, Q' and the keys.
 //
 // Precision: every product that feeds the state goes through split bf16 (hi + lo, three MFMAs, ~2^-17
 // relative), so the chunked state matches the fp32 sequential rule to ~1e-5.  So does Q' S in the
@@ -50,8 +51,9 @@ __device__ __forceinline__ void load8(const float* p, float* v) {
 // exact per-lane order of the state pass's MFMA operands, so that the state pass loads each lane's
 // fragment with one 16-byte access and converts nothing (lane = 16 grp + m):
 struct ChunkWs {
-    u16* Wf;    // [B, Hv, NC][4 rt][8 w][64 lane][8]: W[16 rt + m][16 w + 4 grp + j], hi j < 4, then lo
-    u16* Qf;    // the same for Q'
+    u16* Wf;    // [B, Hv, NC][4 rt][8 n][64 lane][8]: W[16 rt + m][16 n + 4 grp + j], hi j < 4, then lo
+    u16* Qf;    // the same for Q'; in the layer (Q' in bf16 alone) [B, Hv, NC][4 rt][4 s][64 lane][8]:
+                //   Q'[16 rt + m][32 s + 16 (j / 4) + 4 grp + j % 4] (hi)
     u16* Kf;    // [B, Hv, NC][8 w][2 s][2 plane][64 lane][8]: Kt[16 w + m][32 s + 8 grp + j], plane 0 hi, 1 lo
     float* U;   // [B, Hv, NC][4 mi][DV / 16 n][64 lane][4]: U[16 mi + 4 grp + i][16 n + m] (the prep pass's
                 //   MFMA C order: one 16-byte store per lane; the state pass reads 8 contiguous bytes)
@@ -507,10 +509,10 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
         const size_t f8 = ((size_t)(mi * 8 + n) * 64 + lane) * 8;
         *reinterpret_cast<u16x8*>(Wf + f8) = fw;
         if constexpr (FUSED) {
-            // the layer: Q' in bf16 alone (it only feeds the output), row tiles in pairs so that the state pass
-            // reads two of them per 16-byte load: [mi / 2][n][lane][mi % 2][4]
+            // the layer: Q' in bf16 alone (it only feeds the output).  Column tiles 2 s and 2 s + 1 fill the two
+            // halves of one 16-byte fragment, k-slice s of the state pass's 16x16x32 operand
             const u16x4 qh4 = {fq[0], fq[1], fq[2], fq[3]};
-            *reinterpret_cast<u16x4*>(Qf + ((size_t)((mi >> 1) * 8 + n) * 64 + lane) * 8 + (mi & 1) * 4) = qh4;
+            *reinterpret_cast<u16x4*>(Qf + ((size_t)(mi * 4 + (n >> 1)) * 64 + lane) * 8 + 4 * (n & 1)) = qh4;
         } else {
             *reinterpret_cast<u16x8*>(Qf + f8) = fq;
         }
@@ -545,63 +547,42 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
 
 // ------------------------------------------------------------------------------------------------
 // chunk_state_kernel: grid (Hv * DV / 16, B), 512 threads.  blockIdx.x = cb * Hv + h.
+//
+// Wave w holds state rows 16 w .. 16 w + 15 of the workgroup's 16 columns in an MFMA accumulator for the
+// whole launch.  Per chunk, with the chunk's initial state S in LDS as the B operand of a 16x16x32 MFMA:
+//   phase 1: waves 0-3 form W S for token tile w (K = 128: four k-slices, split bf16, three MFMAs each)
+//            and put Vn = U - W S into LDS; waves 4-7 form Q' S for token tile w - 4 and store
+//            O = O_intra + Q' S.
+//   phase 2: every wave updates its rows, S <- e^{G_last} S + (K e^{G_last - G})^T Vn, and puts them into LDS
+//            for the next chunk.
+// A barrier ends each phase.  Splitting phase 1 by token tile keeps each product whole in one accumulator,
+// so LDS carries the state (8 KB written per chunk) and Vn (4 KB) but no partial sums.
 // ------------------------------------------------------------------------------------------------
-typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-// v_mfma_f32_16x16x16_bf16: lane l holds A[l % 16][4 (l / 16) + j] and B[4 (l / 16) + j][l % 16], j < 4;
-// C as for the 16x16x32 form.
-__device__ __forceinline__ f32x4 mfma16k16(s16x4 a, s16x4 b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
-}
-struct Split4 {
-    s16x4 h, l;
-};
-__device__ __forceinline__ Split4 split4(const f32x4 v) {
-    Split4 r;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const __bf16 hi = (__bf16)v[j];
-        r.h[j] = __builtin_bit_cast(short, hi);
-        r.l[j] = __builtin_bit_cast(short, (__bf16)(v[j] - (float)hi));
-    }
-    return r;
-}
-__device__ __forceinline__ f32x4 mfma3k16(const Split4& a, const Split4& b, f32x4 c) {
-    c = mfma16k16(a.l, b.h, c);
-    c = mfma16k16(a.h, b.l, c);
-    return mfma16k16(a.h, b.h, c);
-}
-
-// One chunk's operands for one lane (about 50 VGPRs, so three chunks fit in registers).
-template <bool QSPLIT>
+// One chunk's operands for one lane of a W wave (W_ROLE) or a Q' wave.  QSPLIT: Q' as bf16 hi and lo (the
+// recurrence-only op, whose fp32 output is held to 1e-3), else hi alone (the layer, whose output is bf16
+// after the gated norm; Q' does not enter the state).
+template <bool QSPLIT, bool W_ROLE>
 struct StateOps {
-    u16x8 w[4];                  // W [16 rt + m][16 wave + 4 grp + j]: hi j < 4, then lo
-    u16x8 q[QSPLIT ? 4 : 2];     // Q' at the same place; without the lo half, row tiles 2 i and 2 i + 1 in q[i]
+    static constexpr int NA = (W_ROLE || QSPLIT) ? 8 : 4;
+    u16x8 a[NA];          // the token tile's W (or Q') fragments: [n] hi | lo, or (Q' hi alone) [s]
     u16x8 kh[2], kl[2];   // Kt [16 wave + m][32 s + 8 grp + j] (hi / lo)
+    f32x4 uo;             // U (or the intra-chunk output) of the token tile, C layout
     float glast;          // G of the chunk's last token
-    float2 u;             // U[2 p + e][n0 + col], e < 2
-    float2 o;             // the intra-chunk output at the same places
 };
 
-__device__ __forceinline__ Split4 frag4(const u16x8 v) {
-    Split4 r;
-    r.h = __builtin_bit_cast(s16x4, __builtin_shufflevector(v, v, 0, 1, 2, 3));
-    r.l = __builtin_bit_cast(s16x4, __builtin_shufflevector(v, v, 4, 5, 6, 7));
-    return r;
-}
-
-// QSPLIT: Q' as bf16 hi and lo (the recurrence-only op, whose fp32 output is held to 1e-3), or hi alone (the
-// layer, whose output is bf16 after the gated norm; Q' does not enter the state)
 template <int DK, int DV, bool QSPLIT>
 __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs ws) {
     static_assert(DK == 128 && DV == 128, "chunked path is specialised for 128-wide heads");
-    constexpr int NWV = 8, RS = CK + 4;
-    // per-wave partials of W S and Q' S, [column][token] (a lane's four tokens are one 16-byte store)
-    __shared__ __attribute__((aligned(16))) float red[NWV][2][16][RS];
+    // The chunk's initial state as the B operand of W S and Q' S: k-slice s, plane (hi, lo), lane (m, grp),
+    // slot j holds S[32 s + 16 (j / 4) + 4 grp + j % 4][n0 + m] (the k order of the W and Q' fragments), so
+    // wave w's accumulator is slots 4 (w % 2) .. 4 (w % 2) + 3 of slice w / 2, one 8-byte store per plane.
+    __shared__ __attribute__((aligned(16))) u16 sS[4][2][64][8];
     // Vn split into bf16 hi | lo, in the update's B-operand order: token t at [t / 32][(t / 8) % 4][col][t % 8]
     __shared__ __attribute__((aligned(16))) u16 vnf[2][4][16][16];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int Hv = a.Hv, T = a.T;
     const int h = blockIdx.x % Hv, cb = blockIdx.x / Hv, b = blockIdx.y;
     const int n0 = 16 * cb;
@@ -609,159 +590,174 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
     if ((unsigned)slot >= (unsigned)a.max_slots) return;
     const int m = lane & 15, grp = lane >> 4;
     const int NC = (T + CK - 1) / CK;
-    const int col = tid & 15, p = tid >> 4;  // Vn / output elements of this thread: tokens 2p, 2p + 1
+    const int rt = wave & 3;  // phase 1 token tile
 
-    // This wave's 16 state rows 16 w + 4 grp + i (i < 4), column n0 + m: the C layout of the 16x16 MFMA,
-    // so the update accumulates in place.  As the B operand of W S (16x16x16: k-slot j of lane (m, grp)
-    // is row 4 grp + j of the wave's 16) the same four values serve directly.
+    // this wave's 16 state rows 16 w + 4 grp + i (i < 4), column n0 + m: the C layout of the 16x16 MFMA, so
+    // the update accumulates in place
     float* S = a.state + ((size_t)slot * Hv + h) * DK * DV;
     f32x4 st;
 #pragma unroll
     for (int i = 0; i < 4; ++i) st[i] = S[(size_t)(16 * wave + 4 * grp + i) * DV + n0 + m];
-
-    // One chunk's operands, loaded in four parts (W; Q'; keys and G; U and o).  A step issues the parts of the
-    // chunk two ahead at four points of its own work, so the address units stream them while it computes
-    // rather than stalling every wave on a burst of loads between steps.
-    auto load_part = [&](int c, StateOps<QSPLIT>& op, auto part) {
-        constexpr int P = decltype(part)::value;
-        const size_t hc = ((size_t)b * Hv + h) * ws.NC + c;
-        if constexpr (P == 0 || P == 1) {
-            const u16* src = (P == 0 ? ws.Wf : ws.Qf) + hc * CK * DK * 2 + ((size_t)wave * 64 + lane) * 8;
-            constexpr int NL = P == 0 || QSPLIT ? 4 : 2;
+    auto put_state = [&]() {
+        u16x4 hi, lo;
 #pragma unroll
-            for (int rt = 0; rt < NL; ++rt) {
-                const u16x8 v = *reinterpret_cast<const u16x8*>(src + (size_t)rt * 8 * 64 * 8);
-                if constexpr (P == 0) op.w[rt] = v;
-                else op.q[rt] = v;
+        for (int i = 0; i < 4; ++i) {
+            const __bf16 x = (__bf16)st[i];
+            hi[i] = __builtin_bit_cast(u16, x);
+            lo[i] = (u16)bf16_bits(st[i] - (float)x);
+        }
+        *reinterpret_cast<u16x4*>(&sS[wave >> 1][0][lane][4 * (wave & 1)]) = hi;
+        *reinterpret_cast<u16x4*>(&sS[wave >> 1][1][lane][4 * (wave & 1)]) = lo;
+    };
+    put_state();
+
+    // The two roles run the same sequence of barriers with their own operands, each as straight-line code
+    // (no role test between a load and its use).
+    auto run = [&](auto role) {
+        constexpr bool WR = decltype(role)::value;
+        using Ops = StateOps<QSPLIT, WR>;
+        constexpr int NA = Ops::NA;
+        const u16* abase = (WR ? ws.Wf : ws.Qf) + (size_t)rt * NA * 512 + lane * 8;
+        const float* uobase = (WR ? ws.U : ws.O) + ((size_t)(rt * (DV / 16) + cb) * 64 + lane) * 4;
+        float* obase = a.o + ((size_t)b * T * Hv + h) * DV + n0 + m;
+
+        // One chunk's operands, loaded in four parts; a step issues the parts of the chunk two ahead at four
+        // points of its own work, so the address units stream them while it computes.
+        auto load_part = [&](int c, Ops& op, auto part) {
+            constexpr int P = decltype(part)::value;
+            const size_t hc = ((size_t)b * Hv + h) * ws.NC + c;
+            if constexpr (P == 0 || P == 1) {
+                const u16* src = abase + hc * CK * DK * 2;
+#pragma unroll
+                for (int i = P * NA / 2; i < (P + 1) * NA / 2; ++i)
+                    op.a[i] = *reinterpret_cast<const u16x8*>(src + (size_t)i * 512);
+            } else if constexpr (P == 2) {
+                const size_t kf = hc * DK * CK * 2 + (size_t)wave * 2 * 1024 + lane * 8;
+#pragma unroll
+                for (int s = 0; s < 2; ++s) {
+                    op.kh[s] = *reinterpret_cast<const u16x8*>(ws.Kf + kf + (size_t)s * 1024);
+                    op.kl[s] = *reinterpret_cast<const u16x8*>(ws.Kf + kf + (size_t)s * 1024 + 512);
+                }
+            } else {
+                op.uo = *reinterpret_cast<const f32x4*>(uobase + hc * CK * DV);
+                op.glast = ws.G[hc * CK + CK - 1];
             }
-        } else if constexpr (P == 2) {
-            const size_t kf = hc * DK * CK * 2 + (size_t)wave * 2 * 1024 + lane * 8;
+        };
+        using P0 = std::integral_constant<int, 0>;
+        using P1 = std::integral_constant<int, 1>;
+        using P2 = std::integral_constant<int, 2>;
+        using P3 = std::integral_constant<int, 3>;
+        auto load_ops = [&](int c, Ops& op) {
+            load_part(c, op, P0{});
+            load_part(c, op, P1{});
+            load_part(c, op, P2{});
+            load_part(c, op, P3{});
+        };
+        // part P of the loads into `nxt` (when LD), fenced so that the scheduler keeps it at this point
+        auto issue = [&](int cn, Ops& nxt, auto ld, auto part) {
+            if constexpr (decltype(ld)::value) {
+                __builtin_amdgcn_sched_barrier(0);
+                load_part(cn, nxt, part);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        };
+
+        // FULL: the chunk has CK tokens (no per-token bounds test)
+        // LD: load chunk cn into nxt along the way
+        auto step = [&](int c, const Ops& cur, auto full, int cn, Ops& nxt, auto ld) {
+            constexpr bool FULL = decltype(full)::value;
+            const int t0 = c * CK, len = FULL ? CK : min(CK, T - t0);
+            issue(cn, nxt, ld, P0{});
+
+            // phase 1: W S (Q' S) for token tile rt over the four k-slices of the state
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const Split8 Sb{__builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(&sS[s][0][lane][0])),
+                                __builtin_bit_cast(bf16x8, *reinterpret_cast<const u16x8*>(&sS[s][1][lane][0]))};
+                if constexpr (NA == 8) {
+                    // k-blocks 2 s and 2 s + 1 (four hi, four lo each) joined into the slice's hi and lo
+                    const u16x8 x = cur.a[2 * s], y = cur.a[2 * s + 1];
+                    const Split8 A{__builtin_bit_cast(bf16x8, __builtin_shufflevector(x, y, 0, 1, 2, 3, 8, 9, 10, 11)),
+                                   __builtin_bit_cast(bf16x8, __builtin_shufflevector(x, y, 4, 5, 6, 7, 12, 13, 14, 15))};
+                    acc = mfma3(A, Sb, acc);
+                } else {
+                    const bf16x8 qa = __builtin_bit_cast(bf16x8, cur.a[s]);
+                    acc = mfma16(qa, Sb.h, mfma16(qa, Sb.l, acc));
+                }
+            }
+            if constexpr (WR) {
+                // Vn = U - W S for tokens 16 rt + 4 grp + i of column n0 + m
+                u16x4 hi, lo;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const float v = cur.uo[i] - acc[i];
+                    const __bf16 x = (__bf16)v;
+                    hi[i] = __builtin_bit_cast(u16, x);
+                    lo[i] = (u16)bf16_bits(v - (float)x);
+                }
+                const int t = 16 * rt + 4 * grp;
+                u16* vp = &vnf[t >> 5][(t >> 3) & 3][m][t & 7];
+                *reinterpret_cast<u16x4*>(vp) = hi;
+                *reinterpret_cast<u16x4*>(vp + 8) = lo;
+            } else {
+                // O = O_intra + Q' S for the same tokens
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int t = 16 * rt + 4 * grp + i;
+                    if (FULL || t < len) obase[(size_t)(t0 + t) * Hv * DV] = cur.uo[i] + acc[i];
+                }
+            }
+            issue(cn, nxt, ld, P1{});
+            lds_barrier();
+
+            // phase 2: S <- e^{G_last} S + (K e^{G_last - G})^T Vn
+            issue(cn, nxt, ld, P2{});
+            const float egl = __expf(cur.glast);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) st[i] *= egl;
 #pragma unroll
             for (int s = 0; s < 2; ++s) {
-                op.kh[s] = *reinterpret_cast<const u16x8*>(ws.Kf + kf + (size_t)s * 1024);
-                op.kl[s] = *reinterpret_cast<const u16x8*>(ws.Kf + kf + (size_t)s * 1024 + 512);
+                const u16x8 vh = *reinterpret_cast<const u16x8*>(&vnf[s][grp][m][0]);
+                const u16x8 vl = *reinterpret_cast<const u16x8*>(&vnf[s][grp][m][8]);
+                const Split8 kt{__builtin_bit_cast(bf16x8, cur.kh[s]), __builtin_bit_cast(bf16x8, cur.kl[s])};
+                const Split8 vs{__builtin_bit_cast(bf16x8, vh), __builtin_bit_cast(bf16x8, vl)};
+                st = mfma3(kt, vs, st);
             }
-            op.glast = ws.G[hc * CK + CK - 1];
-        } else {
-            // U and the intra-chunk output for tokens 2p, 2p + 1 of column n0 + col: token tile p / 8, lane
-            // 16 ((p / 2) % 4) + col, slots 2 (p % 2) + e
-            const size_t uo = hc * CK * DV + ((size_t)((p >> 3) * (DV / 16) + cb) * 64 + 16 * ((p >> 1) & 3) + col) * 4 +
-                              2 * (p & 1);
-            op.u = *reinterpret_cast<const float2*>(ws.U + uo);
-            op.o = *reinterpret_cast<const float2*>(ws.O + uo);
-        }
-    };
-    using P0 = std::integral_constant<int, 0>;
-    using P1 = std::integral_constant<int, 1>;
-    using P2 = std::integral_constant<int, 2>;
-    using P3 = std::integral_constant<int, 3>;
-    auto load_ops = [&](int c, StateOps<QSPLIT>& op) {
-        load_part(c, op, P0{});
-        load_part(c, op, P1{});
-        load_part(c, op, P2{});
-        load_part(c, op, P3{});
-    };
-    // part P of the loads into `nxt` (when LD), fenced so that the scheduler keeps it at this point
-    auto issue = [&](int cn, StateOps<QSPLIT>& nxt, auto ld, auto part) {
-        if constexpr (decltype(ld)::value) {
-            __builtin_amdgcn_sched_barrier(0);
-            load_part(cn, nxt, part);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
+            put_state();
+            issue(cn, nxt, ld, P3{});
+            lds_barrier();
+        };
 
-    // FULL: the chunk has CK tokens (no per-token bounds test)
-    // LD: load chunk cn into nxt along the way
-    auto step = [&](int c, const StateOps<QSPLIT>& cur, auto full, int cn, StateOps<QSPLIT>& nxt, auto ld) {
-        constexpr bool FULL = decltype(full)::value;
-        const int t0 = c * CK, len = FULL ? CK : min(CK, T - t0);
-        const size_t row0 = (size_t)b * T + t0;
-        issue(cn, nxt, ld, P0{});
-
-        // W S and Q' S over this wave's 16 state rows
-        const Split4 Sb = split4(st);
-#pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-            const f32x4 pw = mfma3k16(frag4(cur.w[rt]), Sb, z);
-            f32x4 pq;
-            if constexpr (QSPLIT) {
-                pq = mfma3k16(frag4(cur.q[rt]), Sb, z);
-            } else {
-                const u16x8 v = cur.q[rt >> 1];
-                const s16x4 qa = __builtin_bit_cast(s16x4, (rt & 1) ? __builtin_shufflevector(v, v, 4, 5, 6, 7)
-                                                                    : __builtin_shufflevector(v, v, 0, 1, 2, 3));
-                pq = mfma16k16(qa, Sb.h, mfma16k16(qa, Sb.l, z));
+        // Operands two chunks ahead: a 3-slot ring, unrolled so that every slot is a fixed set of registers.
+        // The main loop runs over whole triples of full chunks with no conditional memory operation (loads
+        // past the last chunk re-read the last chunk), so the only waits are for the oldest slot's loads;
+        // the remaining (at most 3, the last possibly partial) chunks follow.
+        using Full = std::integral_constant<bool, true>;
+        using Part = std::integral_constant<bool, false>;
+        using Yes = std::integral_constant<bool, true>;
+        using No = std::integral_constant<bool, false>;
+        const int NCF = T / CK;  // full chunks
+        Ops A, B, C;
+        load_ops(0, A);
+        load_ops(min(1, NC - 1), B);
+        lds_barrier();  // the initial state is in LDS
+        int c = 0;
+        for (; c + 3 <= NCF; c += 3) {
+            step(c, A, Full{}, min(c + 2, NC - 1), C, Yes{});
+            step(c + 1, B, Full{}, min(c + 3, NC - 1), A, Yes{});
+            step(c + 2, C, Full{}, min(c + 4, NC - 1), B, Yes{});
+        }
+        if (c < NC) {
+            step(c, A, Part{}, min(c + 2, NC - 1), C, Yes{});
+            if (c + 1 < NC) {
+                step(c + 1, B, Part{}, 0, A, No{});
+                if (c + 2 < NC) step(c + 2, C, Part{}, 0, A, No{});
             }
-            *reinterpret_cast<f32x4*>(&red[wave][0][m][16 * rt + 4 * grp]) = pw;
-            *reinterpret_cast<f32x4*>(&red[wave][1][m][16 * rt + 4 * grp]) = pq;
         }
-        issue(cn, nxt, ld, P1{});
-        lds_barrier();
-
-        // Vn = U - W S and O += Q' S for tokens 2p, 2p + 1 of column n0 + col
-        {
-            float2 sw = make_float2(0.f, 0.f), sq = sw;
-#pragma unroll
-            for (int w = 0; w < NWV; ++w) {
-                const float2 x = *reinterpret_cast<const float2*>(&red[w][0][col][2 * p]);
-                const float2 y = *reinterpret_cast<const float2*>(&red[w][1][col][2 * p]);
-                sw.x += x.x, sw.y += x.y;
-                sq.x += y.x, sq.y += y.y;
-            }
-            const float v0 = cur.u.x - sw.x, v1 = cur.u.y - sw.y;
-            const __bf16 h0 = (__bf16)v0, h1 = (__bf16)v1;
-            const int t = 2 * p;
-            u16* vp = &vnf[t >> 5][(t >> 3) & 3][col][t & 7];
-            *reinterpret_cast<uint32_t*>(vp) = bf16_bits((float)h0) | (bf16_bits((float)h1) << 16);
-            *reinterpret_cast<uint32_t*>(vp + 8) = bf16_bits(v0 - (float)h0) | (bf16_bits(v1 - (float)h1) << 16);
-            float* op = a.o + ((row0 + t) * Hv + h) * DV + n0 + col;
-            if (FULL || t < len) op[0] = cur.o.x + sq.x;
-            if (FULL || t + 1 < len) op[(size_t)Hv * DV] = cur.o.y + sq.y;
-        }
-        issue(cn, nxt, ld, P2{});
-        lds_barrier();
-
-        // S <- e^{G_last} S + (K e^{G_last - G})^T Vn
-        const float egl = __expf(cur.glast);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) st[i] *= egl;
-#pragma unroll
-        for (int s = 0; s < 2; ++s) {
-            const u16x8 vh = *reinterpret_cast<const u16x8*>(&vnf[s][grp][m][0]);
-            const u16x8 vl = *reinterpret_cast<const u16x8*>(&vnf[s][grp][m][8]);
-            const Split8 kt{__builtin_bit_cast(bf16x8, cur.kh[s]), __builtin_bit_cast(bf16x8, cur.kl[s])};
-            const Split8 vs{__builtin_bit_cast(bf16x8, vh), __builtin_bit_cast(bf16x8, vl)};
-            st = mfma3(kt, vs, st);
-        }
-        issue(cn, nxt, ld, P3{});
     };
-
-    // Operands two chunks ahead: a 3-slot ring, unrolled so that every slot is a fixed set of registers.
-    // The main loop runs over whole triples of full chunks with no conditional memory operation (loads
-    // past the last chunk re-read the last chunk), so the only waits are for the oldest slot's loads;
-    // the remaining (at most 3, the last possibly partial) chunks follow.
-    using Full = std::integral_constant<bool, true>;
-    using Part = std::integral_constant<bool, false>;
-    using Yes = std::integral_constant<bool, true>;
-    using No = std::integral_constant<bool, false>;
-    const int NCF = T / CK;  // full chunks
-    StateOps<QSPLIT> A, B, C;
-    load_ops(0, A);
-    load_ops(min(1, NC - 1), B);
-    int c = 0;
-    for (; c + 3 <= NCF; c += 3) {
-        step(c, A, Full{}, min(c + 2, NC - 1), C, Yes{});
-        step(c + 1, B, Full{}, min(c + 3, NC - 1), A, Yes{});
-        step(c + 2, C, Full{}, min(c + 4, NC - 1), B, Yes{});
-    }
-    if (c < NC) {
-        step(c, A, Part{}, min(c + 2, NC - 1), C, Yes{});
-        if (c + 1 < NC) {
-            step(c + 1, B, Part{}, 0, A, No{});
-            if (c + 2 < NC) step(c + 2, C, Part{}, 0, A, No{});
-        }
-    }
+    if (wave < 4) run(std::true_type{});
+    else run(std::false_type{});
 
 #pragma unroll
     for (int i = 0; i < 4; ++i) S[(size_t)(16 * wave + 4 * grp + i) * DV + n0 + m] = st[i];
