@@ -612,7 +612,9 @@ __global__ __launch_bounds__(512) void chunk_state_kernel(DeltaArgs a, ChunkWs w
     put_state();
 
     // The two roles run the same sequence of barriers with their own operands, each as straight-line code
-    // (no role test between a load and its use).
+    // (no role test between a load and its use).  The role is uniform over a wave (the wave index is a
+    // scalar), and both loops pass the same two barriers per chunk for the same chunk count, so every wave
+    // of the workgroup meets every barrier.
     auto run = [&](auto role) {
         constexpr bool WR = decltype(role)::value;
         using Ops = StateOps<QSPLIT, WR>;
