@@ -99,6 +99,7 @@ struct gdn_layer {
     float* o = nullptr;       // [max_tokens, Vd]
     u16* y = nullptr;         // [max_tokens, Vd]
     float* ab = nullptr;      // [kAbSplits, 64, 2 nv] partial a | b of the decode in_proj
+    float* ss = nullptr;      // [kGnormMaxM, nv, kMixerSplit] partial sums of squares of a split-head launch
     void* chunk_ws = nullptr;
     size_t chunk_ws_bytes = 0;
 
@@ -234,6 +235,12 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, void* 
     const bool frag = M <= 64;
     // the fused mixer writes y straight into W_FRAG layout when it produces every row
     const bool y_frag = frag && ng == 1 && grp[0].T <= kFusedMaxT;
+    // single-token launches of at most 64 (sequence, v-head) pairs would leave most CUs idle with one
+    // workgroup per head: each head's state is split over kMixerSplit workgroups, and the gated RMSNorm
+    // moves into the out_proj (bf16 weights, 128-wide heads)
+    const bool split_heads = y_frag && grp[0].T == 1 && M * nv <= 64 && M <= gdn::kGnormMaxM &&
+                             d.head_k_dim == 128 && d.head_v_dim == 128 && L->wfmt == GDN_WEIGHTS_BF16 &&
+                             (Vd == 4096 || Vd == 2048) && L->NP % 4 == 0;
     // decode: q | k | v | z over workgroups balanced on the CUs, a | b as partial sums for the mixer
     const bool split_ab = frag && gdn::in_proj_decode_supported(L->CD + Vd, L->d.hidden);
     bool ab_split = false;
@@ -265,6 +272,7 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, void* 
             a.eps = d.rms_norm_eps;
             a.rec_state = L->rec, a.conv_state = L->conv, a.conv_pos = L->conv_pos;
             a.y = y_frag ? L->y : L->y + r0 * Vd, a.y_frag = y_frag ? 1 : 0, a.o_tap = nullptr;
+            if (split_heads) a.o_tap = L->o, a.ss_part = L->ss;
             a.ab = ab_split ? L->ab + r0 * 2 * nv : nullptr, a.ab_splits = kAbSplits;
             a.ab_stride = (size_t)M * 2 * nv;
             HIP_OK(gdn::launch_mixer(a, d.head_k_dim, d.head_v_dim, st));
@@ -296,7 +304,16 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, void* 
         }
     }
     if (ev[2]) HIP_OK(hipEventRecord(ev[2], st));
-    HIP_OK(out_proj_rows(L, L->y, y_frag ? gdn::W_FRAG : gdn::W_ROW, M, out, out_kind, st));
+    if (split_heads) {
+        gdn::GnormArgs ga{};
+        ga.o = L->o, ga.ss = L->ss, ga.z = L->P + L->CD, ga.ldz = L->NP, ga.norm_w = L->norm_w;
+        ga.eps = d.rms_norm_eps, ga.nv = nv, ga.dv = d.head_v_dim;
+        ga.w = L->w_out, ga.M = M, ga.N = d.hidden, ga.K = Vd, ga.y = out, ga.ldy = d.hidden;
+        ga.conv_pos = L->conv_pos, ga.slot_ids = grp[0].slots, ga.max_slots = L->max_slots;
+        HIP_OK(gdn::launch_out_proj_gnorm(ga, out_kind, st));
+    } else {
+        HIP_OK(out_proj_rows(L, L->y, y_frag ? gdn::W_FRAG : gdn::W_ROW, M, out, out_kind, st));
+    }
     if (ev[3]) {
         HIP_OK(hipEventRecord(ev[3], st));
         ++L->prof_calls;
@@ -449,7 +466,7 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
         L->x_ws = share->x_ws, L->x_frag = share->x_frag, L->out_ws = share->out_ws, L->P = share->P;
         L->qn = share->qn, L->kn = share->kn, L->v = share->v, L->g = share->g, L->beta = share->beta;
         L->o = share->o, L->y = share->y, L->chunk_ws = share->chunk_ws, L->chunk_ws_bytes = share->chunk_ws_bytes;
-        L->ab = share->ab;
+        L->ab = share->ab, L->ss = share->ss;
     } else {
         take(L->alloc(&L->x_ws, MT * H, true));
         take(L->alloc(&L->x_frag, gdn::frag_elems(64, H), true));
@@ -463,6 +480,7 @@ int create_layer(const gdn_dims* dims, const gdn_weights* w, int max_slots, int 
         take(L->alloc(&L->o, MT * L->Vd, true));
         take(L->alloc(&L->y, std::max(MT * L->Vd, gdn::frag_elems(64, L->Vd)), true));  // W_FRAG y pads rows to 16
         take(L->alloc(&L->ab, (size_t)kAbSplits * 64 * 2 * nv, true));
+        take(L->alloc(&L->ss, (size_t)gdn::kGnormMaxM * nv * gdn::kMixerSplit, true));
         if (max_tokens > kFusedMaxT && gdn::delta_chunked_supported(dk, dv)) {
             // chunked-prefill workspace for the worst launch: sequences of T > kFusedMaxT tokens with
             // at most max_tokens rows in all hold at most max_tokens / 64 + max_tokens / 65 + 1 chunks

@@ -289,6 +289,11 @@ struct MixerArgs {
     u16* y;                 // [M, nv * dv] bf16 gated RMSNorm output
     int y_frag;             // 1: y in W_FRAG layout (rows padded to 16; M <= 64), 0: row-major
     float* o_tap;           // optional [M, nv * dv] recurrence output (nullptr: not written)
+    // split heads (single-token launches of at most 64 sequence-heads, 128-wide heads): when set, each
+    // v-head runs as kMixerSplit workgroups of dv / kMixerSplit state columns that write the recurrence
+    // output to o_tap and their partial sums of its squares to ss_part [M, nv, kMixerSplit] instead of y,
+    // and leave conv_pos to launch_out_proj_gnorm (see there)
+    float* ss_part;
     // optional: a | b as ab_splits partial sums, slice s row m at ab[s * ab_stride + m * 2 nv] (then
     // the a | b columns of P are not read)
     const float* ab;
@@ -298,6 +303,29 @@ struct MixerArgs {
 // Fused mixer of a decode-sized launch: single-token launches one workgroup of 256 threads per (sequence,
 // v-head); longer ones one workgroup of 256 R threads per (sequence, k-head group), R = nv / nk <= 4.
 hipError_t launch_mixer(const MixerArgs& a, int dk, int dv, hipStream_t stream);
+constexpr int kMixerSplit = 4;  // workgroups per v-head of a split-head launch
+
+// The out_proj of a split-head mixer launch (MixerArgs::ss_part): the gated RMSNorm of its rows, then the
+// projection against bf16 W_FRAG weights; it also advances the ring positions of the launch's sequences
+// by the one token, which the split mixer leaves to it.
+struct GnormArgs {
+    const float* o;        // [M, K] recurrence output (K = nv dv)
+    const float* ss;       // [M, nv, kMixerSplit] partial sums of squares of o per head and column slice
+    const float* z;        // gate rows: row m at z + m ldz
+    int ldz;
+    const float* norm_w;   // [dv]
+    float eps;
+    int nv, dv;
+    const u16* w;          // [N, K] bf16, W_FRAG
+    int M, N, K;
+    void* y;               // [M, N] row-major, bf16 or fp32 by the out kind
+    int ldy;
+    int* conv_pos;         // [slots, nv]
+    const int* slot_ids;   // [M] (nullptr: identity)
+    int max_slots;
+};
+constexpr int kGnormMaxM = 4, kGnormMaxK = 4096;
+hipError_t launch_out_proj_gnorm(const GnormArgs& a, int out_kind, hipStream_t stream);
 
 struct FrontArgs {
     const float* P;

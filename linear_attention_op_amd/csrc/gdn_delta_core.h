@@ -14,7 +14,8 @@
 
 namespace gdn {
 
-template <int DK, int DV, int NTH = 256>
+// LD: the row stride of the state in memory (a tile of DV columns out of LD-wide rows when DV < LD).
+template <int DK, int DV, int NTH = 256, int LD = DV>
 struct DeltaTile {
     static constexpr int CG = DV / 4;
     static constexpr int RG = NTH / CG;
@@ -31,22 +32,22 @@ struct DeltaTile {
     }
     // The state is streamed: read once and written once per launch, so both directions use
     // non-temporal accesses and do not displace the projection weights from the caches.  Row i of the
-    // thread is at S + RG DV i (the same for every thread: a scalar base) + rg DV + 4 cg (one 32-bit offset
+    // thread is at S + RG LD i (the same for every thread: a scalar base) + rg LD + 4 cg (one 32-bit offset
     // per thread), so the 16 accesses share a single address register.
     __device__ __forceinline__ void load(const float* S) {
-        const unsigned off = (unsigned)(rg * DV + 4 * cg);
+        const unsigned off = (unsigned)(rg * LD + 4 * cg);
 #pragma unroll
         for (int i = 0; i < RPT; ++i) {
-            const float* row = S + (size_t)RG * DV * i;
+            const float* row = S + (size_t)RG * LD * i;
             const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(row + off));
             s[i] = make_float4(v[0], v[1], v[2], v[3]);
         }
     }
     __device__ __forceinline__ void store(float* S) const {
-        const unsigned off = (unsigned)(rg * DV + 4 * cg);
+        const unsigned off = (unsigned)(rg * LD + 4 * cg);
 #pragma unroll
         for (int i = 0; i < RPT; ++i) {
-            float* row = S + (size_t)RG * DV * i;
+            float* row = S + (size_t)RG * LD * i;
             const f32x4 v = {s[i].x, s[i].y, s[i].z, s[i].w};
             __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(row + off));
         }

@@ -572,6 +572,67 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x
                                                  K >> 5, red);
 }
 
+// Decode out_proj of a split-head mixer launch (GnormArgs).  Each wave first issues every weight fragment
+// of its k-share (SPW k-steps, as gemv_block_allw).  While they are in flight the workgroup forms the gated
+// RMSNorm of the M <= 4 rows, y = o rsqrt(sum_head(o^2) / dv + eps) w silu(z) in bf16, into LDS: 8 columns
+// of one head per thread and pass, the head's sum of squares from the mixer's per-slice partials (HF
+// Qwen3_5RMSNormGated, HF:167-184, as the fused mixer computes it).  The GEMV then reads its activation
+// fragments from LDS.  Workgroup 0 advances the ring position of every (sequence, v-head) by one token.
+template <int NW, int SPW, int OUT>
+__global__ __launch_bounds__(NW * 64) void out_proj_gnorm_kernel(GnormArgs a) {
+    static_assert(kMixerSplit == 4, "one float4 of partial sums per (row, head)");
+    __shared__ __attribute__((aligned(16))) u16 xs[kGnormMaxM][kGnormMaxK + 8];
+    __shared__ float red[gemv_red_floats<1, 1, NW>()];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int M = a.M, K = a.K, KQ = K >> 5, NT = (a.N + 15) >> 4;
+    const int n0 = blockIdx.x * 16, kq0 = wave * SPW;
+
+    const u16* wp = a.w + ((size_t)min(n0 >> 4, NT - 1) * KQ + kq0) * 512 + lane * 8;
+    bf16x8 wb[SPW];
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) wb[s] = ldw(wp + (size_t)s * 512);
+
+    for (int e = 8 * tid; e < M * K; e += 8 * NW * 64) {
+        const int m = e / K, c = e - m * K, hh = c / a.dv;
+        const float* op = a.o + (size_t)m * K + c;
+        const float* zp = a.z + (size_t)m * a.ldz + c;
+        const float* np = a.norm_w + (c - hh * a.dv);
+        const float4 o0 = *reinterpret_cast<const float4*>(op), o1 = *reinterpret_cast<const float4*>(op + 4);
+        const float4 z0 = *reinterpret_cast<const float4*>(zp), z1 = *reinterpret_cast<const float4*>(zp + 4);
+        const float4 w0 = *reinterpret_cast<const float4*>(np), w1 = *reinterpret_cast<const float4*>(np + 4);
+        const float4 sp = *reinterpret_cast<const float4*>(a.ss + ((size_t)m * a.nv + hh) * kMixerSplit);
+        const float rstd = rsqrtf((sp.x + sp.y + sp.z + sp.w) / (float)a.dv + a.eps);
+        const float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
+        const float zv[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
+        const float nv8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+        u16x8 yv;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) yv[j] = f2bf(ov[j] * rstd * nv8[j] * siluf_(zv[j]));
+        *reinterpret_cast<u16x8*>(&xs[m][c]) = yv;
+    }
+    if (blockIdx.x == 0) {
+        for (int t = tid; t < M * a.nv; t += NW * 64) {
+            const int b = t / a.nv, hh = t - b * a.nv;
+            const int slot = a.slot_ids ? a.slot_ids[b] : b;
+            if ((unsigned)slot < (unsigned)a.max_slots) {
+                int* p = a.conv_pos + (size_t)slot * a.nv + hh;
+                *p = (*p + 1) & 3;
+            }
+        }
+    }
+    __syncthreads();
+
+    f32x4 acc[1][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
+    const bf16x8 zero8 = {};
+#pragma unroll
+    for (int s = 0; s < SPW; ++s) {
+        const bf16x8 xb = r < M ? *reinterpret_cast<const bf16x8*>(&xs[r][32 * (kq0 + s) + 8 * g]) : zero8;
+        acc[0][0] = mfma16(wb[s], xb, acc[0][0]);
+    }
+    gemv_finish<1, 1, NW, OUT>(acc, red, M, a.N, a.y, a.ldy, n0, nullptr);
+}
+
 // Decode in_proj (fragment-layout weights and activations, fp32 out), balanced over the CUs: workgroups
 // [0, G) own NTS row tiles each of the first N1 rows (G = N1 / (16 NTS), chosen ~ one per CU) and write
 // them to P (row stride ldp); the remaining N2 rows (the a | b projection, 64 rows at 9B) are split into
@@ -1153,6 +1214,26 @@ hipError_t launch_quantize_mxint8(const void* w, int N, int K, u8* q, u8* scale,
     else
         hipLaunchKernelGGL(quantize_mxint8_kernel<false>, dim3(rows), dim3(256), 0, stream, (const u16*)w, N, K, q,
                            scale);
+    return hipGetLastError();
+}
+
+hipError_t launch_out_proj_gnorm(const GnormArgs& a, int out_kind, hipStream_t stream) {
+    if (a.M <= 0) return hipSuccess;
+    constexpr int NW = 8;
+    const bool ok = a.M <= kGnormMaxM && a.K <= kGnormMaxK && a.N % 16 == 0 && a.dv % 8 == 0 && a.K % a.dv == 0 &&
+                    a.K == a.nv * a.dv && a.ldz % 4 == 0 && ((uintptr_t)a.o & 15) == 0 && ((uintptr_t)a.z & 15) == 0 &&
+                    ((uintptr_t)a.norm_w & 15) == 0 && ((uintptr_t)a.ss & 15) == 0 && a.conv_pos &&
+                    (out_kind == OUT_F32 || out_kind == OUT_BF16);
+    const int KQ = a.K >> 5;
+    if (!ok || (KQ != NW * 16 && KQ != NW * 8)) return hipErrorInvalidValue;
+    const dim3 grid(a.N / 16), block(NW * 64);
+    if (KQ == NW * 16) {
+        if (out_kind == OUT_F32) hipLaunchKernelGGL((out_proj_gnorm_kernel<NW, 16, OUT_F32>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((out_proj_gnorm_kernel<NW, 16, OUT_BF16>), grid, block, 0, stream, a);
+    } else {
+        if (out_kind == OUT_F32) hipLaunchKernelGGL((out_proj_gnorm_kernel<NW, 8, OUT_F32>), grid, block, 0, stream, a);
+        else hipLaunchKernelGGL((out_proj_gnorm_kernel<NW, 8, OUT_BF16>), grid, block, 0, stream, a);
+    }
     return hipGetLastError();
 }
 

@@ -28,20 +28,27 @@
 namespace gdn {
 
 // PER_HEAD: one workgroup of 256 threads per (v-head, sequence), single-token launches only; else one of
-// 256 R threads per (k-head group, sequence).
-template <int DK, int DV, int R, bool PER_HEAD>
+// 256 R threads per (k-head group, sequence).  NS > 1 (PER_HEAD only): NS workgroups per (v-head,
+// sequence), each owning DV / NS state columns; the recurrence is exact per column, but the gated RMSNorm
+// spans the head, so these workgroups write the output and its partial sums of squares (MixerArgs::ss_part)
+// and the norm runs in the out_proj (launch_out_proj_gnorm), which also advances the ring positions: a
+// workgroup that advanced them here could do so before a sibling of the same head has read them.
+template <int DK, int DV, int R, bool PER_HEAD, int NS = 1>
 __global__ __launch_bounds__(PER_HEAD ? 256 : 256 * R) void mixer_kernel(MixerArgs a) {
+    static_assert(NS == 1 || PER_HEAD, "split heads are single-token workgroups");
     constexpr int HW = PER_HEAD ? 1 : R;     // v-heads of the workgroup
     constexpr int NTH = 256 * HW;
+    constexpr int DVS = DV / NS;             // state columns of the workgroup
     constexpr int CHG = 2 * DK + R * DV;     // channels of the group (a ring entry)
-    constexpr int CHW = 2 * DK + HW * DV;    // channels of the workgroup
+    constexpr int CHW = 2 * DK + HW * DVS;   // channels of the workgroup
     constexpr int CPT = (CHW + NTH - 1) / NTH;
-    using Tile = DeltaTile<DK, DV>;
+    using Tile = DeltaTile<DK, DVS, 256, DV>;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int sub = PER_HEAD ? 0 : tid >> 8, stid = tid & 255, swave = wave & 3;  // v-head of the workgroup
-    const int h = PER_HEAD ? blockIdx.x : blockIdx.x * R + sub, b = blockIdx.y;
-    const int kh = PER_HEAD ? blockIdx.x / R : blockIdx.x;
+    const int cs = PER_HEAD ? blockIdx.x % NS : 0, c0 = cs * DVS;  // column slice of the workgroup
+    const int h = PER_HEAD ? blockIdx.x / NS : blockIdx.x * R + sub, b = blockIdx.y;
+    const int kh = PER_HEAD ? blockIdx.x / NS / R : blockIdx.x;
     const int h0 = PER_HEAD ? h : kh * R;    // first v-head of the workgroup
     const int nv = a.nv, nk = a.nk;
     const int Kd = nk * DK, Vd = nv * DV, CD = 2 * Kd + Vd;
@@ -49,8 +56,8 @@ __global__ __launch_bounds__(PER_HEAD ? 256 : 256 * R) void mixer_kernel(MixerAr
     if ((unsigned)slot >= (unsigned)a.max_slots) return;
     const int T = PER_HEAD ? 1 : a.T;  // per-head workgroups run single-token launches only
 
-    __shared__ float sq[DK], sk[DK], sv[HW][DV];
-    __shared__ float red[HW][4][2][DV];
+    __shared__ float sq[DK], sk[DK], sv[HW][DVS];
+    __shared__ float red[HW][4][2][DVS];
 
     // ---- state-independent loads first: history, taps, the first token's projection values --------
     float* hist = a.conv_state + ((size_t)slot * nk + kh) * CONV_RING * CHG;
@@ -66,7 +73,7 @@ __global__ __launch_bounds__(PER_HEAD ? 256 : 256 * R) void mixer_kernel(MixerAr
         pcol[c] = gch[c] = 0;
         if (ch < CHW) {
             // channel of the group: q | k of kh, then the v channels of this workgroup's v-heads
-            gch[c] = ch < 2 * DK ? ch : 2 * DK + (h0 - kh * R) * DV + (ch - 2 * DK);
+            gch[c] = ch < 2 * DK ? ch : 2 * DK + (h0 - kh * R) * DV + c0 + (ch - 2 * DK);
             pcol[c] = group_col(gch[c], kh, DK, DV, R, Kd);
             tap[c] = a.conv_w[pcol[c]];
 #pragma unroll
@@ -92,14 +99,14 @@ __global__ __launch_bounds__(PER_HEAD ? 256 : 256 * R) void mixer_kernel(MixerAr
     float av, bv;
     load_ab((size_t)b * T, av, bv);
     float4 zv = make_float4(0.f, 0.f, 0.f, 0.f), nw = zv;
-    if (stid < Tile::CG) {
-        zv = *reinterpret_cast<const float4*>(Prow + CD + h * DV + 4 * stid);
-        nw = *reinterpret_cast<const float4*>(a.norm_w + 4 * stid);
+    if (NS == 1 && stid < Tile::CG) {
+        zv = *reinterpret_cast<const float4*>(Prow + CD + h * DV + c0 + 4 * stid);
+        nw = *reinterpret_cast<const float4*>(a.norm_w + c0 + 4 * stid);
     }
     const float negA = a.neg_A[h], dtb = a.dt_bias[h];
 
     // ---- then the states ---------------------------------------------------------------------------
-    float* S = a.rec_state + ((size_t)slot * nv + h) * DK * DV;
+    float* S = a.rec_state + ((size_t)slot * nv + h) * DK * DV + c0;
     Tile st;
     st.init(stid);
     st.load(S);
@@ -151,8 +158,14 @@ __global__ __launch_bounds__(PER_HEAD ? 256 : 256 * R) void mixer_kernel(MixerAr
         const float beta = sigmoidf_(bv);
         const float4 o = st.step(sq, sk, sv[sub], red[sub], rq, rk, pqk * rq * rk, d, beta, lane, swave);
 
-        // gated RMSNorm of this head's o on the first wave of its part (lanes < CG hold all dv columns)
-        if (swave == 0) {
+        // gated RMSNorm of this head's o on the first wave of its part (lanes < CG hold all dv columns);
+        // a column slice of a split head leaves o and its sum of squares to the out_proj
+        if (NS > 1 && swave == 0) {
+            float ss = lane < Tile::CG ? o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w : 0.f;
+            ss = warp_sum(ss);
+            if (lane < Tile::CG) *reinterpret_cast<float4*>(a.o_tap + m * Vd + h * DV + c0 + 4 * lane) = o;
+            if (lane == 0) a.ss_part[(m * nv + h) * NS + cs] = ss;
+        } else if (swave == 0) {
             float ss = lane < Tile::CG ? o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w : 0.f;
             ss = warp_sum(ss);
             if (lane < Tile::CG) {
@@ -177,7 +190,7 @@ __global__ __launch_bounds__(PER_HEAD ? 256 : 256 * R) void mixer_kernel(MixerAr
     // the ring: the window's entry j (the input at launch time T - 3 + j) goes to entry (pos + T - 3 + j) % 4
     // when it is an input of this launch; older ones are already in place.  Per head, the group's q and k
     // channels are written by its first v-head's workgroup only.
-    const bool own_qk = !PER_HEAD || h % R == 0;
+    const bool own_qk = !PER_HEAD || (h % R == 0 && cs == 0);
 #pragma unroll
     for (int c = 0; c < CPT; ++c) {
         const int ch = tid + NTH * c;
@@ -187,19 +200,19 @@ __global__ __launch_bounds__(PER_HEAD ? 256 : 256 * R) void mixer_kernel(MixerAr
                 if (T - 3 + j >= 0) hist[ring_put(pos, T - 3 + j) * CHG + gch[c]] = hx[c][j];
     }
     // every thread read the old position before the step's barriers
-    if (tid < HW) posp[tid] = (pos + T) & 3;
+    if (NS == 1 && tid < HW) posp[tid] = (pos + T) & 3;
 }
 
-template <int DK, int DV, bool PER_HEAD>
+template <int DK, int DV, bool PER_HEAD, int NS = 1>
 hipError_t launch_mixer_r(const MixerArgs& a, hipStream_t stream) {
     const int R = a.nv / a.nk;
-    const dim3 grid(PER_HEAD ? a.nv : a.nk, a.B);
+    const dim3 grid(PER_HEAD ? a.nv * NS : a.nk, a.B);
     const dim3 block(PER_HEAD ? 256 : 256 * R);
     switch (R) {
-        case 1: hipLaunchKernelGGL((mixer_kernel<DK, DV, 1, PER_HEAD>), grid, block, 0, stream, a); break;
-        case 2: hipLaunchKernelGGL((mixer_kernel<DK, DV, 2, PER_HEAD>), grid, block, 0, stream, a); break;
-        case 3: hipLaunchKernelGGL((mixer_kernel<DK, DV, 3, PER_HEAD>), grid, block, 0, stream, a); break;
-        case 4: hipLaunchKernelGGL((mixer_kernel<DK, DV, 4, PER_HEAD>), grid, block, 0, stream, a); break;
+        case 1: hipLaunchKernelGGL((mixer_kernel<DK, DV, 1, PER_HEAD, NS>), grid, block, 0, stream, a); break;
+        case 2: hipLaunchKernelGGL((mixer_kernel<DK, DV, 2, PER_HEAD, NS>), grid, block, 0, stream, a); break;
+        case 3: hipLaunchKernelGGL((mixer_kernel<DK, DV, 3, PER_HEAD, NS>), grid, block, 0, stream, a); break;
+        case 4: hipLaunchKernelGGL((mixer_kernel<DK, DV, 4, PER_HEAD, NS>), grid, block, 0, stream, a); break;
         default: return hipErrorInvalidValue;
     }
     return hipGetLastError();
@@ -214,6 +227,10 @@ hipError_t launch_mixer_d(const MixerArgs& a, hipStream_t stream) {
 hipError_t launch_mixer(const MixerArgs& a, int dk, int dv, hipStream_t stream) {
     if (a.B <= 0 || a.T <= 0) return hipSuccess;
     if (a.nk <= 0 || a.nv % a.nk) return hipErrorInvalidValue;
+    if (a.ss_part) {
+        if (a.T != 1 || dk != 128 || dv != 128 || !a.o_tap) return hipErrorInvalidValue;
+        return launch_mixer_r<128, 128, true, kMixerSplit>(a, stream);
+    }
     if (dk == 128 && dv == 128) return launch_mixer_d<128, 128>(a, stream);
     if (dk == 64 && dv == 64) return launch_mixer_d<64, 64>(a, stream);
     if (dk == 32 && dv == 32) return launch_mixer_d<32, 32>(a, stream);
