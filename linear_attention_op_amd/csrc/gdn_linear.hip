@@ -580,7 +580,7 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x
 // fragments from LDS.  Workgroup 0 advances the ring position of every (sequence, v-head) by one token.
 template <int NW, int SPW, int OUT>
 __global__ __launch_bounds__(NW * 64) void out_proj_gnorm_kernel(GnormArgs a) {
-    static_assert(kMixerSplit == 4, "one float4 of partial sums per (row, head)");
+    static_assert(kMixerSplit == 4 || kMixerSplit == 8, "the partial sums of a (row, head) as one or two float4s");
     __shared__ __attribute__((aligned(16))) u16 xs[kGnormMaxM][kGnormMaxK + 8];
     __shared__ float red[gemv_red_floats<1, 1, NW>()];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -588,29 +588,49 @@ __global__ __launch_bounds__(NW * 64) void out_proj_gnorm_kernel(GnormArgs a) {
     const int M = a.M, K = a.K, KQ = K >> 5, NT = (a.N + 15) >> 4;
     const int n0 = blockIdx.x * 16, kq0 = wave * SPW;
 
+    // one pass of the norm: 8 columns of one head of row e / K per thread
+    struct Piece {
+        float4 o0, o1, z0, z1, w0, w1, s0, s1;
+    };
+    auto fetch = [&](int e) {
+        const int m = e / K, c = e - m * K, hh = c / a.dv;
+        const float* op = a.o + (size_t)m * K + c;
+        const float* zp = a.z + (size_t)m * a.ldz + c;
+        const float* np = a.norm_w + (c - hh * a.dv);
+        const float* sq = a.ss + ((size_t)m * a.nv + hh) * kMixerSplit;
+        Piece p;
+        p.o0 = *reinterpret_cast<const float4*>(op), p.o1 = *reinterpret_cast<const float4*>(op + 4);
+        p.z0 = *reinterpret_cast<const float4*>(zp), p.z1 = *reinterpret_cast<const float4*>(zp + 4);
+        p.w0 = *reinterpret_cast<const float4*>(np), p.w1 = *reinterpret_cast<const float4*>(np + 4);
+        p.s0 = *reinterpret_cast<const float4*>(sq);
+        p.s1 = kMixerSplit > 4 ? *reinterpret_cast<const float4*>(sq + 4) : float4{0.f, 0.f, 0.f, 0.f};
+        return p;
+    };
+    auto put = [&](int e, const Piece& p) {
+        const int m = e / K, c = e - m * K;
+        const float ssum = p.s0.x + p.s0.y + p.s0.z + p.s0.w + (kMixerSplit > 4 ? p.s1.x + p.s1.y + p.s1.z + p.s1.w : 0.f);
+        const float rstd = rsqrtf(ssum / (float)a.dv + a.eps);
+        const float ov[8] = {p.o0.x, p.o0.y, p.o0.z, p.o0.w, p.o1.x, p.o1.y, p.o1.z, p.o1.w};
+        const float zv[8] = {p.z0.x, p.z0.y, p.z0.z, p.z0.w, p.z1.x, p.z1.y, p.z1.z, p.z1.w};
+        const float nv8[8] = {p.w0.x, p.w0.y, p.w0.z, p.w0.w, p.w1.x, p.w1.y, p.w1.z, p.w1.w};
+        u16x8 yv;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) yv[j] = f2bf(ov[j] * rstd * nv8[j] * siluf_(zv[j]));
+        *reinterpret_cast<u16x8*>(&xs[m][c]) = yv;
+    };
+    // the first pass's inputs go out before the weights (vector loads complete in order), so the norm runs
+    // while the weights stream in; its index is clamped so that the loads need no branch
+    const int e0 = 8 * tid;
+    const Piece first = fetch(min(e0, M * K - 8) & ~7);
+    __builtin_amdgcn_sched_barrier(0);
+
     const u16* wp = a.w + ((size_t)min(n0 >> 4, NT - 1) * KQ + kq0) * 512 + lane * 8;
     bf16x8 wb[SPW];
 #pragma unroll
     for (int s = 0; s < SPW; ++s) wb[s] = ldw(wp + (size_t)s * 512);
 
-    for (int e = 8 * tid; e < M * K; e += 8 * NW * 64) {
-        const int m = e / K, c = e - m * K, hh = c / a.dv;
-        const float* op = a.o + (size_t)m * K + c;
-        const float* zp = a.z + (size_t)m * a.ldz + c;
-        const float* np = a.norm_w + (c - hh * a.dv);
-        const float4 o0 = *reinterpret_cast<const float4*>(op), o1 = *reinterpret_cast<const float4*>(op + 4);
-        const float4 z0 = *reinterpret_cast<const float4*>(zp), z1 = *reinterpret_cast<const float4*>(zp + 4);
-        const float4 w0 = *reinterpret_cast<const float4*>(np), w1 = *reinterpret_cast<const float4*>(np + 4);
-        const float4 sp = *reinterpret_cast<const float4*>(a.ss + ((size_t)m * a.nv + hh) * kMixerSplit);
-        const float rstd = rsqrtf((sp.x + sp.y + sp.z + sp.w) / (float)a.dv + a.eps);
-        const float ov[8] = {o0.x, o0.y, o0.z, o0.w, o1.x, o1.y, o1.z, o1.w};
-        const float zv[8] = {z0.x, z0.y, z0.z, z0.w, z1.x, z1.y, z1.z, z1.w};
-        const float nv8[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-        u16x8 yv;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) yv[j] = f2bf(ov[j] * rstd * nv8[j] * siluf_(zv[j]));
-        *reinterpret_cast<u16x8*>(&xs[m][c]) = yv;
-    }
+    if (e0 < M * K) put(e0, first);
+    for (int e = e0 + 8 * NW * 64; e < M * K; e += 8 * NW * 64) put(e, fetch(e));
     if (blockIdx.x == 0) {
         for (int t = tid; t < M * a.nv; t += NW * 64) {
             const int b = t / a.nv, hh = t - b * a.nv;
