@@ -1280,11 +1280,12 @@ struct DecodeArgs {
 // 8 waves per workgroup (two per SIMD) with a two-deep ring.  Measured on the 9B shape at M = 64 (with
 // the split a|b workgroups): bf16 23.6 us against 23.9 us for 4 waves and a four-deep ring (bf16 needs
 // <= 128 VGPRs so that the split workgroups can run beside the others), E4M3 18.8 us.  One row tile
-// (M <= 16) leaves room for a four-deep ring (93 VGPRs in bf16): graph steps of 37.0-37.1 against
-// 37.3-37.4 us at 9B batch 1, and 20.1-20.2 against 20.6 us at 0.8B batch 1.
+// (M <= 16) leaves room for a four-deep ring (93 VGPRs in bf16, 120 in E4M3 and MXFP4): graph steps of
+// 37.0-37.1 against 37.3-37.4 us at 9B batch 1, and 20.1-20.2 against 20.6 us at 0.8B batch 1.  MXINT8
+// keeps two (four would take 142 VGPRs: its 9B batch-1 step went from 32.6-32.8 to 34.5 us).
 template <int NTS, int MT, int WL, int XL>
 void in_proj_decode_launch(const DecodeArgs& a, hipStream_t stream) {
-    constexpr int NW = 8, PD = MT == 1 ? 4 : 2;
+    constexpr int NW = 8, PD = MT == 1 && WL != W_I8 ? 4 : 2;
     const dim3 grid(a.G + ((a.N2 + 15) >> 4) * a.KS), block(NW * 64);
     hipLaunchKernelGGL((in_proj_decode_kernel<NTS, MT, NW, PD, WL, XL>), grid, block, 0, stream, a.x, a.w, a.scale,
                        a.w2, a.M, a.N1, a.N2, a.K, a.G, a.KS, a.P, a.ldp, a.Pab);
