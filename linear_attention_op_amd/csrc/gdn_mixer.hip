@@ -434,6 +434,39 @@ __global__ __launch_bounds__(256) void gated_rmsnorm4_kernel(const float* __rest
     }
 }
 
+// The same for rows of exactly RND rounds of 1024 columns (Vd = 1024 RND): every round's o and z loads are
+// issued first, non-temporal (each value is read once), so that the whole row is in flight at once.
+template <int DV, int RND>
+__global__ __launch_bounds__(256) void gated_rmsnorm4r_kernel(const float* __restrict__ o, const float* __restrict__ z,
+                                                              int z_stride, const float* __restrict__ w, float eps,
+                                                              u16* __restrict__ y) {
+    constexpr int TPH = DV / 4, Vd = 1024 * RND;
+    const int m = blockIdx.x, t = threadIdx.x;
+    const float* orow = o + (size_t)m * Vd;
+    const float* zrow = z + (size_t)m * z_stride;
+    u16* yrow = y + (size_t)m * Vd;
+    f32x4 ov[RND], zv[RND];
+#pragma unroll
+    for (int i = 0; i < RND; ++i) {
+        ov[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(orow + 4 * t + 1024 * i));
+        zv[i] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(zrow + 4 * t + 1024 * i));
+    }
+    const float4 wv = *reinterpret_cast<const float4*>(w + (t % TPH) * 4);
+#pragma unroll
+    for (int i = 0; i < RND; ++i) {
+        float ss = ov[i][0] * ov[i][0] + ov[i][1] * ov[i][1] + ov[i][2] * ov[i][2] + ov[i][3] * ov[i][3];
+#pragma unroll
+        for (int off = 1; off < TPH; off <<= 1) ss += __shfl_xor(ss, off, 64);
+        const float rstd = rsqrtf(ss / (float)DV + eps);
+        const float y0 = ov[i][0] * rstd * wv.x * siluf_(zv[i][0]), y1 = ov[i][1] * rstd * wv.y * siluf_(zv[i][1]);
+        const float y2 = ov[i][2] * rstd * wv.z * siluf_(zv[i][2]), y3 = ov[i][3] * rstd * wv.w * siluf_(zv[i][3]);
+        uint2 pk;
+        pk.x = (uint32_t)__builtin_bit_cast(u16, (__bf16)y0) | ((uint32_t)__builtin_bit_cast(u16, (__bf16)y1) << 16);
+        pk.y = (uint32_t)__builtin_bit_cast(u16, (__bf16)y2) | ((uint32_t)__builtin_bit_cast(u16, (__bf16)y3) << 16);
+        *reinterpret_cast<uint2*>(yrow + 4 * t + 1024 * i) = pk;
+    }
+}
+
 hipError_t launch_gated_rmsnorm(const float* o, int M, int nv, int dv, const float* z, int z_stride,
                                 const float* w, float eps, u16* y, hipStream_t stream) {
     if (M <= 0) return hipSuccess;
@@ -441,7 +474,11 @@ hipError_t launch_gated_rmsnorm(const float* o, int M, int nv, int dv, const flo
                      ((uintptr_t)y & 7) == 0 && ((uintptr_t)w & 15) == 0 && (dv == 32 || dv == 64 || dv == 128);
     if (vec) {
         const int Vd = nv * dv;
-        if (dv == 128)
+        if (dv == 128 && Vd == 4096)
+            hipLaunchKernelGGL((gated_rmsnorm4r_kernel<128, 4>), dim3(M), dim3(256), 0, stream, o, z, z_stride, w, eps, y);
+        else if (dv == 128 && Vd == 2048)
+            hipLaunchKernelGGL((gated_rmsnorm4r_kernel<128, 2>), dim3(M), dim3(256), 0, stream, o, z, z_stride, w, eps, y);
+        else if (dv == 128)
             hipLaunchKernelGGL(gated_rmsnorm4_kernel<128>, dim3(M), dim3(256), 0, stream, o, Vd, z, z_stride, w, eps, y);
         else if (dv == 64)
             hipLaunchKernelGGL(gated_rmsnorm4_kernel<64>, dim3(M), dim3(256), 0, stream, o, Vd, z, z_stride, w, eps, y);
