@@ -237,10 +237,13 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, void* 
     const bool y_frag = frag && ng == 1 && grp[0].T <= kFusedMaxT;
     // single-token launches of at most 64 (sequence, v-head) pairs would leave most CUs idle with one
     // workgroup per head: each head's state is split over kMixerSplit workgroups, and the gated RMSNorm
-    // moves into the out_proj (bf16 weights, 128-wide heads)
+    // moves into the out_proj (128-wide heads; bf16 weights need the value width at 2048 or 4096).  Not
+    // with MXINT8 weights: with its norm ahead of its heavier GEMV the 9B batch-1 step took 33.9 against
+    // 32.5 us.
     const bool split_heads = y_frag && grp[0].T == 1 && M * nv <= 64 && M <= gdn::kGnormMaxM &&
-                             d.head_k_dim == 128 && d.head_v_dim == 128 && L->wfmt == GDN_WEIGHTS_BF16 &&
-                             (Vd == 4096 || Vd == 2048) && L->NP % 4 == 0;
+                             d.head_k_dim == 128 && d.head_v_dim == 128 && Vd <= gdn::kGnormMaxK &&
+                             L->wfmt != GDN_WEIGHTS_MXINT8 &&
+                             (L->wfmt != GDN_WEIGHTS_BF16 || Vd == 4096 || Vd == 2048) && L->NP % 4 == 0;
     // decode: q | k | v | z over workgroups balanced on the CUs, a | b as partial sums for the mixer
     const bool split_ab = frag && gdn::in_proj_decode_supported(L->CD + Vd, L->d.hidden);
     bool ab_split = false;
@@ -305,12 +308,13 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, void* 
     }
     if (ev[2]) HIP_OK(hipEventRecord(ev[2], st));
     if (split_heads) {
+        const QW q = w_out_q(L);
         gdn::GnormArgs ga{};
         ga.o = L->o, ga.ss = L->ss, ga.z = L->P + L->CD, ga.ldz = L->NP, ga.norm_w = L->norm_w;
         ga.eps = d.rms_norm_eps, ga.nv = nv, ga.dv = d.head_v_dim;
-        ga.w = L->w_out, ga.M = M, ga.N = d.hidden, ga.K = Vd, ga.y = out, ga.ldy = d.hidden;
+        ga.w = q.w, ga.scale = q.scale, ga.M = M, ga.N = d.hidden, ga.K = Vd, ga.y = out, ga.ldy = d.hidden;
         ga.conv_pos = L->conv_pos, ga.slot_ids = grp[0].slots, ga.max_slots = L->max_slots;
-        HIP_OK(gdn::launch_out_proj_gnorm(ga, out_kind, st));
+        HIP_OK(gdn::launch_out_proj_gnorm(ga, q.layout, out_kind, st));
     } else {
         HIP_OK(out_proj_rows(L, L->y, y_frag ? gdn::W_FRAG : gdn::W_ROW, M, out, out_kind, st));
     }

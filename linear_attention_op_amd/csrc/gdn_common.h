@@ -306,8 +306,8 @@ hipError_t launch_mixer(const MixerArgs& a, int dk, int dv, hipStream_t stream);
 constexpr int kMixerSplit = 4;  // workgroups per v-head of a split-head launch
 
 // The out_proj of a split-head mixer launch (MixerArgs::ss_part): the gated RMSNorm of its rows, then the
-// projection against bf16 W_FRAG weights; it also advances the ring positions of the launch's sequences
-// by the one token, which the split mixer leaves to it.
+// projection (bf16, E4M3, MXFP4 or MXINT8 weights); it also advances the ring positions of the launch's
+// sequences by the one token, which the split mixer leaves to it.
 struct GnormArgs {
     const float* o;        // [M, K] recurrence output (K = nv dv)
     const float* ss;       // [M, nv, kMixerSplit] partial sums of squares of o per head and column slice
@@ -316,7 +316,8 @@ struct GnormArgs {
     const float* norm_w;   // [dv]
     float eps;
     int nv, dv;
-    const u16* w;          // [N, K] bf16, W_FRAG
+    const void* w;         // [N, K]: bf16 W_FRAG, or E4M3 / MXFP4 / MXINT8 fragments (the layout argument)
+    const float* scale;    // the weights' scales (W_F8 per row; W_F4, W_I8 the E8M0 codes); nullptr for bf16
     int M, N, K;
     void* y;               // [M, N] row-major, bf16 or fp32 by the out kind
     int ldy;
@@ -325,7 +326,7 @@ struct GnormArgs {
     int max_slots;
 };
 constexpr int kGnormMaxM = 4, kGnormMaxK = 4096;
-hipError_t launch_out_proj_gnorm(const GnormArgs& a, int out_kind, hipStream_t stream);
+hipError_t launch_out_proj_gnorm(const GnormArgs& a, int wlayout, int out_kind, hipStream_t stream);
 
 struct FrontArgs {
     const float* P;

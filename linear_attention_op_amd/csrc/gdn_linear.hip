@@ -572,21 +572,27 @@ __global__ __launch_bounds__(NW * 64) void gemv_kernel(const u16* __restrict__ x
                                                  K >> 5, red);
 }
 
-// Decode out_proj of a split-head mixer launch (GnormArgs).  Each wave first issues every weight fragment
-// of its k-share (SPW k-steps, as gemv_block_allw).  While they are in flight the workgroup forms the gated
-// RMSNorm of the M <= 4 rows, y = o rsqrt(sum_head(o^2) / dv + eps) w silu(z) in bf16, into LDS: 8 columns
-// of one head per thread and pass, the head's sum of squares from the mixer's per-slice partials (HF
-// Qwen3_5RMSNormGated, HF:167-184, as the fused mixer computes it).  The GEMV then reads its activation
-// fragments from LDS.  Workgroup 0 advances the ring position of every (sequence, v-head) by one token.
-template <int NW, int SPW, int OUT>
+// Decode out_proj of a split-head mixer launch (GnormArgs).  The workgroup forms the gated RMSNorm of the
+// M <= 4 rows, y = o rsqrt(sum_head(o^2) / dv + eps) w silu(z) in bf16, into LDS: 8 columns of one head per
+// thread and pass, the head's sum of squares from the mixer's per-slice partials (HF Qwen3_5RMSNormGated,
+// HF:167-184, as the fused mixer computes it).  The GEMV then reads its activations from LDS.  bf16
+// weights (WL = W_FRAG): each wave issues its first pass of norm inputs, then every weight fragment of its
+// k-share (SPW k-steps, as gemv_block_allw), so that the norm runs while the weights arrive (vector loads
+// complete in order).  E4M3 / MXFP4 / MXINT8 weights: the norm first, then the format's GEMV block on the
+// LDS rows as row-major activations.  Workgroup 0 advances the ring position of every (sequence, v-head) by
+// one token.
+template <int NW, int SPW, int OUT, int WL>
 __global__ __launch_bounds__(NW * 64) void out_proj_gnorm_kernel(GnormArgs a) {
     static_assert(kMixerSplit == 4 || kMixerSplit == 8, "the partial sums of a (row, head) as one or two float4s");
-    __shared__ __attribute__((aligned(16))) u16 xs[kGnormMaxM][kGnormMaxK + 8];
+    constexpr int PD8 = 2;  // the E4M3 / MXINT8 blocks' ring (k-pairs), as gemv() runs them
+    __shared__ __attribute__((aligned(16))) u16 xs[kGnormMaxM * (kGnormMaxK + 8)];
     __shared__ float red[gemv_red_floats<1, 1, NW>()];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int M = a.M, K = a.K, KQ = K >> 5, NT = (a.N + 15) >> 4;
     const int n0 = blockIdx.x * 16, kq0 = wave * SPW;
+    // LDS row stride: padded for the bf16 path's fragment reads, K for the row-major reads of the others
+    const int ldx = WL == W_FRAG ? kGnormMaxK + 8 : K;
 
     // one pass of the norm: 8 columns of one head of row e / K per thread
     struct Piece {
@@ -616,22 +622,10 @@ __global__ __launch_bounds__(NW * 64) void out_proj_gnorm_kernel(GnormArgs a) {
         u16x8 yv;
 #pragma unroll
         for (int j = 0; j < 8; ++j) yv[j] = f2bf(ov[j] * rstd * nv8[j] * siluf_(zv[j]));
-        *reinterpret_cast<u16x8*>(&xs[m][c]) = yv;
+        *reinterpret_cast<u16x8*>(&xs[m * ldx + c]) = yv;
     };
-    // the first pass's inputs go out before the weights (vector loads complete in order), so the norm runs
-    // while the weights stream in; its index is clamped so that the loads need no branch
-    const int e0 = 8 * tid;
-    const Piece first = fetch(min(e0, M * K - 8) & ~7);
-    __builtin_amdgcn_sched_barrier(0);
-
-    const u16* wp = a.w + ((size_t)min(n0 >> 4, NT - 1) * KQ + kq0) * 512 + lane * 8;
-    bf16x8 wb[SPW];
-#pragma unroll
-    for (int s = 0; s < SPW; ++s) wb[s] = ldw(wp + (size_t)s * 512);
-
-    if (e0 < M * K) put(e0, first);
-    for (int e = e0 + 8 * NW * 64; e < M * K; e += 8 * NW * 64) put(e, fetch(e));
-    if (blockIdx.x == 0) {
+    auto advance_ring = [&]() {
+        if (blockIdx.x != 0) return;
         for (int t = tid; t < M * a.nv; t += NW * 64) {
             const int b = t / a.nv, hh = t - b * a.nv;
             const int slot = a.slot_ids ? a.slot_ids[b] : b;
@@ -640,17 +634,45 @@ __global__ __launch_bounds__(NW * 64) void out_proj_gnorm_kernel(GnormArgs a) {
                 *p = (*p + 1) & 3;
             }
         }
-    }
-    __syncthreads();
+    };
 
-    f32x4 acc[1][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
-    const bf16x8 zero8 = {};
+    if constexpr (WL == W_FRAG) {
+        // the first pass's inputs go out before the weights; its index is clamped so that the loads need no
+        // branch
+        const int e0 = 8 * tid;
+        const Piece first = fetch(min(e0, M * K - 8) & ~7);
+        __builtin_amdgcn_sched_barrier(0);
+
+        const u16* wp = (const u16*)a.w + ((size_t)min(n0 >> 4, NT - 1) * KQ + kq0) * 512 + lane * 8;
+        bf16x8 wb[SPW];
 #pragma unroll
-    for (int s = 0; s < SPW; ++s) {
-        const bf16x8 xb = r < M ? *reinterpret_cast<const bf16x8*>(&xs[r][32 * (kq0 + s) + 8 * g]) : zero8;
-        acc[0][0] = mfma16(wb[s], xb, acc[0][0]);
+        for (int s = 0; s < SPW; ++s) wb[s] = ldw(wp + (size_t)s * 512);
+
+        if (e0 < M * K) put(e0, first);
+        for (int e = e0 + 8 * NW * 64; e < M * K; e += 8 * NW * 64) put(e, fetch(e));
+        advance_ring();
+        __syncthreads();
+
+        f32x4 acc[1][1] = {{f32x4{0.f, 0.f, 0.f, 0.f}}};
+        const bf16x8 zero8 = {};
+#pragma unroll
+        for (int s = 0; s < SPW; ++s) {
+            const bf16x8 xb = r < M ? *reinterpret_cast<const bf16x8*>(&xs[r * ldx + 32 * (kq0 + s) + 8 * g]) : zero8;
+            acc[0][0] = mfma16(wb[s], xb, acc[0][0]);
+        }
+        gemv_finish<1, 1, NW, OUT>(acc, red, M, a.N, a.y, a.ldy, n0, nullptr);
+    } else {
+        for (int e = 8 * tid; e < M * K; e += 8 * NW * 64) put(e, fetch(e));
+        advance_ring();
+        __syncthreads();
+        const u16* x = xs;  // the rows in LDS, row-major with stride K
+        if constexpr (WL == W_F4)
+            gemv_block_f4<1, 1, NW, OUT, W_ROW>(x, (const u8*)a.w, reinterpret_cast<const uint32_t*>(a.scale), M, a.N,
+                                                K, a.y, a.ldy, n0, 0, K >> 7, red);
+        else
+            gemv_block_f8<1, 1, NW, PD8, OUT, W_ROW, WL>(x, (const u8*)a.w, a.scale, M, a.N, K, a.y, a.ldy, n0, 0,
+                                                        K >> 6, red);
     }
-    gemv_finish<1, 1, NW, OUT>(acc, red, M, a.N, a.y, a.ldy, n0, nullptr);
 }
 
 // Decode in_proj (fragment-layout weights and activations, fp32 out), balanced over the CUs: workgroups
@@ -1237,22 +1259,43 @@ hipError_t launch_quantize_mxint8(const void* w, int N, int K, u8* q, u8* scale,
     return hipGetLastError();
 }
 
-hipError_t launch_out_proj_gnorm(const GnormArgs& a, int out_kind, hipStream_t stream) {
+template <int SPW, int WL>
+void out_proj_gnorm_launch(const GnormArgs& a, int out_kind, hipStream_t stream) {
+    constexpr int NW = 8;
+    const dim3 grid(a.N / 16), block(NW * 64);
+    if (out_kind == OUT_F32) hipLaunchKernelGGL((out_proj_gnorm_kernel<NW, SPW, OUT_F32, WL>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((out_proj_gnorm_kernel<NW, SPW, OUT_BF16, WL>), grid, block, 0, stream, a);
+}
+
+hipError_t launch_out_proj_gnorm(const GnormArgs& a, int wlayout, int out_kind, hipStream_t stream) {
     if (a.M <= 0) return hipSuccess;
     constexpr int NW = 8;
     const bool ok = a.M <= kGnormMaxM && a.K <= kGnormMaxK && a.N % 16 == 0 && a.dv % 8 == 0 && a.K % a.dv == 0 &&
                     a.K == a.nv * a.dv && a.ldz % 4 == 0 && ((uintptr_t)a.o & 15) == 0 && ((uintptr_t)a.z & 15) == 0 &&
                     ((uintptr_t)a.norm_w & 15) == 0 && ((uintptr_t)a.ss & 15) == 0 && a.conv_pos &&
                     (out_kind == OUT_F32 || out_kind == OUT_BF16);
+    if (!ok) return hipErrorInvalidValue;
     const int KQ = a.K >> 5;
-    if (!ok || (KQ != NW * 16 && KQ != NW * 8)) return hipErrorInvalidValue;
-    const dim3 grid(a.N / 16), block(NW * 64);
-    if (KQ == NW * 16) {
-        if (out_kind == OUT_F32) hipLaunchKernelGGL((out_proj_gnorm_kernel<NW, 16, OUT_F32>), grid, block, 0, stream, a);
-        else hipLaunchKernelGGL((out_proj_gnorm_kernel<NW, 16, OUT_BF16>), grid, block, 0, stream, a);
-    } else {
-        if (out_kind == OUT_F32) hipLaunchKernelGGL((out_proj_gnorm_kernel<NW, 8, OUT_F32>), grid, block, 0, stream, a);
-        else hipLaunchKernelGGL((out_proj_gnorm_kernel<NW, 8, OUT_BF16>), grid, block, 0, stream, a);
+    switch (wlayout) {
+        case W_FRAG:
+            if (KQ == NW * 16) out_proj_gnorm_launch<16, W_FRAG>(a, out_kind, stream);
+            else if (KQ == NW * 8) out_proj_gnorm_launch<8, W_FRAG>(a, out_kind, stream);
+            else return hipErrorInvalidValue;
+            break;
+        case W_F8:
+            if (a.K % 64 || !a.scale) return hipErrorInvalidValue;
+            out_proj_gnorm_launch<1, W_F8>(a, out_kind, stream);
+            break;
+        case W_I8:
+            if (a.K % 128 || !a.scale) return hipErrorInvalidValue;
+            out_proj_gnorm_launch<1, W_I8>(a, out_kind, stream);
+            break;
+        case W_F4:
+            if (a.K % 128 || !a.scale) return hipErrorInvalidValue;
+            out_proj_gnorm_launch<1, W_F4>(a, out_kind, stream);
+            break;
+        default:
+            return hipErrorInvalidValue;
     }
     return hipGetLastError();
 }

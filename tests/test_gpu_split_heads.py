@@ -47,3 +47,29 @@ def test_split_head_decode_matches_per_head(shape, Bs, Bu, out_dtype):
         assert rel(a, b[:Bs]) < 1e-3, f"step {t}"
         assert rel(split.get_recurrent_state(), whole.get_recurrent_state()[:Bs]) < 1e-5, f"step {t}"
         assert torch.equal(split.get_conv_state().cpu(), whole.get_conv_state()[:Bs].cpu()), f"step {t}"
+
+
+@pytest.mark.parametrize("weight_dtype", ["fp8", "mxfp4", "mxint8"])
+def test_split_head_decode_low_precision_weights(weight_dtype):
+    """The same comparison with E4M3 and MXFP4 weights (the out_proj's own GEMV block on the normalised rows
+    in LDS), 9B at batch 1 against batch 3; MXINT8 keeps one workgroup per head at both batches."""
+    d = syn.SHAPES["9b"]
+    w, gen = syn.make_weights(d, seed=6)
+    Bs, Bu, steps = 1, 3, 4
+    x, s0 = syn.make_inputs(d, Bu, steps, gen, state_std=0.05)
+    xp, _ = syn.make_inputs(d, Bu, 5, gen)
+    split = Qwen35GatedDeltaNetHIP(w, dims=d, batch=Bs, max_tokens=64, weight_dtype=weight_dtype,
+                                   out_dtype=torch.float32)
+    whole = Qwen35GatedDeltaNetHIP(w, dims=d, batch=Bu, max_tokens=64, weight_dtype=weight_dtype,
+                                   out_dtype=torch.float32)
+    split.set_state(rec=s0[:Bs].cuda())
+    whole.set_state(rec=s0.cuda())
+    split(xp[:Bs])
+    whole(xp)
+    for t in range(steps):
+        a = split(x[:Bs, t:t + 1])
+        b = whole(x[:, t:t + 1])
+        torch.cuda.synchronize()
+        assert rel(a, b[:Bs]) < 1e-3, f"step {t}"
+        assert rel(split.get_recurrent_state(), whole.get_recurrent_state()[:Bs]) < 1e-5, f"step {t}"
+        assert torch.equal(split.get_conv_state().cpu(), whole.get_conv_state()[:Bs].cpu()), f"step {t}"
