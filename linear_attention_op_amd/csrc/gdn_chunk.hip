@@ -109,7 +109,8 @@ __global__ __launch_bounds__(512, 4) void chunk_prep_kernel(DeltaArgs a, ChunkWs
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int mi = wave & 3, hf = wave >> 2;
-    // heads fastest: the v-heads that share a k-head run back to back and share its rows in L2
+    // heads fastest: the v-heads that share a k-head run back to back (on neighbouring XCDs), so the second
+    // finds the k-head's rows in the memory-side cache
     const int h = blockIdx.x, c = blockIdx.y, b = blockIdx.z;
     const int T = a.T, Hk = a.Hk, Hv = a.Hv, kh = h / (Hv / Hk);
     const int t0 = c * CK, len = min(CK, T - t0);
