@@ -662,7 +662,20 @@ __global__ __launch_bounds__(NW * 64) void out_proj_gnorm_kernel(GnormArgs a) {
         }
         gemv_finish<1, 1, NW, OUT>(acc, red, M, a.N, a.y, a.ldy, n0, nullptr);
     } else {
-        for (int e = 8 * tid; e < M * K; e += 8 * NW * 64) put(e, fetch(e));
+        // The norm's first inputs, then one 4-byte load per 128-byte line of this wave's share of the weights
+        // (as the format's block splits them: a contiguous run of 1 KB blocks of tile n0 / 16), so that those
+        // lines are on their way into L2 while the norm runs; the block's own loads, issued after it, find
+        // them there.  The touched words feed an empty asm at the end, which keeps the loads.
+        const int e0 = 8 * tid;
+        const Piece first = fetch(min(e0, M * K - 8) & ~7);
+        __builtin_amdgcn_sched_barrier(0);
+        const int nb = WL == W_F4 ? K >> 7 : K >> 6, per = (nb + NW - 1) / NW;
+        const int b0 = min(nb, wave * per), nblk = max(1, min(nb, (wave + 1) * per) - b0);
+        const u8* wt = (const u8*)a.w + ((size_t)min(n0 >> 4, NT - 1) * nb + min(b0, nb - 1)) * 1024;
+        const uint32_t touched = *reinterpret_cast<const uint32_t*>(wt + (size_t)min(lane, 8 * nblk - 1) * 128);
+        __builtin_amdgcn_sched_barrier(0);
+        if (e0 < M * K) put(e0, first);
+        for (int e = e0 + 8 * NW * 64; e < M * K; e += 8 * NW * 64) put(e, fetch(e));
         advance_ring();
         __syncthreads();
         const u16* x = xs;  // the rows in LDS, row-major with stride K
@@ -672,6 +685,7 @@ __global__ __launch_bounds__(NW * 64) void out_proj_gnorm_kernel(GnormArgs a) {
         else
             gemv_block_f8<1, 1, NW, PD8, OUT, W_ROW, WL>(x, (const u8*)a.w, a.scale, M, a.N, K, a.y, a.ldy, n0, 0,
                                                         K >> 6, red);
+        asm volatile("" ::"v"(touched));
     }
 }
 
