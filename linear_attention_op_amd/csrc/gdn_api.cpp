@@ -238,8 +238,8 @@ int run_rows(gdn_layer* L, const u16* x, int M, const Group* grp, int ng, void* 
     // single-token launches of at most 64 (sequence, v-head) pairs would leave most CUs idle with one
     // workgroup per head: each head's state is split over kMixerSplit workgroups, and the gated RMSNorm
     // moves into the out_proj (128-wide heads; bf16 weights need the value width at 2048 or 4096).  Not
-    // with MXINT8 weights: with its norm ahead of its heavier GEMV the 9B batch-1 step took 33.9 against
-    // 32.5 us.
+    // with MXINT8 weights, whose heavier GEMV gains nothing from it: the 9B batch-1 step took 32.6 against
+    // 32.5 us split (33.9 before the out_proj touched its weight lines ahead of the norm).
     const bool split_heads = y_frag && grp[0].T == 1 && M * nv <= 64 && M <= gdn::kGnormMaxM &&
                              d.head_k_dim == 128 && d.head_v_dim == 128 && Vd <= gdn::kGnormMaxK &&
                              L->wfmt != GDN_WEIGHTS_MXINT8 &&
