@@ -1339,7 +1339,8 @@ struct DecodeArgs {
 // <= 128 VGPRs so that the split workgroups can run beside the others), E4M3 18.8 us.  One row tile
 // (M <= 16) leaves room for a four-deep ring (93 VGPRs in bf16, 120 in E4M3 and MXFP4): graph steps of
 // 37.0-37.1 against 37.3-37.4 us at 9B batch 1, and 20.1-20.2 against 20.6 us at 0.8B batch 1.  MXINT8
-// keeps two (four would take 142 VGPRs: its 9B batch-1 step went from 32.6-32.8 to 34.5 us).
+// keeps two (four would take 142 VGPRs: its 9B batch-1 step went from 32.6-32.8 to 34.5 us).  Six deep in
+// bf16 (125 VGPRs) measured mixed: 9B batch 1 35.4-35.5 against 35.6-35.7 us, batch 8 40.4-40.5 against 40.3.
 template <int NTS, int MT, int WL, int XL>
 void in_proj_decode_launch(const DecodeArgs& a, hipStream_t stream) {
     constexpr int NW = 8, PD = MT == 1 && WL != W_I8 ? 4 : 2;
